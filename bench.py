@@ -1,0 +1,343 @@
+#!/usr/bin/env python3
+"""Benchmark of the QloraLinear hot path on one MI355X.
+
+Metric: "QloraLinear fwd+bwd TFLOP/s (prefill) & weight GB/s
+(decode), % of roofline".  The headline line is configuration 2 (decode):
+one step is the fused dequant-GEMV forward of the two Llama-7B MLP shapes
+(NF4 11008x4096 then 4096x11008, LoRA r=16 alpha=32) at batch 1; ``value``
+is packed-weight bytes per second.  The same line carries decode at batch 4
+and 16 and configuration 3 (prefill: fused forward+backward of a 4096x4096
+NF4 layer at 4096 tokens, r=64 alpha=16, fp32 and bf16 activations) in
+TFLOP/s.
+
+Inputs are synthetic (torch's seeded generator on the GPU: W ~ 0.02 N(0,1)
+quantized on the GPU, A ~ U(+-1/sqrt(K)), B ~ 0.01 N(0,1), X, dY ~ N(0,1))
+and resident in HBM before timing.  Decode steps rotate over enough weight
+copies (>= 512 MB) that every step reads HBM rather than the 256 MB
+Infinity Cache, and run as a replayed HIP graph so that host launch cost is
+not measured.  ``cpu_baseline`` times the oracle (the C restatement of
+qlora-core's single-threaded CPU path) on a bounded sample on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vkqlora.rs_amd"))
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+METRIC = ("QloraLinear fwd+bwd TFLOP/s (prefill) & weight GB/s (decode), "
+          "% of roofline")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200,
+                    help="timed decode steps (prefill uses steps/20, >= 5)")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU-baseline budget per workload")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+def decode_bench(args, ctx, torch, dev, QD):
+    """Config 2: decode-shaped fused dequant-GEMV forward."""
+    r, alpha = 16, 32.0
+    shapes = [(11008, 4096), (4096, 11008)]  # (out_dim N, in_dim K)
+    g = torch.Generator(device="cuda").manual_seed(0x1234)
+    layers = []
+    for N, K in shapes:
+        w = torch.randn(N, K, device=dev, generator=g) * 0.02
+        base = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+        del w
+        bound = 1.0 / math.sqrt(K)
+        a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) * bound
+        b = torch.randn(N, r, device=dev, generator=g) * 0.01
+        layers.append(dict(N=N, K=K, base=base, a=a, b=b,
+                           lora=QD.lora_struct(a, b, r, alpha)))
+    wbytes = sum(L["base"].nbytes for L in layers)
+    copies = max(2, math.ceil(512e6 / wbytes))
+    for L in layers:
+        L["copies"] = [L["base"]] + [L["base"].clone() for _ in range(copies - 1)]
+        L["structs"] = [c.struct() for c in L["copies"]]
+    torch.cuda.synchronize()
+
+    results = {}
+    for batch in (1, 4, 16):
+        xs = [torch.randn(batch, L["K"], device=dev, generator=g) for L in layers]
+        ys = [torch.empty(batch, L["N"], device=dev) for L in layers]
+
+        def step(i, with_lora=True):
+            for li, L in enumerate(layers):
+                c = (i * len(layers) + li) % copies
+                QD.forward(None, L["lora"] if with_lora else None, xs[li], batch,
+                           ys[li], ctx=ctx, qw=L["structs"][c])
+
+        # eager reference result, then warm the scratch before capture
+        step(0)
+        torch.cuda.synchronize()
+        ref = [y.clone() for y in ys]
+        n_graph = copies  # one graph covers every copy once
+        graphs = {}
+        for lora_on in (True, False):
+            gr = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                step(0, lora_on)  # warm-up on the capture stream
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gr):
+                for i in range(n_graph):
+                    step(i, lora_on)
+            graphs[lora_on] = gr
+        # the graph must reproduce the eager result on every replay
+        for _ in range(2):
+            graphs[True].replay()
+            torch.cuda.synchronize()
+            for y, rr in zip(ys, ref):
+                assert torch.equal(y, rr), "graph replay differs from eager run"
+
+        reps = max(1, -(-args.steps // n_graph))
+        wreps = max(1, -(-args.warmup // n_graph))
+        out = {}
+        for lora_on in (True, False):
+            for _ in range(wreps):
+                graphs[lora_on].replay()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record()
+            for _ in range(reps):
+                graphs[lora_on].replay()
+            e1.record()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            ms = e0.elapsed_time(e1)
+            out[lora_on] = (ms / (reps * n_graph), wall / (reps * n_graph) * 1e3)
+        ms_step, wall_step = out[True]
+        ms_gemv_pair = out[False][0]  # the two GEMV launches alone
+        gemv_bytes = sum(L["base"].nbytes + 4 * batch * (L["K"] + L["N"])
+                         for L in layers)
+        full_bytes = gemv_bytes + sum(4 * (L["a"].numel() + L["b"].numel())
+                                      for L in layers)
+        flops = sum(2 * batch * L["N"] * L["K"] + 2 * batch * r * (L["N"] + L["K"])
+                    for L in layers)
+        results[batch] = dict(
+            ms_per_step=ms_step, wall_ms_per_step=wall_step,
+            weight_gbs=wbytes / (ms_step * 1e6),
+            total_gbs=full_bytes / (ms_step * 1e6),
+            tflops=flops / (ms_step * 1e9),
+            gemv_ms_per_launch=ms_gemv_pair / 2,
+            gemv_achieved_gbs=gemv_bytes / (ms_gemv_pair * 1e6),
+            gemv_bytes_per_launch=gemv_bytes / 2,
+            steps=reps * n_graph)
+    return results, dict(copies=copies, packed_weight_bytes=wbytes, r=r,
+                         alpha=alpha)
+
+
+# ---------------------------------------------------------------------------
+def prefill_bench(args, ctx, torch, dev, QD, act_dtype):
+    """Config 3: fused forward + backward, 4096x4096 NF4, 4096 tokens."""
+    N = K = 4096
+    M, r, alpha = 4096, 64, 16.0
+    g = torch.Generator(device="cuda").manual_seed(0x5678)
+    w = torch.randn(N, K, device=dev, generator=g) * 0.02
+    W = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+    del w
+    bound = 1.0 / math.sqrt(K)
+    a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) * bound
+    b = torch.randn(N, r, device=dev, generator=g) * 0.01
+    lora = QD.lora_struct(a, b, r, alpha)
+    x = torch.randn(M, K, device=dev, generator=g).to(act_dtype)
+    dy = torch.randn(M, N, device=dev, generator=g).to(act_dtype)
+    y = torch.empty(M, N, device=dev)
+    t1 = torch.empty(M, r, device=dev)
+    gx = torch.empty(M, K, device=dev)
+    ga = torch.empty(r, K, device=dev)
+    gb = torch.empty(N, r, device=dev)
+    qw = W.struct()
+
+    def step():
+        QD.forward(None, lora, x, M, y, t1=t1, ctx=ctx, qw=qw)
+        QD.backward(None, lora, x, dy, M, gx, ga, gb, t1=t1, ctx=ctx, qw=qw)
+
+    steps = max(5, args.steps // 20)
+    for _ in range(max(2, args.warmup // 10)):
+        step()
+    torch.cuda.synchronize()
+    ctx.set_timing(True)
+    ctx.timing_report(reset=True)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    rep = ctx.timing_report(reset=True)
+    ctx.set_timing(False)
+    flops = 4 * M * N * K + 6 * M * r * (K + N)
+    kern = {k: dict(launches=v[0], avg_ms=v[1] / max(v[0], 1)) for k, v in rep.items()}
+    fwd_flops = 2 * M * N * K + 2 * M * r * N
+    fk = kern.get("forward_gemm")
+    peak = FP32_MFMA_PEAK_TFLOPS
+    roof = None
+    if fk:
+        ach = fwd_flops / (fk["avg_ms"] * 1e9)
+        roof = dict(bound="mfma", kernel="forward_gemm (k_gemm NF4 fwd)",
+                    achieved=ach, peak=peak, unit="TFLOP/s", frac=ach / peak,
+                    flops_per_launch=fwd_flops, traffic=None)
+    return dict(ms_per_step=ms, tflops=flops / (ms * 1e9),
+                frac_fp32_peak=flops / (ms * 1e9) / peak, flops_per_step=flops,
+                steps=steps, kernels=kern, roofline=roof,
+                act_dtype=str(act_dtype).replace("torch.", ""))
+
+
+# ---------------------------------------------------------------------------
+def cpu_baseline_decode(seconds):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    r, alpha = 16, 32.0
+    rng = O.Rng(0x1234_5678_9ABC_DEF0 ^ 2)
+    layers = []
+    for N, K in ((11008, 4096), (4096, 11008)):
+        w = rng.normal(N * K, 0.02)
+        q = O.quantize(w)
+        bound = 1.0 / math.sqrt(K)
+        layers.append((N, K, q, rng.uniform(r * K, -bound, bound),
+                       rng.normal(N * r, 0.01), rng.normal(K)))
+    wbytes = sum(O.storage_bytes(L[2]) for L in layers)
+    t0, steps = time.perf_counter(), 0
+    while True:
+        for N, K, q, a, b, x in layers:
+            wd = O.dequantize(q)  # qlora.rs:97 dequantizes on every forward
+            O.qlora_forward(wd, N, K, a, b, r, alpha, x, 1)
+        steps += 1
+        if time.perf_counter() - t0 > seconds or steps >= 50:
+            break
+    dt = (time.perf_counter() - t0) / steps
+    return dict(value=wbytes / (dt * 1e9), unit="GB/s", cores=1, kind="port",
+                sample=(f"{steps} full decode steps (both layers, batch 1, "
+                        f"dequantize + forward, single thread), {dt * 1e3:.1f} ms/step"),
+                nproc=os.cpu_count())
+
+
+def cpu_baseline_prefill(seconds):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    N = K = 4096
+    r, alpha, M = 64, 16.0, 4096
+    rows = 16
+    rng = O.Rng(0x1234_5678_9ABC_DEF0 ^ 3)
+    w = rng.normal(N * K, 0.02)
+    q = O.quantize(w)
+    a = rng.uniform(r * K, -1 / 64, 1 / 64)
+    b = rng.normal(N * r, 0.01)
+    x = rng.normal(rows * K)
+    dy = rng.normal(rows * N)
+    t0, steps = time.perf_counter(), 0
+    while True:
+        wd = O.dequantize(q)
+        O.qlora_forward(wd, N, K, a, b, r, alpha, x, rows)
+        O.qlora_backward(wd, N, K, a, b, r, alpha, x, dy, rows)
+        steps += 1
+        if time.perf_counter() - t0 > seconds or steps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / steps
+    flops = 4 * rows * N * K + 6 * rows * r * (K + N)
+    return dict(value=flops / (dt * 1e12), unit="TFLOP/s", cores=1, kind="port",
+                sample=(f"fwd+bwd on a {rows}-row slice of the {M}-token batch "
+                        f"({steps} reps, {dt:.2f} s each incl. 2 dequantizations); "
+                        f"every term is linear in tokens, full step = {M // rows}x"),
+                nproc=os.cpu_count())
+
+
+# ---------------------------------------------------------------------------
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the hot path shards by tokens, see DESIGN.md); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import qlora_hip
+    from qlora_hip import device as QD
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    ctx = qlora_hip.default_context()
+    print(f"# device: {ctx.device_name()}", file=sys.stderr, flush=True)
+
+    dec, dec_cfg = decode_bench(args, ctx, torch, dev, QD)
+    print(f"# decode done: {json.dumps({b: round(v['weight_gbs'], 1) for b, v in dec.items()})}",
+          file=sys.stderr, flush=True)
+    prefill = {}
+    if not args.skip_prefill:
+        for dt_ in (torch.float32, torch.bfloat16):
+            p = prefill_bench(args, ctx, torch, dev, QD, dt_)
+            prefill[p["act_dtype"]] = p
+            print(f"# prefill {p['act_dtype']}: {p['tflops']:.1f} TFLOP/s",
+                  file=sys.stderr, flush=True)
+    cpu_dec = cpu_pre = None
+    if not args.no_cpu_baseline:
+        cpu_dec = cpu_baseline_decode(args.cpu_seconds)
+        if not args.skip_prefill:
+            cpu_pre = cpu_baseline_prefill(args.cpu_seconds)
+            prefill["cpu_baseline"] = cpu_pre
+
+    d1 = dec[1]
+    roof = dict(bound="hbm", kernel="k_gemv (fused NF4 dequant-GEMV, batch 1)",
+                achieved=d1["gemv_achieved_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=d1["gemv_achieved_gbs"] / HBM_PEAK_GBS,
+                bytes_per_launch=d1["gemv_bytes_per_launch"],
+                avg_launch_ms=d1["gemv_ms_per_launch"], traffic=None)
+    line = {
+        "metric": METRIC,
+        "value": d1["weight_gbs"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": d1["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": d1["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch RNG on GPU; NF4 weights quantized on GPU)",
+        "config": {
+            "workload": ("C2 decode: fused NF4 dequant-GEMV forward of 11008x4096 "
+                         "then 4096x11008 (block 64, double quant), LoRA r=16 "
+                         "alpha=32, batch 1, fp32 X"),
+            "global_batch": 1,
+            "weight_copies_rotated": dec_cfg["copies"],
+            "packed_weight_bytes_per_step": dec_cfg["packed_weight_bytes"],
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu_dec,
+        "decode_batches": {str(b): {k: v for k, v in r_.items()} for b, r_ in dec.items()},
+        "prefill": prefill,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

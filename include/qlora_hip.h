@@ -1,0 +1,237 @@
+/*
+ * qlora_hip.h -- C ABI of the MI355X (gfx950) QloraLinear hot path.
+ *
+ * Drop-in boundary for stuarch/VkQLoRA.rs `qlora-wgpu` (the GPU backend of
+ * the QLoRA linear layer) plus GPU versions of the two CPU-only pieces of
+ * `qlora-core` it is used with: `QuantizedTensor::quantize` and
+ * `Adam8bit::step`.  Every entry point names the reference interface it
+ * replaces (paths relative to the reference tree).
+ *
+ * Conventions
+ *  - Plain pointers and sizes only.  Host-memory entry points take
+ *    borrowed host slices plus their lengths, validate them with the
+ *    reference's rules and messages, run on the GPU and return only when
+ *    the result is in the caller's buffers (the reference blocks in
+ *    `pollster::block_on` / `device.poll(Wait)`: qlora-wgpu/src/context.rs:34,
+ *    kernels.rs:413).
+ *  - `*_dev` entry points take device pointers that are already resident in
+ *    HBM, enqueue on `stream` (a hipStream_t; NULL = the context's stream)
+ *    and return without synchronising.  Sizes are trusted.
+ *  - The caller allocates every output at its exact size.  Opaque handles
+ *    (qh_ctx, qh_adam8bit) are the only library-owned memory.
+ *  - Errors never cross the ABI as exceptions: every call returns a
+ *    qh_status whose values map 1:1 onto `QloraError`
+ *    (qlora-core/src/error.rs:6-14), and qh_last_error() returns the
+ *    message in the reference's Display format ("shape mismatch: ...",
+ *    "invalid config: ...", "gpu error: ...", error.rs:16-24).
+ *  - A qh_ctx may be shared between threads; calls on one context are
+ *    serialised by a mutex inside it.
+ */
+#ifndef QLORA_HIP_H
+#define QLORA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QH_API __attribute__((visibility("default")))
+#define QH_ABI_VERSION 1u
+
+typedef enum qh_status {
+  QH_OK = 0,
+  QH_ERR_SHAPE_MISMATCH = 1, /* QloraError::ShapeMismatch (error.rs:8) */
+  QH_ERR_INVALID_CONFIG = 2, /* QloraError::InvalidConfig (error.rs:10) */
+  QH_ERR_GPU = 3,            /* QloraError::Gpu (error.rs:12) */
+  QH_NO_DEVICE = 4 /* try_new_blocking() -> Ok(None) (context.rs:50-53) */
+} qh_status;
+
+/* Scale storage of a quantized weight: `ScaleStore` (quant.rs:84-89). */
+typedef enum qh_scale_kind {
+  QH_SCALES_F32 = 0,     /* ScaleStore::F32: one fp32 absmax per block */
+  QH_SCALES_DQ_INT8 = 1  /* ScaleStore::Int8: i8 code per block, fp32
+                            absmax per 256 blocks (double quantization) */
+} qh_scale_kind;
+
+typedef enum qh_dtype { QH_F32 = 0, QH_BF16 = 1 } qh_dtype;
+
+typedef enum qh_matmul_op {
+  QH_MM_NN = 0, /* C(m,n) = A(m,k) B(k,n)        lora.rs:129-142 */
+  QH_MM_TN = 1, /* C(k,n) = A(m,k)^T B(m,n)      lora.rs:148-162 */
+  QH_MM_NT = 2  /* C(m,n) = A(m,k) B(n,k)^T      lora.rs:169-183 */
+} qh_matmul_op;
+
+/* A row-major (rows x cols) NF4 weight: `QuantizedTensor` (quant.rs:93-100).
+ * codes: ceil(n/2) bytes, element 2i in the low nibble of byte i.
+ * F32 scales: `scales`, ceil(n/block_size) floats.
+ * DQ scales:  `scale_codes` (i8 bit-cast to u8), ceil(n/block_size) bytes,
+ *             and `absmax`, ceil(num_blocks/256) floats. */
+typedef struct qh_qweight {
+  size_t rows, cols, block_size;
+  const uint8_t *codes;
+  int32_t scale_kind; /* qh_scale_kind */
+  const float *scales;
+  const uint8_t *scale_codes;
+  const float *absmax;
+} qh_qweight;
+
+/* `LoraAdapter` (lora.rs:16-24): A (r x in_dim), B (out_dim x r), row-major,
+ * scale alpha / r (lora.rs:64-66).  Pass NULL for "no adapter". */
+typedef struct qh_lora {
+  const float *a;
+  size_t a_len;
+  const float *b;
+  size_t b_len;
+  size_t r;
+  float alpha;
+} qh_lora;
+
+typedef struct qh_ctx qh_ctx;
+
+/* ---- context: GpuContext (qlora-wgpu/src/context.rs:18-115) ------------ */
+QH_API uint32_t qh_abi_version(void);
+/* GpuContext::try_new_blocking (context.rs:33).  QH_NO_DEVICE when no
+ * MI355X is visible (*out stays NULL), QH_ERR_GPU on runtime failure. */
+QH_API qh_status qh_ctx_create(qh_ctx **out);
+QH_API void qh_ctx_destroy(qh_ctx *ctx);
+/* Message of the last failing call on this thread ("" if none). */
+QH_API const char *qh_last_error(void);
+/* Device name / gfx arch of the context's GPU. */
+QH_API qh_status qh_ctx_device_name(qh_ctx *ctx, char *buf, size_t len);
+/* Wait for all work on the context's stream. */
+QH_API qh_status qh_ctx_synchronize(qh_ctx *ctx);
+/* Kernel timing (no counterpart in the reference, whose dispatches carry
+ * no timestamps: kernels.rs:383).  While enabled, every hot-path kernel
+ * launch is bracketed by HIP events recorded on its own stream.  The report
+ * waits for those events and writes one line per kernel name:
+ * "<name> <launches> <total_ms>\n"; `reset` clears the totals. */
+QH_API qh_status qh_ctx_set_timing(qh_ctx *ctx, int enable);
+QH_API qh_status qh_ctx_timing_report(qh_ctx *ctx, char *buf, size_t len,
+                                      int reset);
+
+/* ---- layout helpers (quant.rs:93-100, 223-257) ------------------------- */
+QH_API size_t qh_codes_len(size_t rows, size_t cols);
+QH_API size_t qh_num_blocks(size_t rows, size_t cols, size_t block_size);
+QH_API size_t qh_num_absmax(size_t rows, size_t cols, size_t block_size);
+/* QuantizedTensor::storage_bytes (quant.rs:229-235). */
+QH_API size_t qh_storage_bytes(const qh_qweight *w);
+
+/* ---- quantization ------------------------------------------------------ */
+/* QuantizedTensor::quantize (quant.rs:104-154) with nearest_nf4_code
+ * (:263-278) and double_quantize_scales (:283-299).  Bit-exact.
+ * double_quant == 0 fills `scales`; otherwise `scale_codes` and `absmax`. */
+QH_API qh_status qh_quantize_nf4(qh_ctx *ctx, const float *w, size_t w_len,
+                                 size_t rows, size_t cols, size_t block_size,
+                                 int double_quant, uint8_t *codes,
+                                 float *scales, uint8_t *scale_codes,
+                                 float *absmax);
+/* QuantizedTensor::block_scales (quant.rs:212-221): decoded fp32 scales. */
+QH_API qh_status qh_block_scales(qh_ctx *ctx, const qh_qweight *w,
+                                 float *out);
+/* gpu_dequantize (qlora-wgpu/src/kernels.rs:44-103) ==
+ * QuantizedTensor::dequantize (quant.rs:157-167).  Bit-exact fp32. */
+QH_API qh_status qh_dequantize(qh_ctx *ctx, const qh_qweight *w, float *out);
+
+/* ---- GEMMs: gpu_matmul{,_trans_a,_trans_b} (kernels.rs:140-257) -------- */
+QH_API qh_status qh_matmul(qh_ctx *ctx, const float *a, size_t a_len,
+                           const float *b, size_t b_len, size_t m, size_t k,
+                           size_t n, float *c);
+QH_API qh_status qh_matmul_trans_a(qh_ctx *ctx, const float *a, size_t a_len,
+                                   const float *b, size_t b_len, size_t m,
+                                   size_t k, size_t n, float *c);
+QH_API qh_status qh_matmul_trans_b(qh_ctx *ctx, const float *a, size_t a_len,
+                                   const float *b, size_t b_len, size_t m,
+                                   size_t k, size_t n, float *c);
+
+/* ---- the layer ---------------------------------------------------------- */
+/* gpu_qlora_forward (kernels.rs:262-296) == QloraLinear::forward
+ * (qlora.rs:86-107).  y: batch x out_dim. */
+QH_API qh_status qh_qlora_forward(qh_ctx *ctx, const qh_qweight *w,
+                                  const qh_lora *lora, const float *x,
+                                  size_t x_len, size_t batch, float *y);
+/* gpu_qlora_backward (kernels.rs:301-353) == QloraLinear::backward
+ * (qlora.rs:116-165).  grad_x: batch x in_dim; grad_a (r x in_dim) and
+ * grad_b (out_dim x r) are written only when lora != NULL. */
+QH_API qh_status qh_qlora_backward(qh_ctx *ctx, const qh_qweight *w,
+                                   const qh_lora *lora, const float *x,
+                                   size_t x_len, const float *dy,
+                                   size_t dy_len, size_t batch, float *grad_x,
+                                   float *grad_a, float *grad_b);
+
+/* ---- paged 8-bit Adam: Adam8bit (qlora-core/src/optim.rs:32-249) ------- */
+typedef struct qh_adam_config { /* AdamConfig (optim.rs:32-60) */
+  float lr, beta1, beta2, eps;
+  size_t block_size;
+  size_t max_resident_pages; /* SIZE_MAX = everything resident */
+} qh_adam_config;
+
+typedef struct qh_adam_stats { /* AdamStats (optim.rs:135-141) */
+  size_t pages_streamed;
+  size_t state_bytes;
+} qh_adam_stats;
+
+typedef struct qh_adam8bit qh_adam8bit;
+
+/* AdamConfig::default (optim.rs:49-60). */
+QH_API void qh_adam_config_default(qh_adam_config *cfg);
+/* Adam8bit::new (optim.rs:155-161): validates the config. */
+QH_API qh_status qh_adam8bit_create(qh_ctx *ctx, const qh_adam_config *cfg,
+                                    qh_adam8bit **out);
+QH_API void qh_adam8bit_destroy(qh_adam8bit *opt);
+/* Adam8bit::step (optim.rs:164-199) on host slices: params updated in
+ * place.  Bit-exact with the reference's f32 arithmetic. */
+QH_API qh_status qh_adam8bit_step(qh_adam8bit *opt, float *const *params,
+                                  const size_t *param_lens,
+                                  const float *const *grads,
+                                  const size_t *grad_lens, size_t count,
+                                  qh_adam_stats *stats);
+/* Same step on device-resident params/grads, enqueued on `stream`. */
+QH_API qh_status qh_adam8bit_step_dev(qh_adam8bit *opt,
+                                      float *const *d_params,
+                                      const float *const *d_grads,
+                                      const size_t *lens, size_t count,
+                                      qh_adam_stats *stats, void *stream);
+/* Adam8bit::state_bytes (optim.rs:201-204). */
+QH_API size_t qh_adam8bit_state_bytes(const qh_adam8bit *opt);
+/* Copy the int8 state of parameter `idx` to host memory (m/v codes: numel
+ * bytes, m/v scales: ceil(numel/block_size) floats). */
+QH_API qh_status qh_adam8bit_get_state(qh_adam8bit *opt, size_t idx,
+                                       uint8_t *m_codes, float *m_scales,
+                                       uint8_t *v_codes, float *v_scales,
+                                       uint64_t *step);
+
+/* ---- device-resident hot path (async on `stream`) ----------------------- */
+/* All pointers are device pointers; `w` describes device buffers. */
+QH_API qh_status qh_quantize_nf4_dev(qh_ctx *ctx, const float *d_w,
+                                     size_t rows, size_t cols,
+                                     size_t block_size, int double_quant,
+                                     uint8_t *d_codes, float *d_scales,
+                                     uint8_t *d_scale_codes, float *d_absmax,
+                                     void *stream);
+QH_API qh_status qh_dequantize_dev(qh_ctx *ctx, const qh_qweight *w,
+                                   float *d_out, void *stream);
+QH_API qh_status qh_matmul_dev(qh_ctx *ctx, int op, const float *d_a,
+                               const float *d_b, size_t m, size_t k, size_t n,
+                               float *d_c, void *stream);
+/* Fused forward.  x: batch x in_dim in `x_dtype` (QH_BF16 = bf16
+ * activations, upcast exactly).  d_t1 (optional, batch x r fp32) receives
+ * X.A^T for reuse by the backward. */
+QH_API qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w,
+                                      const qh_lora *lora, const void *d_x,
+                                      int x_dtype, size_t batch, float *d_y,
+                                      float *d_t1, void *stream);
+/* Fused backward.  x and dy in `act_dtype`.  d_t1: X.A^T from the forward
+ * (NULL = recompute). */
+QH_API qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w,
+                                       const qh_lora *lora, const void *d_x,
+                                       const void *d_dy, int act_dtype,
+                                       size_t batch, const float *d_t1,
+                                       float *d_grad_x, float *d_grad_a,
+                                       float *d_grad_b, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QLORA_HIP_H */

@@ -1,0 +1,292 @@
+"""ctypes view of the CPU oracle (``liboracle.so``, built from qlora_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP library.  Only tests/,
+``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg import this
+module; the product path (``vkqlora.rs_amd``) never does.
+
+Each wrapper restates one function of stuarch/VkQLoRA.rs ``qlora-core``;
+the C source cites the reference file:line it follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+NF4_ZERO_CODE = 7
+DOUBLE_QUANT_BLOCK = 256
+
+_f32p = C.POINTER(C.c_float)
+_u8p = C.POINTER(C.c_uint8)
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (always re-run by callers)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        L.or_rng_next_f64.restype = C.c_double
+        L.or_rng_next_f64.argtypes = [C.POINTER(C.c_uint64)]
+        L.or_rng_next_normal.restype = C.c_float
+        L.or_nearest_nf4_code.restype = C.c_uint8
+        L.or_nearest_nf4_code.argtypes = [C.c_float, C.c_float]
+        L.or_quantize.restype = C.c_int
+        L.or_quantize.argtypes = [_f32p, C.c_size_t, C.c_size_t, C.c_int, _u8p,
+                                  _f32p, _u8p, _f32p]
+        L.or_block_scales_dq.argtypes = [_u8p, _f32p, C.c_size_t, _f32p]
+        L.or_dequantize.argtypes = [_u8p, _f32p, C.c_size_t, C.c_size_t, _f32p]
+        for fn in ("or_matmul", "or_matmul_trans_a", "or_matmul_trans_b"):
+            getattr(L, fn).argtypes = [_f32p, _f32p, C.c_size_t, C.c_size_t,
+                                       C.c_size_t, _f32p]
+        L.or_qlora_forward.argtypes = [_f32p, C.c_size_t, C.c_size_t, _f32p, _f32p,
+                                       C.c_size_t, C.c_float, _f32p, C.c_size_t,
+                                       _f32p]
+        L.or_qlora_backward.argtypes = [_f32p, C.c_size_t, C.c_size_t, _f32p,
+                                        _f32p, C.c_size_t, C.c_float, _f32p,
+                                        _f32p, C.c_size_t, _f32p, _f32p, _f32p]
+        L.or_fill_normal.argtypes = [C.POINTER(C.c_uint64), _f32p, C.c_size_t,
+                                     C.c_float]
+        L.or_fill_uniform.argtypes = [C.POINTER(C.c_uint64), _f32p, C.c_size_t,
+                                      C.c_float, C.c_float]
+        L.or_adam_create.restype = C.c_void_p
+        L.or_adam_create.argtypes = [C.c_float, C.c_float, C.c_float, C.c_float,
+                                     C.c_size_t, C.c_size_t]
+        L.or_adam_destroy.argtypes = [C.c_void_p]
+        L.or_adam_step.restype = C.c_size_t
+        L.or_adam_step.argtypes = [C.c_void_p, C.POINTER(_f32p),
+                                   C.POINTER(_f32p), C.POINTER(C.c_size_t),
+                                   C.c_size_t]
+        L.or_adam_state_bytes.restype = C.c_size_t
+        L.or_adam_state_bytes.argtypes = [C.c_void_p]
+        L.or_quantize_block_i8.restype = C.c_float
+        L.or_quantize_block_i8.argtypes = [_f32p, C.c_size_t, _u8p]
+        L.or_dequant_block_i8.argtypes = [_u8p, C.c_float, C.c_size_t, _f32p]
+        L.or_adam_get_state.restype = C.c_int
+        L.or_adam_get_state.argtypes = [C.c_void_p, C.c_size_t, _u8p, _f32p, _u8p,
+                                        _f32p, C.POINTER(C.c_uint64)]
+        _lib = L
+    return _lib
+
+
+def _fp(a):
+    return a.ctypes.data_as(_f32p)
+
+
+def _bp(a):
+    return a.ctypes.data_as(_u8p)
+
+
+def nf4_levels() -> np.ndarray:
+    arr = (C.c_float * 16).in_dll(lib(), "OR_NF4_LEVELS")
+    return np.array(arr[:], dtype=np.float32)
+
+
+# ---- generator (qlora-core/tests/quant.rs:6-24) ---------------------------
+class Rng:
+    """xorshift64* + Box-Muller, as in the reference's tests."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF)
+
+    def normal(self, n: int, scale: float = 1.0) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        lib().or_fill_normal(C.byref(self.state), _fp(out), n, scale)
+        return out
+
+    def uniform(self, n: int, lo: float, hi: float) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        lib().or_fill_uniform(C.byref(self.state), _fp(out), n, lo, hi)
+        return out
+
+    def next_f64(self) -> float:
+        return float(lib().or_rng_next_f64(C.byref(self.state)))
+
+
+# ---- quant.rs -------------------------------------------------------------
+def nearest_nf4_code(w: float, absmax: float) -> int:
+    return int(lib().or_nearest_nf4_code(w, absmax))
+
+
+def quantize(w: np.ndarray, block_size: int = 64, double_quant: bool = True):
+    """Returns dict(codes, scales | scale_codes+absmax) (quant.rs:104-154)."""
+    w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+    n = w.size
+    if block_size == 0:
+        raise ValueError("invalid config: block_size must be > 0")
+    nb = -(-n // block_size)
+    codes = np.zeros((n + 1) // 2, dtype=np.uint8)
+    out = {"codes": codes, "n": n, "block_size": block_size}
+    if double_quant:
+        sc = np.zeros(nb, dtype=np.uint8)
+        am = np.zeros(-(-nb // DOUBLE_QUANT_BLOCK), dtype=np.float32)
+        rc = lib().or_quantize(_fp(w), n, block_size, 1, _bp(codes), None,
+                               _bp(sc), _fp(am))
+        out.update(scale_codes=sc, absmax=am)
+    else:
+        sf = np.zeros(nb, dtype=np.float32)
+        rc = lib().or_quantize(_fp(w), n, block_size, 0, _bp(codes), _fp(sf),
+                               None, None)
+        out.update(scales=sf)
+    if rc != 0:
+        raise ValueError("invalid config: block_size must be > 0")
+    return out
+
+
+def block_scales(q) -> np.ndarray:
+    """quant.rs:212-221."""
+    if "scales" in q:
+        return q["scales"].copy()
+    nb = q["scale_codes"].size
+    out = np.empty(nb, dtype=np.float32)
+    lib().or_block_scales_dq(_bp(q["scale_codes"]), _fp(q["absmax"]), nb,
+                             _fp(out))
+    return out
+
+
+def dequantize(q) -> np.ndarray:
+    """quant.rs:157-167."""
+    sc = block_scales(q)
+    out = np.empty(q["n"], dtype=np.float32)
+    lib().or_dequantize(_bp(q["codes"]), _fp(sc), q["n"], q["block_size"],
+                        _fp(out))
+    return out
+
+
+def storage_bytes(q) -> int:
+    """quant.rs:229-235."""
+    if "scales" in q:
+        return q["codes"].size + 4 * q["scales"].size
+    return q["codes"].size + q["scale_codes"].size + 4 * q["absmax"].size
+
+
+# ---- lora.rs --------------------------------------------------------------
+def _mm(fn, a, b, m, k, n, out_len):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    c = np.empty(out_len, dtype=np.float32)
+    getattr(lib(), fn)(_fp(a), _fp(b), m, k, n, _fp(c))
+    return c
+
+
+def matmul(a, b, m, k, n):
+    return _mm("or_matmul", a, b, m, k, n, m * n)
+
+
+def matmul_trans_a(a, b, m, k, n):
+    return _mm("or_matmul_trans_a", a, b, m, k, n, k * n)
+
+
+def matmul_trans_b(a, b, m, k, n):
+    return _mm("or_matmul_trans_b", a, b, m, k, n, m * n)
+
+
+# ---- qlora.rs -------------------------------------------------------------
+def qlora_forward(w_deq, out_dim, in_dim, a, b, r, alpha, x, batch):
+    w_deq = np.ascontiguousarray(w_deq, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(batch * out_dim, dtype=np.float32)
+    if a is None:
+        lib().or_qlora_forward(_fp(w_deq), out_dim, in_dim, None, None, 0, 0.0,
+                               _fp(x), batch, _fp(y))
+    else:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        lib().or_qlora_forward(_fp(w_deq), out_dim, in_dim, _fp(a), _fp(b), r,
+                               alpha, _fp(x), batch, _fp(y))
+    return y
+
+
+def qlora_backward(w_deq, out_dim, in_dim, a, b, r, alpha, x, dy, batch):
+    w_deq = np.ascontiguousarray(w_deq, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    dy = np.ascontiguousarray(dy, dtype=np.float32)
+    gx = np.empty(batch * in_dim, dtype=np.float32)
+    if a is None:
+        lib().or_qlora_backward(_fp(w_deq), out_dim, in_dim, None, None, 0, 0.0,
+                                _fp(x), _fp(dy), batch, _fp(gx), None, None)
+        return gx, None, None
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    ga = np.empty(r * in_dim, dtype=np.float32)
+    gb = np.empty(out_dim * r, dtype=np.float32)
+    lib().or_qlora_backward(_fp(w_deq), out_dim, in_dim, _fp(a), _fp(b), r,
+                            alpha, _fp(x), _fp(dy), batch, _fp(gx), _fp(ga),
+                            _fp(gb))
+    return gx, ga, gb
+
+
+# ---- optim.rs -------------------------------------------------------------
+class Adam8bit:
+    """optim.rs:147-249 (paged 8-bit Adam, `v` in the sqrt domain)."""
+
+    def __init__(self, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
+                 block_size=256, max_resident_pages=None):
+        mrp = (1 << 64) - 1 if max_resident_pages is None else max_resident_pages
+        self.block_size = block_size
+        self._h = lib().or_adam_create(lr, beta1, beta2, eps, block_size, mrp)
+        if not self._h:
+            raise ValueError("invalid config")
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().or_adam_destroy(self._h)
+            self._h = None
+
+    def step(self, params, grads):
+        """Updates the float32 arrays in ``params`` in place; returns
+        pages_streamed."""
+        if len(params) != len(grads):
+            raise ValueError("shape mismatch")
+        for p, g in zip(params, grads):
+            if p.size != g.size:
+                raise ValueError("shape mismatch")
+            assert p.dtype == np.float32 and p.flags.c_contiguous
+        cnt = len(params)
+        pp = (_f32p * cnt)(*[_fp(p) for p in params])
+        gs = [np.ascontiguousarray(g, dtype=np.float32) for g in grads]
+        gp = (_f32p * cnt)(*[_fp(g) for g in gs])
+        lens = (C.c_size_t * cnt)(*[p.size for p in params])
+        return int(lib().or_adam_step(self._h, pp, gp, lens, cnt))
+
+    def state_bytes(self) -> int:
+        return int(lib().or_adam_state_bytes(self._h))
+
+    def state(self, idx: int, numel: int):
+        nb = -(-numel // self.block_size)
+        mc = np.zeros(numel, np.uint8)
+        vc = np.zeros(numel, np.uint8)
+        ms = np.zeros(nb, np.float32)
+        vs = np.zeros(nb, np.float32)
+        step = C.c_uint64(0)
+        rc = lib().or_adam_get_state(self._h, idx, _bp(mc), _fp(ms), _bp(vc),
+                                     _fp(vs), C.byref(step))
+        if rc != 0:
+            raise IndexError(idx)
+        return dict(m_codes=mc, m_scales=ms, v_codes=vc, v_scales=vs,
+                    step=step.value)
+
+
+def quantize_block_i8(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    codes = np.zeros(x.size, np.uint8)
+    am = lib().or_quantize_block_i8(_fp(x), x.size, _bp(codes))
+    return codes, float(am)
+
+
+def dequant_block_i8(codes, absmax):
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.empty(codes.size, np.float32)
+    lib().or_dequant_block_i8(_bp(codes), absmax, codes.size, _fp(out))
+    return out

@@ -1,0 +1,56 @@
+"""Shared helpers: seeded inputs (the reference's xorshift64* generator) and
+the normalised error metric used by every floating-point parity test.
+
+err = max_i |got_i - want_i| / (sqrt(K_red) * rms(opA) * rms(opB))
+
+K_red is the reduction length of the output (K for Y, out_dim for grad_x,
+batch for grad_A and grad_B); opA, opB are the two operands of that
+reduction.  It is the error relative to one output's standard deviation
+for i.i.d. inputs.  Bars: 1e-4 for fp32, 5e-3 for bf16 activations.
+"""
+import numpy as np
+
+TOL_F32 = 1e-4
+TOL_BF16 = 5e-3
+SEED = 0x1234_5678_9ABC_DEF0
+
+
+def rms(a) -> float:
+    a = np.asarray(a, dtype=np.float64)
+    return float(np.sqrt(np.mean(a * a))) if a.size else 0.0
+
+
+def nerr(got, want, k_red, op_a, op_b) -> float:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    if got.size == 0:
+        return 0.0
+    den = np.sqrt(max(k_red, 1)) * rms(op_a) * rms(op_b)
+    if den == 0.0:
+        den = 1.0
+    return float(np.max(np.abs(got - want)) / den)
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even of float32 to bfloat16, returned as float32."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def layer_inputs(oracle, out_dim, in_dim, r, batch, seed=SEED, wscale=0.02):
+    """W = wscale*N, A = U(+-1/sqrt(in)), B = 0.01*N, X = N, dY = N, drawn in
+    that order from one generator."""
+    g = oracle.Rng(seed)
+    w = g.normal(out_dim * in_dim, wscale)
+    bound = 1.0 / np.sqrt(in_dim)
+    a = g.uniform(r * in_dim, -bound, bound) if r else None
+    b = g.normal(out_dim * r, 0.01) if r else None
+    x = g.normal(batch * in_dim)
+    dy = g.normal(batch * out_dim)
+    return w, a, b, x, dy

@@ -1,0 +1,194 @@
+"""GPU parity of the device-resident entry points (``*_dev``) at the
+BASELINE shapes: bf16 activations, the T1 cache handed from forward to
+backward, and full-size size-independent checks.
+
+Outputs are compared with the oracle on sampled rows (every output row is
+an independent reduction, so a row sample is exact per row); grad_A and
+grad_B are compared in full.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from parity import SEED, TOL_BF16, TOL_F32, bf16_round, nerr
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def QD(ctx):
+    from qlora_hip import device
+    return device
+
+
+def _setup(QD, ctx, N, K, r, M, seed, act=torch.float32):
+    g = O.Rng(seed)
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+    b = g.normal(N * r, 0.01)
+    x = g.normal(M * K)
+    dy = g.normal(M * N)
+    if act == torch.bfloat16:
+        x, dy = bf16_round(x), bf16_round(dy)
+    dev = torch.device("cuda:0")
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    t = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
+    return dict(w=w, a=a, b=b, x=x, dy=dy, W=W, ta=t(a), tb=t(b),
+                tx=t(x).to(act), tdy=t(dy).to(act))
+
+
+def _run(QD, ctx, d, N, K, r, M, alpha, rows):
+    dev = torch.device("cuda:0")
+    lora = QD.lora_struct(d["ta"], d["tb"], r, alpha)
+    y = torch.empty(M, N, device=dev)
+    t1 = torch.empty(M, r, device=dev)
+    gx = torch.empty(M, K, device=dev)
+    ga = torch.empty(r, K, device=dev)
+    gb = torch.empty(N, r, device=dev)
+    QD.forward(d["W"], lora, d["tx"], M, y, t1=t1, ctx=ctx)
+    QD.backward(d["W"], lora, d["tx"], d["tdy"], M, gx, ga, gb, t1=t1, ctx=ctx)
+    torch.cuda.synchronize()
+    q = O.quantize(d["w"])
+    # the device quantization is bit-exact with the oracle's
+    assert np.array_equal(d["W"].codes.cpu().numpy(), q["codes"])
+    assert np.array_equal(d["W"].scale_codes.cpu().numpy(), q["scale_codes"])
+    wd = O.dequantize(q)
+    x, dy = d["x"], d["dy"]
+    xs, dys = x.reshape(M, K)[rows].ravel(), dy.reshape(M, N)[rows].ravel()
+    yo = O.qlora_forward(wd, N, K, d["a"], d["b"], r, alpha, xs, len(rows))
+    gxo, _, _ = O.qlora_backward(wd, N, K, d["a"], d["b"], r, alpha, xs, dys, len(rows))
+    s = np.float32(alpha / r)
+    t1o = O.matmul_trans_b(x, d["a"], M, K, r)
+    ds = O.matmul(dy * s, d["b"], M, N, r)
+    gao = O.matmul_trans_a(ds, x, M, r, K)
+    gbo = O.matmul_trans_a(dy * s, t1o, M, N, r)
+    return dict(
+        y=nerr(y.cpu().numpy()[rows].ravel(), yo, K, x, wd),
+        t1=nerr(t1.cpu().numpy().ravel(), t1o, K, x, d["a"]),
+        gx=nerr(gx.cpu().numpy()[rows].ravel(), gxo, N, dy, wd),
+        ga=nerr(ga.cpu().numpy().ravel(), gao, M, ds, x),
+        gb=nerr(gb.cpu().numpy().ravel(), gbo, M, dy * s, t1o))
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_prefill_shape_parity(ctx, QD, act):
+    # config 3 at a reduced token count (the kernels and tiles are the same)
+    N = K = 4096
+    r, M, alpha = 64, 512, 16.0
+    _say(f"prefill-shape parity act={act}")
+    d = _setup(QD, ctx, N, K, r, M, SEED ^ 3, act)
+    rows = [0, 1, 127, 128, 255, 300, 511]
+    e = _run(QD, ctx, d, N, K, r, M, alpha, rows)
+    tol = TOL_F32 if act == torch.float32 else TOL_BF16
+    _say(e)
+    assert all(v < tol for v in e.values()), e
+
+
+@pytest.mark.parametrize("N,K", [(11008, 4096), (4096, 11008)])
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_decode_shape_forward_parity(ctx, QD, N, K, M):
+    # config 2: forward only
+    _say(f"decode parity N={N} K={K} M={M}")
+    r, alpha = 16, 32.0
+    d = _setup(QD, ctx, N, K, r, M, SEED ^ 2)
+    lora = QD.lora_struct(d["ta"], d["tb"], r, alpha)
+    y = torch.empty(M, N, device="cuda:0")
+    QD.forward(d["W"], lora, d["tx"], M, y, ctx=ctx)
+    torch.cuda.synchronize()
+    wd = O.dequantize(O.quantize(d["w"]))
+    yo = O.qlora_forward(wd, N, K, d["a"], d["b"], r, alpha, d["x"], M)
+    e = nerr(y.cpu().numpy().ravel(), yo, K, d["x"], wd)
+    assert e < TOL_F32, e
+
+
+def test_smollm_block_projections_and_adam(ctx, QD):
+    # config 4: seven projections fwd+bwd at 8x256 tokens, then one
+    # PagedAdam step (max_resident_pages=4) over the 14 adapter tensors
+    import qlora_hip as QH
+    projs = [(576, 576), (192, 576), (192, 576), (576, 576), (1536, 576),
+             (1536, 576), (576, 1536)]
+    M, r, alpha = 2048, 8, 16.0
+    grads_dev, params_dev, params_np = [], [], []
+    for i, (N, K) in enumerate(projs):
+        d = _setup(QD, ctx, N, K, r, M, SEED ^ (40 + i))
+        e = _run(QD, ctx, d, N, K, r, M, alpha, [0, 1000, 2047])
+        assert all(v < TOL_F32 for v in e.values()), (i, e)
+    # Adam over 14 tensors, device path vs oracle, bit-exact
+    g = O.Rng(SEED ^ 99)
+    lens = []
+    for N, K in projs:
+        lens += [r * K, N * r]
+    p_np = [g.normal(n, 0.05) for n in lens]
+    gr_np = [g.normal(n, 0.01) for n in lens]
+    p_dev = [torch.from_numpy(p).cuda() for p in p_np]
+    g_dev = [torch.from_numpy(x).cuda() for x in gr_np]
+    import ctypes as C
+    opt = QH.Adam8bit(lr=1e-3, max_resident_pages=4, ctx=ctx)
+    oo = O.Adam8bit(lr=1e-3, max_resident_pages=4)
+    cnt = len(lens)
+    pp = (C.c_void_p * cnt)(*[t.data_ptr() for t in p_dev])
+    gp = (C.c_void_p * cnt)(*[t.data_ptr() for t in g_dev])
+    ll = (C.c_size_t * cnt)(*lens)
+    st = QH._lib.AdamStats()
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    QH._lib.check(ctx.lib.qh_adam8bit_step_dev(opt.h, pp, gp, ll, cnt, C.byref(st),
+                                               stream))
+    pages = oo.step(p_np, gr_np)
+    torch.cuda.synchronize()
+    assert st.pages_streamed == pages == 318
+    for t, p in zip(p_dev, p_np):
+        assert np.array_equal(t.cpu().numpy().view(np.uint32), p.view(np.uint32))
+
+
+def test_quantize_70b_layer_bit_exact(ctx, QD):
+    # config 5's quantize pass at full size (28672 x 8192), bit-exact
+    N, K = 28672, 8192
+    _say("quantize 28672x8192")
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    w = torch.randn(N, K, device="cuda", generator=gen) * 0.02
+    W = QD.DeviceWeight.quantize(w, ctx=ctx)
+    torch.cuda.synchronize()
+    q = O.quantize(w.cpu().numpy().ravel())
+    assert np.array_equal(W.codes.cpu().numpy(), q["codes"])
+    assert np.array_equal(W.scale_codes.cpu().numpy(), q["scale_codes"])
+    assert np.array_equal(W.absmax.cpu().numpy().view(np.uint32),
+                          q["absmax"].view(np.uint32))
+    # dequantize at full size, bit-exact
+    wd = W.dequantize(ctx=ctx).cpu().numpy()
+    assert np.array_equal(wd.view(np.uint32), O.dequantize(q).view(np.uint32))
+
+
+def test_70b_layer_forward_backward_sampled(ctx, QD):
+    # config 5's fwd+bwd (28672x8192, r=64, 2048 tokens): sampled rows,
+    # plus the size-independent linearity check y(2x) = 2 y(x)
+    N, K, M, r, alpha = 28672, 8192, 2048, 64, 16.0
+    _say("70b fwd+bwd")
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    dev = torch.device("cuda:0")
+    w = torch.randn(N, K, device=dev, generator=gen) * 0.02
+    W = QD.DeviceWeight.quantize(w, ctx=ctx)
+    del w
+    a = (torch.rand(r, K, device=dev, generator=gen) * 2 - 1) / np.sqrt(K)
+    b = torch.randn(N, r, device=dev, generator=gen) * 0.01
+    x = torch.randn(M, K, device=dev, generator=gen)
+    lora = QD.lora_struct(a, b, r, alpha)
+    y = torch.empty(M, N, device=dev)
+    y2 = torch.empty(M, N, device=dev)
+    QD.forward(W, lora, x, M, y, ctx=ctx)
+    x2 = x * 2
+    QD.forward(W, lora, x2, M, y2, ctx=ctx)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, 2 * y)  # scaling by 2 is exact at every step
+    rows = [0, 777, 2047]
+    wd = W.dequantize(ctx=ctx).cpu().numpy()
+    xs = x.cpu().numpy()[rows].ravel()
+    yo = O.qlora_forward(wd, N, K, a.cpu().numpy().ravel(), b.cpu().numpy().ravel(),
+                         r, alpha, xs, len(rows))
+    e = nerr(y.cpu().numpy()[rows].ravel(), yo, K, xs, wd)
+    assert e < TOL_F32, e

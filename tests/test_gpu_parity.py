@@ -1,0 +1,321 @@
+"""GPU parity: the HIP library (through the C ABI) against the oracle on the
+same seeded inputs.
+
+Bars: quantize codes, scale codes, absmax and dequantized fp32 weights are
+bit-exact; the Adam step is bit-exact; GEMM / forward / backward outputs are
+within the normalised error 1e-4 (fp32) or 5e-3 (bf16 activations), see
+tests/parity.py.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+import qlora_hip as QH
+from parity import (SEED, TOL_BF16, TOL_F32, bf16_bits, bf16_round, layer_inputs,
+                    nerr)
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _same_bits(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape and a.dtype == b.dtype
+    if a.dtype == np.float32:
+        return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    return np.array_equal(a, b)
+
+
+def _q_equal(qg, qo):
+    assert _same_bits(qg["codes"], qo["codes"])
+    if "scales" in qo:
+        assert _same_bits(qg["scales"], qo["scales"])
+    else:
+        assert _same_bits(qg["scale_codes"], qo["scale_codes"])
+        assert _same_bits(qg["absmax"], qo["absmax"])
+
+
+# ---- quantize / dequantize: bit-exact -----------------------------------------
+SHAPES = [(576, 576), (10, 10), (2, 5), (1, 1), (3, 7), (64, 1000), (1, 16385),
+          (129, 512)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+@pytest.mark.parametrize("bs", [64, 32, 5])
+@pytest.mark.parametrize("dq", [True, False])
+def test_quantize_dequantize_bit_exact(ctx, rows, cols, bs, dq):
+    _say(f"quantize rows={rows} cols={cols} bs={bs} dq={dq}")
+    w = O.Rng(SEED ^ (rows * 7919 + cols)).normal(rows * cols, 0.02)
+    qg = QH.quantize(w, rows, cols, bs, dq, ctx=ctx)
+    qo = O.quantize(w, bs, dq)
+    _q_equal(qg, qo)
+    assert _same_bits(QH.dequantize(qg, ctx=ctx), O.dequantize(qo))
+    assert _same_bits(QH.block_scales(qg, ctx=ctx), O.block_scales(qo))
+
+
+def test_quantize_special_values(ctx):
+    _say("quantize special values")
+    w = O.Rng(11).normal(64 * 300, 1.0)
+    w[5] = np.inf
+    w[70] = np.nan
+    w[200:264] = 0.0                      # an all-zero block
+    w[300] = -0.0
+    w[400] = 1e-40                        # denormal
+    w[1000:1064] = 1e-42                  # a block of denormals
+    w[2000] = 3e38
+    w[5000:5064] = -np.inf
+    for dq in (True, False):
+        _q_equal(QH.quantize(w, 300, 64, 64, dq, ctx=ctx), O.quantize(w, 64, dq))
+
+
+def test_reference_quant_known_answers(ctx):
+    # tests/quant.rs:89-134 through the GPU path
+    w = np.array([i / 10 for i in range(10)], np.float32)
+    q = QH.quantize(w, 2, 5, ctx=ctx)
+    assert q["codes"].size == 5 and abs(QH.block_scales(q, ctx=ctx)[0] - 0.9) < 1e-6
+    w = np.array([((i % 251) - 125) / 125 for i in range(65536)], np.float32)
+    plain = QH.quantize(w, 256, 256, 64, False, ctx=ctx)
+    dq = QH.quantize(w, 256, 256, 64, True, ctx=ctx)
+    assert QH.storage_bytes(plain) - QH.storage_bytes(dq) == 4096 - 1040
+    z = QH.quantize(np.zeros(64, np.float32), 8, 8, ctx=ctx)
+    assert np.array_equal(QH.dequantize(z, ctx=ctx), np.zeros(64, np.float32))
+
+
+# ---- GEMMs -------------------------------------------------------------------
+@pytest.mark.parametrize("m,k,n", [(18, 20, 33), (2, 2, 2), (64, 576, 576),
+                                   (130, 257, 65), (1, 4096, 3), (300, 64, 300)])
+def test_matmuls(ctx, m, k, n):
+    _say(f"matmul m={m} k={k} n={n}")
+    g = O.Rng(m * 31 + k * 7 + n)
+    a, b_nn, b_nt, b_tn = (g.normal(m * k), g.normal(k * n), g.normal(n * k),
+                           g.normal(m * n))
+    assert nerr(QH.matmul(a, b_nn, m, k, n, ctx=ctx), O.matmul(a, b_nn, m, k, n),
+                k, a, b_nn) < TOL_F32
+    assert nerr(QH.matmul_trans_b(a, b_nt, m, k, n, ctx=ctx),
+                O.matmul_trans_b(a, b_nt, m, k, n), k, a, b_nt) < TOL_F32
+    assert nerr(QH.matmul_trans_a(a, b_tn, m, k, n, ctx=ctx),
+                O.matmul_trans_a(a, b_tn, m, k, n), m, a, b_tn) < TOL_F32
+
+
+def test_matmul_known_answer(ctx):
+    assert list(QH.matmul([1, 2, 3, 4], [5, 6, 7, 8], 2, 2, 2, ctx=ctx)) == [19, 22, 43, 50]
+
+
+def test_reference_gpu_gemm_tolerances(ctx):
+    # qlora-wgpu/tests/gpu_backward.rs:20-52
+    m, k, n = 18, 20, 33
+    a = np.array([((i * 11) % 13) / 13 - 0.5 for i in range(m * k)], np.float32)
+    b_nn = np.array([((i * 7) % 11) / 11 - 0.5 for i in range(k * n)], np.float32)
+    b_nt = np.array([((i * 5) % 9) / 9 - 0.5 for i in range(n * k)], np.float32)
+    b_tn = np.array([((i * 3) % 7) / 7 - 0.5 for i in range(m * n)], np.float32)
+    assert np.max(np.abs(QH.matmul(a, b_nn, m, k, n, ctx=ctx) - O.matmul(a, b_nn, m, k, n))) < 1e-3
+    assert np.max(np.abs(QH.matmul_trans_b(a, b_nt, m, k, n, ctx=ctx)
+                         - O.matmul_trans_b(a, b_nt, m, k, n))) < 1e-3
+    assert np.max(np.abs(QH.matmul_trans_a(a, b_tn, m, k, n, ctx=ctx)
+                         - O.matmul_trans_a(a, b_tn, m, k, n))) < 1e-3
+
+
+# ---- the layer ---------------------------------------------------------------
+def _check_layer(ctx, out_dim, in_dim, r, batch, alpha, dq=True, bs=64, seed=SEED):
+    w, a, b, x, dy = layer_inputs(O, out_dim, in_dim, r, batch, seed)
+    q = QH.quantize(w, out_dim, in_dim, bs, dq, ctx=ctx)
+    wd = O.dequantize(O.quantize(w, bs, dq))
+    y = QH.forward(q, a, b, r, alpha, x, batch, ctx=ctx)
+    yo = O.qlora_forward(wd, out_dim, in_dim, a, b, r, alpha, x, batch)
+    assert nerr(y, yo, in_dim, x, wd) < TOL_F32, "forward"
+    gx, ga, gb = QH.backward(q, a, b, r, alpha, x, dy, batch, ctx=ctx)
+    gxo, gao, gbo = O.qlora_backward(wd, out_dim, in_dim, a, b, r, alpha, x, dy, batch)
+    assert nerr(gx, gxo, out_dim, dy, wd) < TOL_F32, "grad_x"
+    if r:
+        s = alpha / r
+        t1 = O.matmul_trans_b(x, a, batch, in_dim, r)
+        ds = O.matmul(dy * np.float32(s), b, batch, out_dim, r)
+        assert nerr(ga, gao, batch, ds, x) < TOL_F32, "grad_a"
+        assert nerr(gb, gbo, batch, dy * np.float32(s), t1) < TOL_F32, "grad_b"
+    else:
+        assert ga is None and gb is None
+
+
+@pytest.mark.parametrize("out_dim,in_dim,r,batch,alpha", [
+    (576, 576, 8, 64, 16.0),     # config 1
+    (18, 20, 5, 3, 8.0),          # odd sizes (gpu_backward.rs:55-97)
+    (8, 32, 4, 2, 8.0),           # gpu_parity.rs:113-157
+    (192, 576, 8, 256, 16.0),     # SmolLM k/v projection
+    (576, 1536, 8, 70, 16.0),     # SmolLM down projection, ragged batch
+    (300, 128, 16, 1, 32.0),      # decode GEMV path
+    (300, 128, 16, 2, 32.0),
+    (300, 128, 16, 3, 32.0),
+    (300, 128, 16, 4, 32.0),
+    (257, 192, 3, 5, 3.0),        # s = 1: not the GEMV path, N ragged
+    (64, 64, 64, 130, 16.0),
+])
+def test_layer_parity(ctx, out_dim, in_dim, r, batch, alpha):
+    _say(f"layer out={out_dim} in={in_dim} r={r} batch={batch}")
+    _check_layer(ctx, out_dim, in_dim, r, batch, alpha)
+
+
+def test_layer_no_adapter_and_f32_scales(ctx):
+    _say("layer no adapter / f32 scales / other block sizes")
+    _check_layer(ctx, 64, 128, 0, 9, 0.0)
+    _check_layer(ctx, 64, 128, 4, 9, 8.0, dq=False)
+    _check_layer(ctx, 40, 96, 4, 9, 8.0, bs=32)   # generic (non-64 block) path
+    _check_layer(ctx, 40, 96, 4, 2, 8.0, bs=32)
+
+
+def test_reference_gpu_layer_tolerances(ctx):
+    # qlora-wgpu/tests/gpu_backward.rs:55-97 with its absolute tolerances
+    out_dim, in_dim, r, batch = 18, 20, 5, 3
+    w = np.array([((i * 37) % 17) / 17 - 1 for i in range(out_dim * in_dim)], np.float32)
+    a = np.array([((i * 13) % 7) / 7 - 0.5 for i in range(r * in_dim)], np.float32)
+    b = np.array([((i * 29) % 5) / 5 - 0.5 for i in range(out_dim * r)], np.float32)
+    x = np.array([((i * 3) % 11) / 11 - 0.5 for i in range(batch * in_dim)], np.float32)
+    dy = np.array([((i * 7) % 13) / 13 - 0.5 for i in range(batch * out_dim)], np.float32)
+    q = QH.quantize(w, out_dim, in_dim, ctx=ctx)
+    wd = O.dequantize(O.quantize(w))
+    y = QH.forward(q, a, b, r, 8.0, x, batch, ctx=ctx)
+    assert np.max(np.abs(y - O.qlora_forward(wd, out_dim, in_dim, a, b, r, 8.0, x, batch))) < 1e-3
+    g = QH.backward(q, a, b, r, 8.0, x, dy, batch, ctx=ctx)
+    go = O.qlora_backward(wd, out_dim, in_dim, a, b, r, 8.0, x, dy, batch)
+    for u, v in zip(g, go):
+        assert np.max(np.abs(u - v)) < 1e-2
+
+
+# ---- Adam: bit-exact ---------------------------------------------------------
+def test_adam_bit_exact_multi_tensor(ctx):
+    _say("adam bit-exact, SmolLM adapter tensors")
+    # config 4's 14 adapter tensors (r=8): q,k,v,o,gate,up,down A and B
+    dims = [(576, 576), (576, 192), (576, 192), (576, 576), (576, 1536),
+            (576, 1536), (1536, 576)]
+    lens = []
+    for din, dout in dims:
+        lens += [8 * din, dout * 8]
+    g = O.Rng(SEED)
+    params = [g.normal(n, 0.05) for n in lens]
+    pg = [p.copy() for p in params]
+    og = QH.Adam8bit(lr=1e-3, max_resident_pages=4, ctx=ctx)
+    oo = O.Adam8bit(lr=1e-3, max_resident_pages=4)
+    for step in range(4):
+        grads = [g.normal(n, 0.01 * (step + 1)) for n in lens]
+        st = og.step(pg, grads)
+        pages = oo.step(params, grads)
+        assert st.pages_streamed == pages == sum(-(-n // 256) for n in lens)
+        assert st.state_bytes == oo.state_bytes()
+        for i in range(len(lens)):
+            assert _same_bits(pg[i], params[i]), (step, i)
+    for i in (0, 5, 13):
+        sg, so = og.state(i, lens[i]), oo.state(i, lens[i])
+        for key in ("m_codes", "m_scales", "v_codes", "v_scales"):
+            assert _same_bits(sg[key], so[key]), (i, key)
+        assert sg["step"] == 4
+
+
+def test_adam_reference_behaviour(ctx):
+    # tests/optim.rs:62-131 through the GPU path
+    g = np.array([((i * 7) % 43) / 43 - 0.5 for i in range(256)], np.float32)
+    pa = [np.full(256, 0.5, np.float32), np.full(256, -1.0, np.float32)]
+    pb = [p.copy() for p in pa]
+    oa = QH.Adam8bit(lr=0.01, block_size=16, max_resident_pages=1, ctx=ctx)
+    ob = QH.Adam8bit(lr=0.01, block_size=16, ctx=ctx)
+    for _ in range(3):
+        sa, sb = oa.step(pa, [g, g]), ob.step(pb, [g, g])
+        assert sa.pages_streamed == sb.pages_streamed == 32
+        assert all(_same_bits(x, y) for x, y in zip(pa, pb))
+    p = [np.full(32, 2.0, np.float32)]
+    opt = QH.Adam8bit(lr=0.05, block_size=32, ctx=ctx)
+    for _ in range(300):
+        opt.step(p, [2.0 * p[0]])
+    assert np.max(np.abs(p[0])) < 0.05
+    opt = QH.Adam8bit(ctx=ctx)
+    opt.step([np.full(1024, 0.1, np.float32)], [np.full(1024, 0.01, np.float32)])
+    assert opt.state_bytes() == 2048 + 2 * 4 * 4
+    with pytest.raises(QH.QloraError, match="param 0: len = 4 but grad len = 5"):
+        opt.step([np.ones(4, np.float32)], [np.ones(5, np.float32)])
+
+
+def test_adam_numel_change_resets_state(ctx):
+    # optim.rs:189-192: a reshaped param gets a fresh state
+    og = QH.Adam8bit(lr=0.01, block_size=64, ctx=ctx)
+    oo = O.Adam8bit(lr=0.01, block_size=64)
+    r = O.Rng(3)
+    for n in (100, 100, 300, 300):
+        p = r.normal(n)
+        gr = r.normal(n)
+        pg, po = p.copy(), p.copy()
+        og.step([pg], [gr])
+        oo.step([po], [gr])
+        assert _same_bits(pg, po)
+
+
+# ---- qlora_wgpu surface (qlora-python/tests/test_qlora.py) -------------------
+def test_python_surface_reference_tests(ctx):
+    rows, cols = 8, 32
+    w = [((i * 11) % 13) / 13.0 - 0.5 for i in range(rows * cols)]
+    q = QH.quantize_nf4(w, rows, cols)
+    assert q.rows == rows and q.cols == cols
+    assert len(q.codes_list) == (rows * cols + 1) // 2
+    back = q.dequantize()
+    assert sum((b - o) ** 2 for b, o in zip(back, w)) / len(w) < 0.01
+
+    out_dim, in_dim, r, batch = 4, 16, 2, 2
+    w = [((i * 37) % 17) / 8.0 - 1.0 for i in range(out_dim * in_dim)]
+    a, b, x = [0.05] * (r * in_dim), [0.07] * (out_dim * r), [0.5] * (batch * in_dim)
+    q = QH.quantize_nf4(w, out_dim, in_dim)
+    y = QH.qlora_linear_forward(x, batch, q, a, b, 8.0)
+    scale = 8.0 / r
+    expected = []
+    for bi in range(batch):
+        for oi in range(out_dim):
+            base = sum(x[bi * in_dim + k] * w[oi * in_dim + k] for k in range(in_dim))
+            adapt = scale * sum(sum(x[bi * in_dim + k] * a[ri * in_dim + k]
+                                    for k in range(in_dim)) * b[oi * r + ri]
+                                for ri in range(r))
+            expected.append(base + adapt)
+    assert max(abs(u - v) for u, v in zip(y, expected)) < 0.2
+    assert len(QH.qlora_linear_forward([1.0] * in_dim, 1, QH.quantize_nf4([0.1] * 64, 4, 16))) == 4
+
+    out_dim, in_dim, r, batch = 3, 4, 2, 2
+    w = [((i * 37) % 11) / 11.0 - 0.5 for i in range(out_dim * in_dim)]
+    a = [((i * 13) % 7) / 7.0 - 0.5 for i in range(r * in_dim)]
+    b = [((i * 29) % 5) / 5.0 - 0.5 for i in range(out_dim * r)]
+    x = [0.5, -0.25, 0.75, 1.0, 0.0, 0.25, -0.5, 1.5]
+    q = QH.quantize_nf4(w, out_dim, in_dim)
+    g = QH.qlora_linear_backward(x, [1.0] * (batch * out_dim), batch, q, a, b, 8.0)
+    assert (len(g.grad_x), len(g.grad_a), len(g.grad_b)) == (8, 8, 6)
+
+    def loss(x_, a_, b_):
+        return sum(QH.qlora_linear_forward(x_, batch, q, a_, b_, 8.0))
+
+    def fd(buf, idx):
+        bufs = [list(x), list(a), list(b)]
+        bufs[buf][idx] += 1e-3
+        hi = loss(*bufs)
+        bufs[buf][idx] -= 2e-3
+        return (hi - loss(*bufs)) / 2e-3
+
+    for buf, grads in ((0, g.grad_x), (1, g.grad_a), (2, g.grad_b)):
+        for i, got in enumerate(grads):
+            assert abs(got - fd(buf, i)) < 2e-2
+
+    out_dim, in_dim, r, batch = 4, 8, 2, 2
+    w = [((i * 37) % 17) / 8.0 - 1.0 for i in range(out_dim * in_dim)]
+    a, b, x = [0.05] * (r * in_dim), [0.07] * (out_dim * r), [0.5] * (batch * in_dim)
+    q = QH.quantize_nf4(w, out_dim, in_dim)
+    opt = QH.PagedAdam(lr=0.05, max_resident_pages=1)
+
+    def mse(a_, b_):
+        y = QH.qlora_linear_forward(x, batch, q, a_, b_, 8.0)
+        return sum(u * u for u in y) / len(y)
+
+    before = mse(a, b)
+    for _ in range(5):
+        y = QH.qlora_linear_forward(x, batch, q, a, b, 8.0)
+        dy = [2 * u / len(y) for u in y]
+        g = QH.qlora_linear_backward(x, dy, batch, q, a, b, 8.0)
+        a, b = opt.step([a, b], [g.grad_a, g.grad_b])
+    assert mse(a, b) < before
+    assert opt.state_bytes() < 8 * (len(a) + len(b))

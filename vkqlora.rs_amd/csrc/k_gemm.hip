@@ -1,0 +1,466 @@
+// k_gemm.hip -- the fp32-MFMA tile engine for gfx950.
+//
+// One engine serves every GEMM of the path (the reference's three WGSL
+// kernels mm_nn / mm_nt / mm_tn, qlora-wgpu/shaders/gemm.wgsl:34-136, and the
+// CPU GEMMs of qlora-core/src/lora.rs:129-183 used by qlora.rs:86-165):
+//
+//   C[m][n] = alpha * ( sum_{k<K}  A[m][k] * B[k][n]
+//                     + sum_{j<K2} A2[m][j] * B2[j][n] )
+//
+// * B may be the packed NF4 weight: its tile is dequantized bit-exactly
+//   (L[code] * block_scale, quant.rs:157-167) from the code stream into LDS
+//   as fp32, so the MFMA sees exactly the reference's dequantized W.
+// * The optional second segment carries the LoRA term, so the forward
+//   X.W^T + s.T1.B^T and the input gradient dY.W + Ds.A each run as ONE
+//   kernel over a concatenated reduction.
+// * Activations may be bf16 (upcast exactly when staged).
+// * Split-K writes per-split partials that a second kernel sums in a fixed
+//   order: results are deterministic, no float atomics.
+//
+// Tiles: 256 threads = 4 waves; each wave owns a (BM/WAVES_M) x
+// (BN/(4/WAVES_M)) sub-tile built from v_mfma_f32_32x32x2_f32 tiles.
+// Operand tiles live in LDS k-major ([BK][rows + 4]) so that the 32 lanes
+// of an MFMA operand read 32 consecutive floats.  The next K-step's global
+// loads are issued before the current step's MFMAs (register prefetch).
+#include <type_traits>
+
+#include "qh_internal.h"
+#include "qh_nf4.h"
+
+namespace qh {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int NT = 256;  // threads per workgroup
+constexpr int BK = 32;   // reduction step
+constexpr int PAD = 4;
+
+__constant__ float c_lut16[17] = QH_NF4_LUT17_INIT;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// ---------------------------------------------------------------------------
+// Staging of one operand tile: R rows x BK reduction indices -> LDS S[BK][R+PAD]
+// ---------------------------------------------------------------------------
+template <int R, int FORM, int ELEM>
+struct Stage;
+
+// fp32 / bf16, ROWK: element (r, k) at p[r * ld + k]
+template <int R, int ELEM>
+struct Stage<R, ROWK, ELEM> {
+  static constexpr int V = R * BK / 4 / NT;
+  using raw_t = typename std::conditional<ELEM == E_F32, float4, uint2>::type;
+  raw_t raw[V];
+  __device__ __forceinline__ void load(const Operand &op, int64_t r0,
+                                       int64_t rlim, int64_t k0, int64_t klim,
+                                       bool vec_ok) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int idx = threadIdx.x + NT * v;
+      const int row = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
+      const int64_t gr = r0 + row, gk = k0 + kq;
+      if constexpr (ELEM == E_F32) {
+        const float *p = (const float *)op.p;
+        if (vec_ok && gr < rlim && gk + 3 < klim) {
+          raw[v] = *(const float4 *)(p + gr * op.ld + gk);
+        } else {
+          float t[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            t[j] = (gr < rlim && gk + j < klim) ? p[gr * op.ld + gk + j] : 0.0f;
+          ((float4 *)&raw[v])[0] = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      } else {
+        const uint16_t *p = (const uint16_t *)op.p;
+        if (vec_ok && gr < rlim && gk + 3 < klim) {
+          ((uint2 *)&raw[v])[0] = *(const uint2 *)(p + gr * op.ld + gk);
+        } else {
+          uint32_t t[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            t[j] = (gr < rlim && gk + j < klim) ? p[gr * op.ld + gk + j] : 0u;
+          ((uint2 *)&raw[v])[0] = make_uint2(t[0] | (t[1] << 16), t[2] | (t[3] << 16));
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float *S, float scale) const {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int idx = threadIdx.x + NT * v;
+      const int row = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
+      float f[4];
+      if constexpr (ELEM == E_F32) {
+        const float4 t = ((const float4 *)&raw[v])[0];
+        f[0] = t.x; f[1] = t.y; f[2] = t.z; f[3] = t.w;
+      } else {
+        const uint2 t = ((const uint2 *)&raw[v])[0];
+        f[0] = bf16_to_f32(t.x & 0xffffu); f[1] = bf16_to_f32(t.x >> 16);
+        f[2] = bf16_to_f32(t.y & 0xffffu); f[3] = bf16_to_f32(t.y >> 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) S[(kq + j) * (R + PAD) + row] = f[j] * scale;
+    }
+  }
+};
+
+// fp32 / bf16, KROW: element (r, k) at p[k * ld + r]
+template <int R, int ELEM>
+struct Stage<R, KROW, ELEM> {
+  static constexpr int V = R * BK / 4 / NT;
+  using raw_t = typename std::conditional<ELEM == E_F32, float4, uint2>::type;
+  raw_t raw[V];
+  __device__ __forceinline__ void load(const Operand &op, int64_t r0,
+                                       int64_t rlim, int64_t k0, int64_t klim,
+                                       bool vec_ok) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int idx = threadIdx.x + NT * v;
+      const int k = idx / (R / 4), rq = (idx % (R / 4)) * 4;
+      const int64_t gk = k0 + k, gr = r0 + rq;
+      if constexpr (ELEM == E_F32) {
+        const float *p = (const float *)op.p;
+        if (vec_ok && gk < klim && gr + 3 < rlim) {
+          raw[v] = *(const float4 *)(p + gk * op.ld + gr);
+        } else {
+          float t[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            t[j] = (gk < klim && gr + j < rlim) ? p[gk * op.ld + gr + j] : 0.0f;
+          ((float4 *)&raw[v])[0] = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      } else {
+        const uint16_t *p = (const uint16_t *)op.p;
+        if (vec_ok && gk < klim && gr + 3 < rlim) {
+          ((uint2 *)&raw[v])[0] = *(const uint2 *)(p + gk * op.ld + gr);
+        } else {
+          uint32_t t[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            t[j] = (gk < klim && gr + j < rlim) ? p[gk * op.ld + gr + j] : 0u;
+          ((uint2 *)&raw[v])[0] = make_uint2(t[0] | (t[1] << 16), t[2] | (t[3] << 16));
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float *S, float scale) const {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int idx = threadIdx.x + NT * v;
+      const int k = idx / (R / 4), rq = (idx % (R / 4)) * 4;
+      float4 f;
+      if constexpr (ELEM == E_F32) {
+        f = ((const float4 *)&raw[v])[0];
+      } else {
+        const uint2 t = ((const uint2 *)&raw[v])[0];
+        f = make_float4(bf16_to_f32(t.x & 0xffffu), bf16_to_f32(t.x >> 16),
+                        bf16_to_f32(t.y & 0xffffu), bf16_to_f32(t.y >> 16));
+      }
+      f.x *= scale; f.y *= scale; f.z *= scale; f.w *= scale;
+      *(float4 *)&S[k * (R + PAD) + rq] = f;
+    }
+  }
+};
+
+// Raw block-scale fields, decoded at store time (quant.rs:212-221).
+struct ScaleRaw {
+  float a;     // fp32 scale, or the super-block absmax
+  int32_t c;   // int8 scale code (DQ only)
+};
+
+__device__ __forceinline__ ScaleRaw load_scale(const DevQW &w, int64_t b) {
+  ScaleRaw s;
+  if (w.kind == 0) {
+    s.a = w.scales[b];
+    s.c = 0;
+  } else {
+    s.c = (int8_t)w.scale_codes[b];
+    s.a = w.absmax[b >> 8];
+  }
+  return s;
+}
+
+__device__ __forceinline__ float decode_scale(int kind, ScaleRaw s) {
+  return kind == 0 ? s.a : (float)s.c / 127.0f * s.a;
+}
+
+template <int BYTES>
+struct CodeWord;
+template <> struct CodeWord<8> { using t = uint2; };
+template <> struct CodeWord<4> { using t = uint32_t; };
+
+__device__ __forceinline__ uint32_t nib(uint2 w, int e) {
+  return ((e < 8 ? w.x : w.y) >> (4 * (e & 7))) & 15u;
+}
+__device__ __forceinline__ uint32_t nib(uint32_t w, int e) {
+  return (w >> (4 * e)) & 15u;
+}
+
+// NF4, ROWK (forward): tile rows are W rows n, reduction along W's row.
+// Requires cols % 64 == 0 (whole blocks per row).
+template <int R>
+struct Stage<R, ROWK, E_NF4> {
+  static constexpr int BYTES = R / 16;      // 8 (R=128) or 4 (R=64)
+  static constexpr int EPT = 2 * BYTES;     // elements per thread
+  static constexpr int TPR = 16 / BYTES;    // threads per row
+  using word_t = typename CodeWord<BYTES>::t;
+  word_t raw;
+  ScaleRaw sc;
+  bool valid;
+  __device__ __forceinline__ void load(const DevQW &w, int64_t r0, int64_t k0) {
+    const int row = threadIdx.x / TPR, kq = (threadIdx.x % TPR) * EPT;
+    const int64_t gr = r0 + row;
+    valid = gr < w.rows;
+    if (valid) {
+      const int64_t e = gr * w.cols + k0 + kq;
+      raw = *(const word_t *)(w.codes + (e >> 1));
+      sc = load_scale(w, e >> 6);
+    }
+  }
+  __device__ __forceinline__ void store(float *S, const float *lut,
+                                        int kind) const {
+    const int row = threadIdx.x / TPR, kq = (threadIdx.x % TPR) * EPT;
+    const float s = valid ? decode_scale(kind, sc) : 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      float v = valid ? lut[nib(raw, e)] * s : 0.0f;
+      S[(kq + e) * (R + PAD) + row] = v;
+    }
+  }
+};
+
+// NF4, KROW (input gradient): reduction index = W row n, tile rows = W
+// columns.  Requires cols % 64 == 0.
+template <int R>
+struct Stage<R, KROW, E_NF4> {
+  static constexpr int BYTES = R / 16;
+  static constexpr int EPT = 2 * BYTES;
+  using word_t = typename CodeWord<BYTES>::t;
+  word_t raw;
+  ScaleRaw sc;
+  bool valid;
+  // r0: first W column of the tile, k0: first W row; klim = W rows
+  __device__ __forceinline__ void load(const DevQW &w, int64_t r0, int64_t k0) {
+    const int kr = threadIdx.x / 8, cq = (threadIdx.x % 8) * EPT;
+    const int64_t gn = k0 + kr, gc = r0 + cq;
+    valid = gn < w.rows && gc < w.cols;
+    if (valid) {
+      const int64_t e = gn * w.cols + gc;
+      raw = *(const word_t *)(w.codes + (e >> 1));
+      sc = load_scale(w, e >> 6);
+    }
+  }
+  __device__ __forceinline__ void store(float *S, const float *lut,
+                                        int kind) const {
+    const int kr = threadIdx.x / 8, cq = (threadIdx.x % 8) * EPT;
+    const float s = valid ? decode_scale(kind, sc) : 0.0f;
+#pragma unroll
+    for (int e4 = 0; e4 < EPT; e4 += 4) {
+      float4 f;
+      f.x = valid ? lut[nib(raw, e4 + 0)] * s : 0.0f;
+      f.y = valid ? lut[nib(raw, e4 + 1)] * s : 0.0f;
+      f.z = valid ? lut[nib(raw, e4 + 2)] * s : 0.0f;
+      f.w = valid ? lut[nib(raw, e4 + 3)] * s : 0.0f;
+      *(float4 *)&S[kr * (R + PAD) + cq + e4] = f;
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// The kernel
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WAVES_M, int AF, int AE, int BF, int BE, int B2F>
+__global__ __launch_bounds__(NT) void k_gemm(GemmArgs g) {
+  constexpr int WAVES_N = 4 / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile must hold one 32x32 MFMA");
+  __shared__ float As[BK * (BM + PAD)];
+  __shared__ float Bs[BK * (BN + PAD)];
+  __shared__ float lut[16];
+
+  const int tid = threadIdx.x;
+  if (BE == E_NF4 && tid < 16) lut[tid] = c_lut16[tid];
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int wm0 = (wave / WAVES_N) * WM, wn0 = (wave % WAVES_N) * WN;
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  const int z = blockIdx.z;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  auto mma_step = [&]() {
+#pragma unroll 4
+    for (int s = 0; s < BK / 2; ++s) {
+      float a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = As[(2 * s + h) * (BM + PAD) + wm0 + i * 32 + l32];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = Bs[(2 * s + h) * (BN + PAD) + wn0 + j * 32 + l32];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // ---- segment 1 --------------------------------------------------------
+  int64_t kbeg = 0, kend = g.K;
+  if (g.splits > 1) {
+    const int64_t kps = ((g.K + g.splits - 1) / g.splits + 63) / 64 * 64;
+    kbeg = (int64_t)z * kps;
+    kend = kbeg + kps < g.K ? kbeg + kps : g.K;
+  }
+  const bool a_vec = (g.A.ld % 4 == 0) && (((uintptr_t)g.A.p & 15) == 0);
+  const bool b_vec = (g.B.ld % 4 == 0) && (((uintptr_t)g.B.p & 15) == 0);
+  const float bscale = g.B.scale;
+  {
+    Stage<BM, AF, AE> sa;
+    Stage<BN, BF, BE> sb;
+    auto load = [&](int64_t k0) {
+      sa.load(g.A, m0, g.M, k0, kend, a_vec);
+      if constexpr (BE == E_NF4) {
+        if (BF == ROWK) sb.load(g.qw, n0, k0);
+        else sb.load(g.qw, n0, k0);
+      } else {
+        sb.load(g.B, n0, g.N, k0, kend, b_vec);
+      }
+    };
+    auto store = [&]() {
+      sa.store(As, g.A.scale);
+      if constexpr (BE == E_NF4) sb.store(Bs, lut, g.qw.kind);
+      else sb.store(Bs, bscale);
+    };
+    if (kbeg < kend) {
+      load(kbeg);
+      __syncthreads();  // lut
+      store();
+      __syncthreads();
+      for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+        const bool more = k0 + BK < kend;
+        if (more) load(k0 + BK);
+        mma_step();
+        __syncthreads();
+        if (more) {
+          store();
+          __syncthreads();
+        }
+      }
+    }
+  }
+
+  // ---- segment 2 (LoRA) -------------------------------------------------
+  if (g.K2 > 0 && z == 0) {
+    Stage<BM, ROWK, E_F32> sa;
+    Stage<BN, B2F, E_F32> sb;
+    const bool a2_vec = (g.A2.ld % 4 == 0) && (((uintptr_t)g.A2.p & 15) == 0);
+    const bool b2_vec = (g.B2.ld % 4 == 0) && (((uintptr_t)g.B2.p & 15) == 0);
+    for (int64_t k0 = 0; k0 < g.K2; k0 += BK) {
+      sa.load(g.A2, m0, g.M, k0, g.K2, a2_vec);
+      sb.load(g.B2, n0, g.N, k0, g.K2, b2_vec);
+      sa.store(As, g.A2.scale);
+      sb.store(Bs, g.B2.scale);
+      __syncthreads();
+      mma_step();
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue -----------------------------------------------------------
+  float *C = g.C + (g.splits > 1 ? (int64_t)z * g.split_stride : 0);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm0 + i * 32 + 8 * (v / 4) + 4 * h + (v % 4);
+        const int64_t n = n0 + wn0 + j * 32 + l32;
+        if (m < g.M && n < g.N) C[m * g.ldc + n] = g.alpha * acc[i][j][v];
+      }
+}
+
+__global__ void k_reduce_splits(const float *__restrict__ part, int splits,
+                                int64_t stride, int64_t M, int64_t N,
+                                float *__restrict__ C, int64_t ldc) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * N) return;
+  float s = part[i];
+  for (int z = 1; z < splits; ++z) s += part[z * stride + i];
+  C[(i / N) * ldc + (i % N)] = s;
+}
+
+template <int BM, int BN, int WM_, int AF, int AE, int BF, int BE, int B2F>
+hipError_t run(const GemmArgs &g0, float *partial, hipStream_t s) {
+  GemmArgs g = g0;
+  float *out = g.C;
+  int64_t ldc = g.ldc;
+  if (g.splits > 1) {
+    g.C = partial;
+    g.ldc = g.N;
+    g.split_stride = g.M * g.N;
+  }
+  dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + BM - 1) / BM),
+            (unsigned)(g.splits > 1 ? g.splits : 1));
+  k_gemm<BM, BN, WM_, AF, AE, BF, BE, B2F><<<grid, dim3(NT), 0, s>>>(g);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || g.splits <= 1) return e;
+  const int64_t tot = g.M * g.N;
+  k_reduce_splits<<<dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s>>>(
+      partial, g.splits, g.M * g.N, g.M, g.N, out, ldc);
+  return hipGetLastError();
+}
+
+// Tile shape by problem size: 128x128 for big outputs, 64x64 otherwise.
+template <int AF, int AE, int BF, int BE, int B2F>
+hipError_t pick(const GemmArgs &g, float *partial, hipStream_t s) {
+  if (g.M >= 128 && g.N >= 128 && (g.M / 128) * (g.N / 128) >= 64)
+    return run<128, 128, 2, AF, AE, BF, BE, B2F>(g, partial, s);
+  return run<64, 64, 2, AF, AE, BF, BE, B2F>(g, partial, s);
+}
+
+template <int AF, int BF, int BE, int B2F>
+hipError_t pick_ae(const GemmArgs &g, float *partial, hipStream_t s) {
+  if (g.A.elem == E_BF16) return pick<AF, E_BF16, BF, BE, B2F>(g, partial, s);
+  return pick<AF, E_F32, BF, BE, B2F>(g, partial, s);
+}
+
+}  // namespace
+
+bool nf4_fast_ok(const DevQW &w) { return w.bs == 64 && w.cols % 64 == 0; }
+
+hipError_t launch_gemm(const GemmArgs &g, float *partial, hipStream_t s) {
+  if (g.M == 0 || g.N == 0) return hipSuccess;
+  const int af = g.A.form, bf = g.B.form, be = g.B.elem;
+  const int b2f = g.K2 > 0 ? g.B2.form : ROWK;
+  if (be == E_NF4) {
+    if (bf == ROWK) return pick_ae<ROWK, ROWK, E_NF4, ROWK>(g, partial, s);
+    return pick_ae<ROWK, KROW, E_NF4, KROW>(g, partial, s);
+  }
+  if (be == E_BF16) {  // grad_A with bf16 X: A = Ds^T (fp32, KROW)
+    return pick<KROW, E_F32, KROW, E_BF16, ROWK>(g, partial, s);
+  }
+  if (af == ROWK && bf == ROWK) {
+    if (b2f == ROWK) return pick_ae<ROWK, ROWK, E_F32, ROWK>(g, partial, s);
+  }
+  if (af == ROWK && bf == KROW) {
+    if (b2f == KROW) return pick_ae<ROWK, KROW, E_F32, KROW>(g, partial, s);
+    return pick_ae<ROWK, KROW, E_F32, ROWK>(g, partial, s);
+  }
+  if (af == KROW && bf == KROW) return pick_ae<KROW, KROW, E_F32, ROWK>(g, partial, s);
+  if (af == ROWK && bf == ROWK) return pick_ae<ROWK, ROWK, E_F32, KROW>(g, partial, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace qh

@@ -1,0 +1,99 @@
+// qh_internal.h -- declarations shared by the runtime (runtime.cpp) and the
+// gfx950 kernels (k_*.hip).  Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qh {
+
+// Device view of a quantized weight (rows x cols, flat row-major index).
+struct DevQW {
+  int64_t rows, cols, n, bs, nb;
+  const uint8_t *codes;
+  int kind;  // 0 = fp32 scales, 1 = int8 codes + fp32 absmax per 256 blocks
+  const float *scales;
+  const uint8_t *scale_codes;
+  const float *absmax;
+};
+
+// Operand storage forms of the GEMM tile engine.  The engine computes
+// C[m][n] = sum_k A[m][k] * B[k][n]; an operand with "rows" r (m for A, n
+// for B) and reduction index k is stored either
+//   ROWK: element (r, k) at p[r * ld + k]   (k contiguous), or
+//   KROW: element (r, k) at p[k * ld + r]   (r contiguous).
+enum Form { ROWK = 0, KROW = 1 };
+enum Elem { E_F32 = 0, E_BF16 = 1, E_NF4 = 2 };
+
+struct Operand {
+  const void *p;
+  int64_t ld;
+  int form;  // Form
+  int elem;  // Elem
+  float scale;  // multiplies the operand when staged (1.0f = none)
+};
+
+struct GemmArgs {
+  int64_t M, N;
+  // segment 1: reduction over K with operands A, B (B may be NF4)
+  Operand A, B;
+  int64_t K;
+  DevQW qw;  // valid when B.elem == E_NF4
+  // segment 2 (optional, K2 == 0 = none): extra reduction with fp32 operands
+  Operand A2, B2;
+  int64_t K2;
+  // output C[m * ldc + n] = alpha * acc; with split-K, split z writes to
+  // C + z * split_stride and only covers its K range of segment 1.
+  float *C;
+  int64_t ldc;
+  float alpha;
+  int splits;
+  int64_t split_stride;
+};
+
+// ---- k_quant.hip ----
+hipError_t launch_quantize(const float *w, int64_t n, int64_t bs, int dq,
+                           uint8_t *codes, float *scales, uint8_t *scale_codes,
+                           float *absmax, float *scratch, hipStream_t s);
+hipError_t launch_block_scales(const DevQW &w, float *out, hipStream_t s);
+hipError_t launch_dequantize(const DevQW &w, float *out, hipStream_t s);
+
+// ---- k_gemm.hip ----
+// Runs the tile engine; splits > 1 needs `partial` (splits * M * N floats)
+// and reduces into args.C deterministically.
+hipError_t launch_gemm(const GemmArgs &args, float *partial, hipStream_t s);
+// Tile-engine eligibility of a quantized B operand: block_size 64 and
+// whole blocks per row of the reduction form.
+bool nf4_fast_ok(const DevQW &w);
+
+// ---- k_gemv.hip ----
+// y[m][n] = sum_k x[m][k] W[n][k] + s * sum_j t1[m][j] * lb[n][j]  (M <= 4)
+hipError_t launch_gemv(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                       const float *t1, const float *lb, int64_t r, float s,
+                       float *y, hipStream_t st);
+bool gemv_ok(const DevQW &w, int64_t M);
+// out[m][j] = sum_k x[m][k] * a[j][k]  (T1 for small batches)
+hipError_t launch_dot_rows(const void *x, int x_bf16, const float *a,
+                           int64_t M, int64_t K, int64_t r, float *out,
+                           hipStream_t st);
+
+// ---- k_elem.hip ----
+hipError_t launch_axpy_inplace(float *y, const float *x, int64_t n,
+                               hipStream_t s);  // y += x
+hipError_t launch_bf16_to_f32(const uint16_t *x, float *y, int64_t n,
+                              hipStream_t s);
+
+// ---- k_adam.hip ----
+struct AdamTensor {
+  float *p;
+  const float *g;
+  uint8_t *m_codes, *v_codes;
+  float *m_scales, *v_scales;
+  int64_t numel, nblocks, block_offset;  // block_offset: prefix over tensors
+  float b1t, b2t;
+};
+hipError_t launch_adam(const AdamTensor *d_tensors, int ntensors,
+                       int64_t total_blocks, int64_t block_size, float lr,
+                       float beta1, float beta2, float eps, hipStream_t s);
+
+}  // namespace qh

@@ -1,0 +1,1057 @@
+// runtime.cpp -- host side of the C ABI declared in include/qlora_hip.h.
+//
+// Context and stream management, argument validation with the reference's
+// accept/reject rules and messages, staging of host slices, choice of
+// kernel per shape, and the 8-bit Adam state that lives in HBM.
+#include "qlora_hip.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "qh_internal.h"
+
+using qh::DevQW;
+using qh::GemmArgs;
+using qh::Operand;
+
+namespace {
+
+thread_local std::string g_err;
+
+qh_status fail(qh_status st, const std::string &msg) {
+  // Display formats of QloraError (qlora-core/src/error.rs:16-24).
+  switch (st) {
+    case QH_ERR_SHAPE_MISMATCH: g_err = "shape mismatch: " + msg; break;
+    case QH_ERR_INVALID_CONFIG: g_err = "invalid config: " + msg; break;
+    case QH_ERR_GPU: g_err = "gpu error: " + msg; break;
+    default: g_err = msg; break;
+  }
+  return st;
+}
+
+std::string fmt(const char *f, ...) __attribute__((format(printf, 1, 2)));
+std::string fmt(const char *f, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, f);
+  vsnprintf(buf, sizeof buf, f, ap);
+  va_end(ap);
+  return buf;
+}
+
+struct GpuError {
+  std::string msg;
+};
+
+void check(hipError_t e, const char *what) {
+  if (e != hipSuccess) throw GpuError{std::string(what) + ": " + hipGetErrorString(e)};
+}
+
+// Growable device buffer.
+struct DevBuf {
+  void *p = nullptr;
+  size_t cap = 0;
+  void *ensure(size_t bytes) {
+    if (bytes <= cap) return p;
+    if (p) check(hipFree(p), "hipFree");
+    p = nullptr;
+    cap = 0;
+    size_t want = bytes < 256 ? 256 : bytes;
+    want = (want + 255) / 256 * 256;
+    check(hipMalloc(&p, want), "hipMalloc");
+    cap = want;
+    return p;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
+// Bump allocator over one DevBuf: sizes are laid out first, then carved.
+struct Carve {
+  std::vector<size_t> sizes;
+  size_t add(size_t bytes) {
+    sizes.push_back((bytes + 255) / 256 * 256);
+    return sizes.size() - 1;
+  }
+  size_t total() const {
+    size_t t = 0;
+    for (size_t s : sizes) t += s;
+    return t;
+  }
+  std::vector<char *> bind(DevBuf &b) {
+    char *base = (char *)b.ensure(total());
+    std::vector<char *> out;
+    for (size_t s : sizes) {
+      out.push_back(base);
+      base += s;
+    }
+    return out;
+  }
+};
+
+inline size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
+
+bool mul_overflows(size_t a, size_t b, size_t *out) {
+  return __builtin_mul_overflow(a, b, out);
+}
+
+}  // namespace
+
+struct TimedLaunch {
+  std::string name;
+  hipEvent_t start, stop;
+};
+
+struct qh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  DevBuf stage[10];  // host-API staging
+  DevBuf scratch;    // internal scratch of the fused paths
+  char name[256] = {0};
+  bool timing = false;
+  std::vector<TimedLaunch> pending;
+  std::vector<hipEvent_t> event_pool;
+  std::map<std::string, std::pair<uint64_t, double>> totals;
+};
+
+namespace {
+
+hipEvent_t take_event(qh_ctx *c) {
+  if (!c->event_pool.empty()) {
+    hipEvent_t e = c->event_pool.back();
+    c->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  check(hipEventCreate(&e), "hipEventCreate");
+  return e;
+}
+
+// Brackets one kernel launch with events on its stream while timing is on.
+struct Timed {
+  qh_ctx *c;
+  const char *name;
+  hipStream_t s;
+  hipEvent_t a = nullptr, b = nullptr;
+  Timed(qh_ctx *ctx, const char *n, hipStream_t st) : c(ctx), name(n), s(st) {
+    if (!c->timing) return;
+    a = take_event(c);
+    b = take_event(c);
+    check(hipEventRecord(a, s), "hipEventRecord");
+  }
+  ~Timed() {
+    if (!a) return;
+    if (hipEventRecord(b, s) == hipSuccess) c->pending.push_back({name, a, b});
+  }
+};
+
+template <class F>
+void timed(qh_ctx *c, const char *name, hipStream_t s, F &&f) {
+  Timed t(c, name, s);
+  check(f(), name);
+}
+
+void drain_timing(qh_ctx *c) {
+  for (auto &t : c->pending) {
+    check(hipEventSynchronize(t.stop), "hipEventSynchronize");
+    float ms = 0.0f;
+    check(hipEventElapsedTime(&ms, t.start, t.stop), "hipEventElapsedTime");
+    auto &slot = c->totals[t.name];
+    slot.first += 1;
+    slot.second += ms;
+    c->event_pool.push_back(t.start);
+    c->event_pool.push_back(t.stop);
+  }
+  c->pending.clear();
+}
+
+}  // namespace
+
+struct ParamStateDev {
+  size_t numel = 0, nb = 0;
+  uint8_t *m_codes = nullptr, *v_codes = nullptr;
+  float *m_scales = nullptr, *v_scales = nullptr;
+  uint64_t step = 0;
+};
+
+struct qh_adam8bit {
+  qh_ctx *ctx;
+  qh_adam_config cfg;
+  std::vector<ParamStateDev> states;
+  DevBuf stage_p, stage_g;
+};
+
+namespace {
+
+hipStream_t pick_stream(qh_ctx *ctx, void *stream) {
+  return stream ? (hipStream_t)stream : ctx->stream;
+}
+
+DevQW make_devqw(const qh_qweight &w) {
+  DevQW d;
+  d.rows = (int64_t)w.rows;
+  d.cols = (int64_t)w.cols;
+  d.n = (int64_t)(w.rows * w.cols);
+  d.bs = (int64_t)w.block_size;
+  d.nb = w.block_size ? (d.n + d.bs - 1) / d.bs : 0;
+  d.codes = w.codes;
+  d.kind = w.scale_kind;
+  d.scales = w.scales;
+  d.scale_codes = w.scale_codes;
+  d.absmax = w.absmax;
+  return d;
+}
+
+// QuantizedTensor invariants (quant.rs:171-207): block_size > 0 and no
+// rows*cols overflow; the scale kind must be one of the two stores.
+qh_status validate_weight(const qh_qweight *w) {
+  if (!w) return fail(QH_ERR_SHAPE_MISMATCH, "weight descriptor is NULL");
+  if (w->block_size == 0)
+    return fail(QH_ERR_INVALID_CONFIG, "block_size must be > 0");
+  size_t n;
+  if (mul_overflows(w->rows, w->cols, &n))
+    return fail(QH_ERR_INVALID_CONFIG, "rows*cols overflow");
+  if (w->scale_kind != QH_SCALES_F32 && w->scale_kind != QH_SCALES_DQ_INT8)
+    return fail(QH_ERR_INVALID_CONFIG, "unknown scale kind");
+  return QH_OK;
+}
+
+// LoraAdapter::new (lora.rs:28-61) against the layer's dims.
+qh_status validate_lora(const qh_lora *l, size_t in_dim, size_t out_dim) {
+  if (!l) return QH_OK;
+  if (l->r == 0) return fail(QH_ERR_INVALID_CONFIG, "rank r must be > 0");
+  if (l->a_len != l->r * in_dim)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("a.len() = %zu but r*in_dim = %zu", l->a_len, l->r * in_dim));
+  if (l->b_len != out_dim * l->r)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("b.len() = %zu but out_dim*r = %zu", l->b_len, out_dim * l->r));
+  return QH_OK;
+}
+
+// Scale kind and pointer for one weight: upload to staging for host calls.
+size_t scale_bytes(const qh_qweight &w, size_t *am_bytes) {
+  size_t n = w.rows * w.cols;
+  size_t nb = div_ceil(n, w.block_size);
+  if (w.scale_kind == QH_SCALES_F32) {
+    *am_bytes = 0;
+    return nb * 4;
+  }
+  *am_bytes = div_ceil(nb, 256) * 4;
+  return nb;
+}
+
+// Copies a host weight into device staging buffers and returns a device
+// view of it.
+DevQW upload_weight(qh_ctx *ctx, const qh_qweight &w, int slot, hipStream_t s) {
+  size_t n = w.rows * w.cols;
+  size_t cb = div_ceil(n, 2), amb = 0;
+  size_t sb = scale_bytes(w, &amb);
+  Carve c;
+  size_t ic = c.add(cb + 16), is = c.add(sb + 16), ia = c.add(amb + 16);
+  auto p = c.bind(ctx->stage[slot]);
+  if (cb) check(hipMemcpyAsync(p[ic], w.codes, cb, hipMemcpyHostToDevice, s), "upload codes");
+  qh_qweight d = w;
+  d.codes = (const uint8_t *)p[ic];
+  if (w.scale_kind == QH_SCALES_F32) {
+    if (sb) check(hipMemcpyAsync(p[is], w.scales, sb, hipMemcpyHostToDevice, s), "upload scales");
+    d.scales = (const float *)p[is];
+  } else {
+    if (sb) check(hipMemcpyAsync(p[is], w.scale_codes, sb, hipMemcpyHostToDevice, s), "upload scale codes");
+    if (amb) check(hipMemcpyAsync(p[ia], w.absmax, amb, hipMemcpyHostToDevice, s), "upload absmax");
+    d.scale_codes = (const uint8_t *)p[is];
+    d.absmax = (const float *)p[ia];
+  }
+  return make_devqw(d);
+}
+
+float *upload_f32(qh_ctx *ctx, int slot, const float *h, size_t n, hipStream_t s) {
+  float *d = (float *)ctx->stage[slot].ensure(n * 4 + 16);
+  if (n) check(hipMemcpyAsync(d, h, n * 4, hipMemcpyHostToDevice, s), "upload");
+  return d;
+}
+
+float *alloc_f32(qh_ctx *ctx, int slot, size_t n) {
+  return (float *)ctx->stage[slot].ensure(n * 4 + 16);
+}
+
+void download_f32(float *h, const float *d, size_t n, hipStream_t s) {
+  if (n) check(hipMemcpyAsync(h, d, n * 4, hipMemcpyDeviceToHost, s), "download");
+}
+
+Operand op(const void *p, int64_t ld, int form, int elem, float scale = 1.0f) {
+  Operand o;
+  o.p = p;
+  o.ld = ld;
+  o.form = form;
+  o.elem = elem;
+  o.scale = scale;
+  return o;
+}
+
+GemmArgs gemm_args(int64_t M, int64_t N, int64_t K, Operand A, Operand B,
+                   float *C, int64_t ldc, float alpha) {
+  GemmArgs g;
+  std::memset(&g, 0, sizeof g);
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.A = A;
+  g.B = B;
+  g.C = C;
+  g.ldc = ldc;
+  g.alpha = alpha;
+  g.splits = 1;
+  g.K2 = 0;
+  g.A2 = op(nullptr, 0, qh::ROWK, qh::E_F32);
+  g.B2 = op(nullptr, 0, qh::ROWK, qh::E_F32);
+  return g;
+}
+
+// Split-K factor for outputs that cover too few tiles to fill 256 CUs.
+int choose_splits(int64_t M, int64_t N, int64_t K) {
+  int64_t tiles = div_ceil(M, 64) * div_ceil(N, 64);
+  if (M >= 128 && N >= 128 && (M / 128) * (N / 128) >= 64) return 1;
+  if (tiles >= 256) return 1;
+  int64_t sp = 512 / (tiles ? tiles : 1);
+  if (sp > 32) sp = 32;
+  int64_t kmax = K / 256;
+  if (sp > kmax) sp = kmax;
+  return sp < 1 ? 1 : (int)sp;
+}
+
+size_t partial_floats(const GemmArgs &g) {
+  return g.splits > 1 ? (size_t)g.splits * g.M * g.N : 0;
+}
+
+// ---- fused forward on device pointers -----------------------------------
+void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
+                 int xdt, size_t batch, float *y, float *t1_out, hipStream_t s) {
+  const int64_t M = (int64_t)batch, N = W.rows, K = W.cols;
+  if (M == 0 || N == 0) return;
+  const bool lora = l != nullptr;
+  const int64_t r = lora ? (int64_t)l->r : 0;
+  const float sc = lora ? l->alpha / (float)l->r : 0.0f;  // lora.rs:64-66
+  const int xe = xdt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
+  const bool fast = qh::nf4_fast_ok(W);
+  const bool gemv = qh::gemv_ok(W, M);
+
+  GemmArgs gt1{}, gm{};
+  if (lora) {
+    gt1 = gemm_args(M, r, K, op(x, K, qh::ROWK, xe), op(l->a, K, qh::ROWK, qh::E_F32),
+                    nullptr, r, 1.0f);
+    gt1.splits = choose_splits(M, r, K);
+  }
+  Carve c;
+  size_t i_t1 = c.add(lora && !t1_out ? (size_t)M * r * 4 : 0);
+  size_t i_w32 = c.add(fast ? 0 : (size_t)W.n * 4);
+  size_t i_p1 = c.add(lora && !gemv ? partial_floats(gt1) * 4 : 0);
+  size_t i_p2 = c.add(0);
+  auto p = c.bind(ctx->scratch);
+  float *t1 = lora ? (t1_out ? t1_out : (float *)p[i_t1]) : nullptr;
+
+  if (gemv) {
+    if (lora) timed(ctx, "t1", s, [&] { return qh::launch_dot_rows(x, xe == qh::E_BF16, l->a, M, K, r, t1, s); });
+    timed(ctx, "gemv", s, [&] { return qh::launch_gemv(W, x, xe == qh::E_BF16, M, t1, lora ? l->b : nullptr, r, sc, y, s); });
+    return;
+  }
+  if (lora) {
+    gt1.C = t1;
+    timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(gt1, (float *)p[i_p1], s); });
+  }
+  Operand B;
+  DevQW qw = W;
+  if (fast) {
+    B = op(W.codes, K, qh::ROWK, qh::E_NF4);
+  } else {
+    float *w32 = (float *)p[i_w32];
+    timed(ctx, "dequantize", s, [&] { return qh::launch_dequantize(W, w32, s); });
+    B = op(w32, K, qh::ROWK, qh::E_F32);
+  }
+  gm = gemm_args(M, N, K, op(x, K, qh::ROWK, xe), B, y, N, 1.0f);
+  gm.qw = qw;
+  if (lora) {
+    gm.K2 = r;
+    gm.A2 = op(t1, r, qh::ROWK, qh::E_F32);
+    gm.B2 = op(l->b, r, qh::ROWK, qh::E_F32, sc);
+  }
+  (void)i_p2;
+  timed(ctx, "forward_gemm", s, [&] { return qh::launch_gemm(gm, nullptr, s); });
+}
+
+// ---- fused backward on device pointers ----------------------------------
+void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
+                  const void *dy, int adt, size_t batch, const float *t1_in,
+                  float *gx, float *ga, float *gb, hipStream_t s) {
+  const int64_t M = (int64_t)batch, N = W.rows, K = W.cols;
+  const bool lora = l != nullptr;
+  const int64_t r = lora ? (int64_t)l->r : 0;
+  const float sc = lora ? l->alpha / (float)l->r : 0.0f;
+  const int ae = adt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
+  const bool fast = qh::nf4_fast_ok(W);
+  if (K == 0) return;
+
+  GemmArgs gt1{}, gds{}, ggb{}, gga{};
+  if (lora) {
+    gt1 = gemm_args(M, r, K, op(x, K, qh::ROWK, ae), op(l->a, K, qh::ROWK, qh::E_F32),
+                    nullptr, r, 1.0f);
+    gt1.splits = choose_splits(M, r, K);
+    // Ds = s * dY . B   (qlora.rs:143,149)
+    gds = gemm_args(M, r, N, op(dy, N, qh::ROWK, ae), op(l->b, r, qh::KROW, qh::E_F32),
+                    nullptr, r, sc);
+    gds.splits = choose_splits(M, r, N);
+    // grad_B = (s * dY)^T . T1  (qlora.rs:147)
+    ggb = gemm_args(N, r, M, op(dy, N, qh::KROW, ae), op(nullptr, r, qh::KROW, qh::E_F32),
+                    gb, r, sc);
+    ggb.splits = choose_splits(N, r, M);
+    // grad_A = Ds^T . X  (qlora.rs:151)
+    gga = gemm_args(r, K, M, op(nullptr, r, qh::KROW, qh::E_F32), op(x, K, qh::KROW, ae),
+                    ga, K, 1.0f);
+    gga.splits = choose_splits(r, K, M);
+  }
+  Carve c;
+  size_t i_t1 = c.add(lora && !t1_in ? (size_t)M * r * 4 : 0);
+  size_t i_ds = c.add(lora ? (size_t)M * r * 4 : 0);
+  size_t i_w32 = c.add(fast ? 0 : (size_t)W.n * 4);
+  size_t i_p1 = c.add(lora ? partial_floats(gt1) * 4 : 0);
+  size_t i_p2 = c.add(lora ? partial_floats(gds) * 4 : 0);
+  size_t i_p3 = c.add(lora ? partial_floats(ggb) * 4 : 0);
+  size_t i_p4 = c.add(lora ? partial_floats(gga) * 4 : 0);
+  auto p = c.bind(ctx->scratch);
+
+  const float *t1 = nullptr;
+  float *ds = nullptr;
+  if (lora) {
+    if (t1_in) {
+      t1 = t1_in;
+    } else {
+      gt1.C = (float *)p[i_t1];
+      timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(gt1, (float *)p[i_p1], s); });
+      t1 = gt1.C;
+    }
+    ds = (float *)p[i_ds];
+    gds.C = ds;
+    timed(ctx, "ds_gemm", s, [&] { return qh::launch_gemm(gds, (float *)p[i_p2], s); });
+    if (M > 0) {
+      ggb.B.p = t1;
+      timed(ctx, "grad_b_gemm", s, [&] { return qh::launch_gemm(ggb, (float *)p[i_p3], s); });
+      gga.A.p = ds;
+      timed(ctx, "grad_a_gemm", s, [&] { return qh::launch_gemm(gga, (float *)p[i_p4], s); });
+    } else {
+      check(hipMemsetAsync(gb, 0, (size_t)N * r * 4, s), "memset");
+      check(hipMemsetAsync(ga, 0, (size_t)r * K * 4, s), "memset");
+    }
+  }
+  if (M == 0) return;
+  Operand B;
+  if (fast) {
+    B = op(W.codes, K, qh::KROW, qh::E_NF4);
+  } else {
+    float *w32 = (float *)p[i_w32];
+    timed(ctx, "dequantize", s, [&] { return qh::launch_dequantize(W, w32, s); });
+    B = op(w32, K, qh::KROW, qh::E_F32);
+  }
+  GemmArgs gm = gemm_args(M, K, N, op(dy, N, qh::ROWK, ae), B, gx, K, 1.0f);
+  gm.qw = W;
+  if (lora) {
+    gm.K2 = r;
+    gm.A2 = op(ds, r, qh::ROWK, qh::E_F32);
+    gm.B2 = op(l->a, K, qh::KROW, qh::E_F32);
+  }
+  timed(ctx, "grad_x_gemm", s, [&] { return qh::launch_gemm(gm, nullptr, s); });
+}
+
+// Plain GEMMs (gpu_matmul*): C = A.B, A^T.B, A.B^T.
+void matmul_dev(qh_ctx *ctx, int opk, const float *a, const float *b, size_t m,
+                size_t k, size_t n, float *c, hipStream_t s) {
+  GemmArgs g;
+  if (opk == QH_MM_NN) {
+    g = gemm_args(m, n, k, op(a, k, qh::ROWK, qh::E_F32), op(b, n, qh::KROW, qh::E_F32), c, n, 1.0f);
+  } else if (opk == QH_MM_NT) {
+    g = gemm_args(m, n, k, op(a, k, qh::ROWK, qh::E_F32), op(b, k, qh::ROWK, qh::E_F32), c, n, 1.0f);
+  } else {
+    // C(k x n) = A(m x k)^T B(m x n): rows of C index A's columns.
+    g = gemm_args(k, n, m, op(a, k, qh::KROW, qh::E_F32), op(b, n, qh::KROW, qh::E_F32), c, n, 1.0f);
+  }
+  g.splits = choose_splits(g.M, g.N, g.K);
+  Carve cv;
+  size_t ip = cv.add(partial_floats(g) * 4);
+  auto p = cv.bind(ctx->scratch);
+  timed(ctx, "matmul", s, [&] { return qh::launch_gemm(g, (float *)p[ip], s); });
+}
+
+template <class F>
+qh_status guarded(qh_ctx *ctx, F &&f) {
+  if (!ctx) return fail(QH_ERR_GPU, "context is NULL");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  try {
+    check(hipSetDevice(ctx->device), "hipSetDevice");
+    return f();
+  } catch (const GpuError &e) {
+    return fail(QH_ERR_GPU, e.msg);
+  } catch (const std::bad_alloc &) {
+    return fail(QH_ERR_GPU, "host allocation failed");
+  } catch (...) {
+    return fail(QH_ERR_GPU, "unexpected failure");
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+uint32_t qh_abi_version(void) { return QH_ABI_VERSION; }
+
+const char *qh_last_error(void) { return g_err.c_str(); }
+
+qh_status qh_ctx_create(qh_ctx **out) {
+  if (!out) return fail(QH_ERR_GPU, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e == hipErrorNoDevice || (e == hipSuccess && n == 0) ||
+      e == hipErrorInsufficientDriver) {
+    (void)hipGetLastError();
+    return fail(QH_NO_DEVICE, "no GPU device is visible");
+  }
+  if (e != hipSuccess) return fail(QH_ERR_GPU, hipGetErrorString(e));
+  qh_ctx *c = new (std::nothrow) qh_ctx();
+  if (!c) return fail(QH_ERR_GPU, "host allocation failed");
+  if (hipGetDevice(&c->device) != hipSuccess) c->device = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, c->device) == hipSuccess)
+    snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+  if ((e = hipSetDevice(c->device)) != hipSuccess ||
+      (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+    delete c;
+    return fail(QH_ERR_GPU, hipGetErrorString(e));
+  }
+  *out = c;
+  return QH_OK;
+}
+
+void qh_ctx_destroy(qh_ctx *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+  }
+  for (auto &b : ctx->stage) b.release();
+  ctx->scratch.release();
+  delete ctx;
+}
+
+qh_status qh_ctx_device_name(qh_ctx *ctx, char *buf, size_t len) {
+  if (!ctx || !buf || !len) return fail(QH_ERR_GPU, "bad arguments");
+  snprintf(buf, len, "%s", ctx->name);
+  return QH_OK;
+}
+
+qh_status qh_ctx_synchronize(qh_ctx *ctx) {
+  return guarded(ctx, [&] {
+    check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return QH_OK;
+  });
+}
+
+qh_status qh_ctx_set_timing(qh_ctx *ctx, int enable) {
+  return guarded(ctx, [&] {
+    ctx->timing = enable != 0;
+    return QH_OK;
+  });
+}
+
+qh_status qh_ctx_timing_report(qh_ctx *ctx, char *buf, size_t len, int reset) {
+  return guarded(ctx, [&] {
+    drain_timing(ctx);
+    std::string out;
+    for (const auto &kv : ctx->totals)
+      out += fmt("%s %llu %.6f\n", kv.first.c_str(), (unsigned long long)kv.second.first,
+                 kv.second.second);
+    if (buf && len) snprintf(buf, len, "%s", out.c_str());
+    if (reset) ctx->totals.clear();
+    return QH_OK;
+  });
+}
+
+size_t qh_codes_len(size_t rows, size_t cols) { return div_ceil(rows * cols, 2); }
+size_t qh_num_blocks(size_t rows, size_t cols, size_t bs) {
+  return bs ? div_ceil(rows * cols, bs) : 0;
+}
+size_t qh_num_absmax(size_t rows, size_t cols, size_t bs) {
+  return div_ceil(qh_num_blocks(rows, cols, bs), 256);
+}
+size_t qh_storage_bytes(const qh_qweight *w) {
+  if (!w || !w->block_size) return 0;
+  size_t nb = qh_num_blocks(w->rows, w->cols, w->block_size);
+  size_t sb = w->scale_kind == QH_SCALES_F32 ? nb * 4 : nb + div_ceil(nb, 256) * 4;
+  return qh_codes_len(w->rows, w->cols) + sb;
+}
+
+// ---- quantization ---------------------------------------------------------
+qh_status qh_quantize_nf4(qh_ctx *ctx, const float *w, size_t w_len,
+                          size_t rows, size_t cols, size_t block_size,
+                          int double_quant, uint8_t *codes, float *scales,
+                          uint8_t *scale_codes, float *absmax) {
+  // quant.rs:110-119: validate, overflow, then length.
+  if (block_size == 0) return fail(QH_ERR_INVALID_CONFIG, "block_size must be > 0");
+  size_t n;
+  if (mul_overflows(rows, cols, &n)) return fail(QH_ERR_INVALID_CONFIG, "rows*cols overflow");
+  if (w_len != n)
+    return fail(QH_ERR_SHAPE_MISMATCH, fmt("weights.len() = %zu but rows*cols = %zu", w_len, n));
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    const size_t nb = div_ceil(n, block_size), nsb = div_ceil(nb, 256);
+    const size_t cb = div_ceil(n, 2);
+    Carve c;
+    size_t iw = c.add(n * 4), ic = c.add(cb + 16), is = c.add(nb * 4 + 16),
+           isc = c.add(nb + 16), ia = c.add(nsb * 4 + 16), it = c.add(nb * 4 + 16);
+    auto p = c.bind(ctx->stage[0]);
+    if (n) check(hipMemcpyAsync(p[iw], w, n * 4, hipMemcpyHostToDevice, s), "upload");
+    timed(ctx, "quantize", s, [&] { return qh::launch_quantize((float *)p[iw], (int64_t)n, (int64_t)block_size,
+                              double_quant ? 1 : 0, (uint8_t *)p[ic], (float *)p[is],
+                              (uint8_t *)p[isc], (float *)p[ia], (float *)p[it], s); });
+    if (cb) check(hipMemcpyAsync(codes, p[ic], cb, hipMemcpyDeviceToHost, s), "download");
+    if (double_quant) {
+      if (nb) check(hipMemcpyAsync(scale_codes, p[isc], nb, hipMemcpyDeviceToHost, s), "download");
+      if (nsb) check(hipMemcpyAsync(absmax, p[ia], nsb * 4, hipMemcpyDeviceToHost, s), "download");
+    } else if (nb) {
+      check(hipMemcpyAsync(scales, p[is], nb * 4, hipMemcpyDeviceToHost, s), "download");
+    }
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_quantize_nf4_dev(qh_ctx *ctx, const float *d_w, size_t rows,
+                              size_t cols, size_t block_size, int double_quant,
+                              uint8_t *d_codes, float *d_scales,
+                              uint8_t *d_scale_codes, float *d_absmax,
+                              void *stream) {
+  if (block_size == 0) return fail(QH_ERR_INVALID_CONFIG, "block_size must be > 0");
+  size_t n;
+  if (mul_overflows(rows, cols, &n)) return fail(QH_ERR_INVALID_CONFIG, "rows*cols overflow");
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    float *tmp = nullptr;
+    if (double_quant && block_size != 64)
+      tmp = (float *)ctx->scratch.ensure(div_ceil(n, block_size) * 4 + 16);
+    timed(ctx, "quantize", s, [&] { return qh::launch_quantize(d_w, (int64_t)n, (int64_t)block_size, double_quant ? 1 : 0,
+                              d_codes, d_scales, d_scale_codes, d_absmax, tmp, s); });
+    return QH_OK;
+  });
+}
+
+qh_status qh_block_scales(qh_ctx *ctx, const qh_qweight *w, float *out) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    DevQW d = upload_weight(ctx, *w, 0, s);
+    float *o = alloc_f32(ctx, 1, (size_t)d.nb);
+    timed(ctx, "block_scales", s, [&] { return qh::launch_block_scales(d, o, s); });
+    download_f32(out, o, (size_t)d.nb, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_dequantize(qh_ctx *ctx, const qh_qweight *w, float *out) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    DevQW d = upload_weight(ctx, *w, 0, s);
+    float *o = alloc_f32(ctx, 1, (size_t)d.n);
+    timed(ctx, "dequantize", s, [&] { return qh::launch_dequantize(d, o, s); });
+    download_f32(out, o, (size_t)d.n, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_dequantize_dev(qh_ctx *ctx, const qh_qweight *w, float *d_out,
+                            void *stream) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    timed(ctx, "dequantize", s, [&] { return qh::launch_dequantize(make_devqw(*w), d_out, s); });
+    return QH_OK;
+  });
+}
+
+// ---- GEMMs ------------------------------------------------------------------
+static qh_status matmul_host(qh_ctx *ctx, int opk, const char *name,
+                             const float *a, size_t a_len, const float *b,
+                             size_t b_len, size_t m, size_t k, size_t n,
+                             float *c) {
+  // kernels.rs:151-160 (NN, NT) and :231-240 (TN): empty output first,
+  // then the length check.
+  size_t out_len;
+  if (opk == QH_MM_TN) {
+    if (k == 0 || n == 0) return QH_OK;
+    if (a_len != m * k || b_len != m * n)
+      return fail(QH_ERR_SHAPE_MISMATCH,
+                  fmt("%s: a.len() = %zu, b.len() = %zu, expected %zu*%zu and %zu*%zu",
+                      name, a_len, b_len, m, k, m, n));
+    out_len = k * n;
+  } else {
+    if (m == 0 || n == 0) return QH_OK;
+    size_t bl = opk == QH_MM_NN ? k * n : n * k;
+    if (a_len != m * k || b_len != bl)
+      return fail(QH_ERR_SHAPE_MISMATCH,
+                  opk == QH_MM_NN
+                      ? fmt("%s: a.len() = %zu, b.len() = %zu, expected %zu*%zu and %zu*%zu",
+                            name, a_len, b_len, m, k, k, n)
+                      : fmt("%s: a.len() = %zu, b.len() = %zu, expected %zu*%zu and %zu*%zu",
+                            name, a_len, b_len, m, k, n, k));
+    out_len = m * n;
+  }
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    float *da = upload_f32(ctx, 0, a, a_len, s);
+    float *db = upload_f32(ctx, 1, b, b_len, s);
+    float *dc = alloc_f32(ctx, 2, out_len);
+    matmul_dev(ctx, opk, da, db, m, k, n, dc, s);
+    download_f32(c, dc, out_len, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_matmul(qh_ctx *ctx, const float *a, size_t a_len, const float *b,
+                    size_t b_len, size_t m, size_t k, size_t n, float *c) {
+  return matmul_host(ctx, QH_MM_NN, "gpu_matmul", a, a_len, b, b_len, m, k, n, c);
+}
+qh_status qh_matmul_trans_a(qh_ctx *ctx, const float *a, size_t a_len,
+                            const float *b, size_t b_len, size_t m, size_t k,
+                            size_t n, float *c) {
+  return matmul_host(ctx, QH_MM_TN, "gpu_matmul_trans_a", a, a_len, b, b_len, m, k, n, c);
+}
+qh_status qh_matmul_trans_b(qh_ctx *ctx, const float *a, size_t a_len,
+                            const float *b, size_t b_len, size_t m, size_t k,
+                            size_t n, float *c) {
+  return matmul_host(ctx, QH_MM_NT, "gpu_matmul_trans_b", a, a_len, b, b_len, m, k, n, c);
+}
+
+qh_status qh_matmul_dev(qh_ctx *ctx, int opk, const float *d_a, const float *d_b,
+                        size_t m, size_t k, size_t n, float *d_c, void *stream) {
+  if (opk != QH_MM_NN && opk != QH_MM_NT && opk != QH_MM_TN)
+    return fail(QH_ERR_INVALID_CONFIG, "unknown matmul op");
+  return guarded(ctx, [&] {
+    matmul_dev(ctx, opk, d_a, d_b, m, k, n, d_c, pick_stream(ctx, stream));
+    return QH_OK;
+  });
+}
+
+// ---- the layer ------------------------------------------------------------------
+qh_status qh_qlora_forward(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
+                           const float *x, size_t x_len, size_t batch, float *y) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  const size_t in_dim = w->cols, out_dim = w->rows;
+  if ((st = validate_lora(lora, in_dim, out_dim)) != QH_OK) return st;
+  if (x_len != batch * in_dim)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("x.len() = %zu but batch*in_dim = %zu", x_len, batch * in_dim));
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    DevQW d = upload_weight(ctx, *w, 0, s);
+    float *dx = upload_f32(ctx, 1, x, x_len, s);
+    float *dy = alloc_f32(ctx, 2, batch * out_dim);
+    qh_lora dl{};
+    if (lora) {
+      dl = *lora;
+      dl.a = upload_f32(ctx, 3, lora->a, lora->a_len, s);
+      dl.b = upload_f32(ctx, 4, lora->b, lora->b_len, s);
+    }
+    forward_dev(ctx, d, lora ? &dl : nullptr, dx, QH_F32, batch, dy, nullptr, s);
+    download_f32(y, dy, batch * out_dim, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_qlora_backward(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
+                            const float *x, size_t x_len, const float *dy,
+                            size_t dy_len, size_t batch, float *grad_x,
+                            float *grad_a, float *grad_b) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  const size_t in_dim = w->cols, out_dim = w->rows;
+  if ((st = validate_lora(lora, in_dim, out_dim)) != QH_OK) return st;
+  // qlora.rs:119-132
+  if (x_len != batch * in_dim)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("x.len() = %zu but batch*in_dim = %zu", x_len, batch * in_dim));
+  if (dy_len != batch * out_dim)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("dy.len() = %zu but batch*out_dim = %zu", dy_len, batch * out_dim));
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    DevQW d = upload_weight(ctx, *w, 0, s);
+    float *dx = upload_f32(ctx, 1, x, x_len, s);
+    float *ddy = upload_f32(ctx, 2, dy, dy_len, s);
+    float *dgx = alloc_f32(ctx, 5, batch * in_dim);
+    qh_lora dl{};
+    float *dga = nullptr, *dgb = nullptr;
+    if (lora) {
+      dl = *lora;
+      dl.a = upload_f32(ctx, 3, lora->a, lora->a_len, s);
+      dl.b = upload_f32(ctx, 4, lora->b, lora->b_len, s);
+      dga = alloc_f32(ctx, 6, lora->r * in_dim);
+      dgb = alloc_f32(ctx, 7, out_dim * lora->r);
+    }
+    backward_dev(ctx, d, lora ? &dl : nullptr, dx, ddy, QH_F32, batch, nullptr, dgx, dga,
+                 dgb, s);
+    download_f32(grad_x, dgx, batch * in_dim, s);
+    if (lora) {
+      download_f32(grad_a, dga, lora->r * in_dim, s);
+      download_f32(grad_b, dgb, out_dim * lora->r, s);
+    }
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
+                               const void *d_x, int x_dtype, size_t batch, float *d_y,
+                               float *d_t1, void *stream) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  if ((st = validate_lora(lora, w->cols, w->rows)) != QH_OK) return st;
+  if (x_dtype != QH_F32 && x_dtype != QH_BF16)
+    return fail(QH_ERR_INVALID_CONFIG, "x_dtype must be QH_F32 or QH_BF16");
+  return guarded(ctx, [&] {
+    forward_dev(ctx, make_devqw(*w), lora, d_x, x_dtype, batch, d_y, d_t1,
+                pick_stream(ctx, stream));
+    return QH_OK;
+  });
+}
+
+qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
+                                const void *d_x, const void *d_dy, int act_dtype,
+                                size_t batch, const float *d_t1, float *d_grad_x,
+                                float *d_grad_a, float *d_grad_b, void *stream) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  if ((st = validate_lora(lora, w->cols, w->rows)) != QH_OK) return st;
+  if (act_dtype != QH_F32 && act_dtype != QH_BF16)
+    return fail(QH_ERR_INVALID_CONFIG, "act_dtype must be QH_F32 or QH_BF16");
+  return guarded(ctx, [&] {
+    backward_dev(ctx, make_devqw(*w), lora, d_x, d_dy, act_dtype, batch, d_t1, d_grad_x,
+                 d_grad_a, d_grad_b, pick_stream(ctx, stream));
+    return QH_OK;
+  });
+}
+
+// ---- Adam -------------------------------------------------------------------
+void qh_adam_config_default(qh_adam_config *cfg) {
+  if (!cfg) return;
+  cfg->lr = 1e-3f;
+  cfg->beta1 = 0.9f;
+  cfg->beta2 = 0.999f;
+  cfg->eps = 1e-8f;
+  cfg->block_size = 256;
+  cfg->max_resident_pages = SIZE_MAX;
+}
+
+qh_status qh_adam8bit_create(qh_ctx *ctx, const qh_adam_config *cfg,
+                             qh_adam8bit **out) {
+  if (!out || !cfg) return fail(QH_ERR_INVALID_CONFIG, "NULL argument");
+  *out = nullptr;
+  // optim.rs:63-80
+  if (cfg->lr <= 0.0f || !std::isfinite(cfg->lr))
+    return fail(QH_ERR_INVALID_CONFIG, "lr must be positive and finite");
+  if (!(cfg->beta1 >= 0.0f && cfg->beta1 < 1.0f) || !(cfg->beta2 >= 0.0f && cfg->beta2 < 1.0f))
+    return fail(QH_ERR_INVALID_CONFIG, "betas must be in (0, 1)");
+  if (cfg->block_size == 0 || cfg->max_resident_pages == 0)
+    return fail(QH_ERR_INVALID_CONFIG, "block_size and max_resident_pages must be > 0");
+  if (cfg->block_size > 8192)
+    return fail(QH_ERR_INVALID_CONFIG,
+                "block_size > 8192 exceeds the GPU kernel's LDS staging");
+  if (!ctx) return fail(QH_ERR_GPU, "context is NULL");
+  qh_adam8bit *o = new (std::nothrow) qh_adam8bit();
+  if (!o) return fail(QH_ERR_GPU, "host allocation failed");
+  o->ctx = ctx;
+  o->cfg = *cfg;
+  *out = o;
+  return QH_OK;
+}
+
+static void free_state(ParamStateDev &st) {
+  if (st.m_codes) (void)hipFree(st.m_codes);
+  if (st.v_codes) (void)hipFree(st.v_codes);
+  if (st.m_scales) (void)hipFree(st.m_scales);
+  if (st.v_scales) (void)hipFree(st.v_scales);
+  st = ParamStateDev();
+}
+
+void qh_adam8bit_destroy(qh_adam8bit *o) {
+  if (!o) return;
+  (void)hipSetDevice(o->ctx->device);
+  (void)hipStreamSynchronize(o->ctx->stream);
+  for (auto &st : o->states) free_state(st);
+  o->stage_p.release();
+  o->stage_g.release();
+  delete o;
+}
+
+static void init_state(ParamStateDev &st, size_t numel, size_t bs, hipStream_t s) {
+  free_state(st);
+  st.numel = numel;
+  st.nb = div_ceil(numel, bs);
+  check(hipMalloc(&st.m_codes, numel + 16), "hipMalloc");
+  check(hipMalloc(&st.v_codes, numel + 16), "hipMalloc");
+  check(hipMalloc(&st.m_scales, st.nb * 4 + 16), "hipMalloc");
+  check(hipMalloc(&st.v_scales, st.nb * 4 + 16), "hipMalloc");
+  check(hipMemsetAsync(st.m_codes, 0, numel + 16, s), "memset");
+  check(hipMemsetAsync(st.v_codes, 0, numel + 16, s), "memset");
+  check(hipMemsetAsync(st.m_scales, 0, st.nb * 4 + 16, s), "memset");
+  check(hipMemsetAsync(st.v_scales, 0, st.nb * 4 + 16, s), "memset");
+  st.step = 0;
+}
+
+// Adam8bit::step (optim.rs:164-199): tensors before the first length
+// mismatch are stepped, then the mismatch is reported.
+static qh_status adam_step_core(qh_adam8bit *o, float *const *d_params,
+                                const float *const *d_grads, const size_t *lens,
+                                size_t count, size_t mismatch_at,
+                                qh_adam_stats *stats, hipStream_t s) {
+  const qh_adam_config &c = o->cfg;
+  std::vector<qh::AdamTensor> ts;
+  size_t pages = 0;
+  int64_t blocks = 0;
+  for (size_t i = 0; i < count && i < mismatch_at; ++i) {
+    if (o->states.size() <= i) o->states.emplace_back();
+    ParamStateDev &st = o->states[i];
+    if (st.m_codes == nullptr || st.numel != lens[i]) init_state(st, lens[i], c.block_size, s);
+    st.step += 1;
+    const float t = (float)st.step;
+    qh::AdamTensor at;
+    at.p = d_params[i];
+    at.g = d_grads[i];
+    at.m_codes = st.m_codes;
+    at.v_codes = st.v_codes;
+    at.m_scales = st.m_scales;
+    at.v_scales = st.v_scales;
+    at.numel = (int64_t)st.numel;
+    at.nblocks = (int64_t)st.nb;
+    at.block_offset = blocks;
+    at.b1t = 1.0f - powf(c.beta1, t);  // optim.rs:209-210
+    at.b2t = 1.0f - powf(c.beta2, t);
+    blocks += at.nblocks;
+    pages += st.nb;
+    ts.push_back(at);
+  }
+  if (!ts.empty())
+    timed(o->ctx, "adam", s, [&] {
+      return qh::launch_adam(ts.data(), (int)ts.size(), blocks, (int64_t)c.block_size,
+                             c.lr, c.beta1, c.beta2, c.eps, s);
+    });
+  if (stats) {
+    stats->pages_streamed = pages;
+    stats->state_bytes = qh_adam8bit_state_bytes(o);
+  }
+  return QH_OK;
+}
+
+qh_status qh_adam8bit_step(qh_adam8bit *o, float *const *params,
+                           const size_t *param_lens, const float *const *grads,
+                           const size_t *grad_lens, size_t count,
+                           qh_adam_stats *stats) {
+  if (!o) return fail(QH_ERR_INVALID_CONFIG, "optimizer is NULL");
+  size_t mismatch = count;
+  for (size_t i = 0; i < count; ++i)
+    if (param_lens[i] != grad_lens[i]) {
+      mismatch = i;
+      break;
+    }
+  qh_ctx *ctx = o->ctx;
+  qh_status st = guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    size_t tot = 0;
+    for (size_t i = 0; i < mismatch; ++i) tot += param_lens[i];
+    float *dp = (float *)o->stage_p.ensure(tot * 4 + 16);
+    float *dg = (float *)o->stage_g.ensure(tot * 4 + 16);
+    std::vector<float *> pp(mismatch);
+    std::vector<const float *> gp(mismatch);
+    size_t off = 0;
+    for (size_t i = 0; i < mismatch; ++i) {
+      pp[i] = dp + off;
+      gp[i] = dg + off;
+      if (param_lens[i]) {
+        check(hipMemcpyAsync(pp[i], params[i], param_lens[i] * 4, hipMemcpyHostToDevice, s), "upload");
+        check(hipMemcpyAsync((void *)gp[i], grads[i], param_lens[i] * 4, hipMemcpyHostToDevice, s), "upload");
+      }
+      off += (param_lens[i] + 3) / 4 * 4;
+    }
+    adam_step_core(o, pp.data(), gp.data(), param_lens, mismatch, mismatch, stats, s);
+    for (size_t i = 0; i < mismatch; ++i)
+      if (param_lens[i])
+        check(hipMemcpyAsync(params[i], pp[i], param_lens[i] * 4, hipMemcpyDeviceToHost, s), "download");
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+  if (st != QH_OK) return st;
+  if (mismatch < count)
+    return fail(QH_ERR_SHAPE_MISMATCH, fmt("param %zu: len = %zu but grad len = %zu", mismatch,
+                                           param_lens[mismatch], grad_lens[mismatch]));
+  return QH_OK;
+}
+
+qh_status qh_adam8bit_step_dev(qh_adam8bit *o, float *const *d_params,
+                               const float *const *d_grads, const size_t *lens,
+                               size_t count, qh_adam_stats *stats, void *stream) {
+  if (!o) return fail(QH_ERR_INVALID_CONFIG, "optimizer is NULL");
+  qh_ctx *ctx = o->ctx;
+  return guarded(ctx, [&] {
+    return adam_step_core(o, d_params, d_grads, lens, count, count, stats,
+                          pick_stream(ctx, stream));
+  });
+}
+
+size_t qh_adam8bit_state_bytes(const qh_adam8bit *o) {
+  // optim.rs:128-131: m and v codes plus 4-byte scales for both.
+  if (!o) return 0;
+  size_t t = 0;
+  for (const auto &st : o->states) t += 2 * st.numel + 2 * st.nb * 4;
+  return t;
+}
+
+qh_status qh_adam8bit_get_state(qh_adam8bit *o, size_t idx, uint8_t *m_codes,
+                                float *m_scales, uint8_t *v_codes, float *v_scales,
+                                uint64_t *step) {
+  if (!o) return fail(QH_ERR_INVALID_CONFIG, "optimizer is NULL");
+  if (idx >= o->states.size()) return fail(QH_ERR_SHAPE_MISMATCH, "no state at this index");
+  qh_ctx *ctx = o->ctx;
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    const ParamStateDev &st = o->states[idx];
+    check(hipStreamSynchronize(s), "sync");
+    if (st.numel) {
+      check(hipMemcpy(m_codes, st.m_codes, st.numel, hipMemcpyDeviceToHost), "download");
+      check(hipMemcpy(v_codes, st.v_codes, st.numel, hipMemcpyDeviceToHost), "download");
+      check(hipMemcpy(m_scales, st.m_scales, st.nb * 4, hipMemcpyDeviceToHost), "download");
+      check(hipMemcpy(v_scales, st.v_scales, st.nb * 4, hipMemcpyDeviceToHost), "download");
+    }
+    if (step) *step = st.step;
+    return QH_OK;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,201 @@
+"""ctypes binding of libqlora_hip.so (include/qlora_hip.h).
+
+Loads the in-tree library built by ``vkqlora.rs_amd/build_lib.py``.  There is
+no CPU fallback: if the library is missing, or no GPU is visible when a
+context is created, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqlora_hip.so")
+
+QH_OK = 0
+QH_ERR_SHAPE_MISMATCH = 1
+QH_ERR_INVALID_CONFIG = 2
+QH_ERR_GPU = 3
+QH_NO_DEVICE = 4
+
+QH_SCALES_F32 = 0
+QH_SCALES_DQ_INT8 = 1
+QH_F32 = 0
+QH_BF16 = 1
+QH_MM_NN, QH_MM_TN, QH_MM_NT = 0, 1, 2
+
+EXPORTED = [
+    "qh_abi_version", "qh_ctx_create", "qh_ctx_destroy", "qh_last_error",
+    "qh_ctx_device_name", "qh_ctx_synchronize", "qh_ctx_set_timing",
+    "qh_ctx_timing_report", "qh_codes_len", "qh_num_blocks",
+    "qh_num_absmax", "qh_storage_bytes", "qh_quantize_nf4", "qh_block_scales",
+    "qh_dequantize", "qh_matmul", "qh_matmul_trans_a", "qh_matmul_trans_b",
+    "qh_qlora_forward", "qh_qlora_backward", "qh_adam_config_default",
+    "qh_adam8bit_create", "qh_adam8bit_destroy", "qh_adam8bit_step",
+    "qh_adam8bit_step_dev", "qh_adam8bit_state_bytes", "qh_adam8bit_get_state",
+    "qh_quantize_nf4_dev", "qh_dequantize_dev", "qh_matmul_dev",
+    "qh_qlora_forward_dev", "qh_qlora_backward_dev",
+]
+
+
+class QWeight(C.Structure):
+    _fields_ = [("rows", C.c_size_t), ("cols", C.c_size_t),
+                ("block_size", C.c_size_t), ("codes", C.c_void_p),
+                ("scale_kind", C.c_int32), ("scales", C.c_void_p),
+                ("scale_codes", C.c_void_p), ("absmax", C.c_void_p)]
+
+
+class Lora(C.Structure):
+    _fields_ = [("a", C.c_void_p), ("a_len", C.c_size_t), ("b", C.c_void_p),
+                ("b_len", C.c_size_t), ("r", C.c_size_t), ("alpha", C.c_float)]
+
+
+class AdamConfig(C.Structure):
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("eps", C.c_float), ("block_size", C.c_size_t),
+                ("max_resident_pages", C.c_size_t)]
+
+
+class AdamStats(C.Structure):
+    _fields_ = [("pages_streamed", C.c_size_t), ("state_bytes", C.c_size_t)]
+
+
+class QloraError(ValueError):
+    """Raised for every non-OK status; ``str()`` is the reference's
+    ``QloraError`` Display text (qlora-core/src/error.rs:16-24)."""
+
+    def __init__(self, status: int, msg: str):
+        super().__init__(msg)
+        self.status = status
+
+
+class NoDevice(RuntimeError):
+    pass
+
+
+_lib = None
+_lock = threading.Lock()
+
+vp, sz, f32, i32 = C.c_void_p, C.c_size_t, C.c_float, C.c_int
+
+
+def load() -> C.CDLL:
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with vkqlora.rs_amd/build_lib.py "
+                "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        L.qh_abi_version.restype = C.c_uint32
+        L.qh_last_error.restype = C.c_char_p
+        L.qh_ctx_create.argtypes = [C.POINTER(vp)]
+        L.qh_ctx_destroy.argtypes = [vp]
+        L.qh_ctx_destroy.restype = None
+        L.qh_ctx_device_name.argtypes = [vp, C.c_char_p, sz]
+        L.qh_ctx_synchronize.argtypes = [vp]
+        L.qh_ctx_set_timing.argtypes = [vp, i32]
+        L.qh_ctx_timing_report.argtypes = [vp, C.c_char_p, sz, i32]
+        for fn in ("qh_codes_len", "qh_num_blocks", "qh_num_absmax"):
+            getattr(L, fn).restype = sz
+        L.qh_codes_len.argtypes = [sz, sz]
+        L.qh_num_blocks.argtypes = [sz, sz, sz]
+        L.qh_num_absmax.argtypes = [sz, sz, sz]
+        L.qh_storage_bytes.restype = sz
+        L.qh_storage_bytes.argtypes = [C.POINTER(QWeight)]
+        L.qh_quantize_nf4.argtypes = [vp, vp, sz, sz, sz, sz, i32, vp, vp, vp, vp]
+        L.qh_block_scales.argtypes = [vp, C.POINTER(QWeight), vp]
+        L.qh_dequantize.argtypes = [vp, C.POINTER(QWeight), vp]
+        for fn in ("qh_matmul", "qh_matmul_trans_a", "qh_matmul_trans_b"):
+            getattr(L, fn).argtypes = [vp, vp, sz, vp, sz, sz, sz, sz, vp]
+        L.qh_qlora_forward.argtypes = [vp, C.POINTER(QWeight), C.POINTER(Lora), vp,
+                                       sz, sz, vp]
+        L.qh_qlora_backward.argtypes = [vp, C.POINTER(QWeight), C.POINTER(Lora), vp,
+                                        sz, vp, sz, sz, vp, vp, vp]
+        L.qh_adam_config_default.argtypes = [C.POINTER(AdamConfig)]
+        L.qh_adam_config_default.restype = None
+        L.qh_adam8bit_create.argtypes = [vp, C.POINTER(AdamConfig), C.POINTER(vp)]
+        L.qh_adam8bit_destroy.argtypes = [vp]
+        L.qh_adam8bit_destroy.restype = None
+        L.qh_adam8bit_step.argtypes = [vp, vp, vp, vp, vp, sz, C.POINTER(AdamStats)]
+        L.qh_adam8bit_step_dev.argtypes = [vp, vp, vp, vp, sz, C.POINTER(AdamStats), vp]
+        L.qh_adam8bit_state_bytes.restype = sz
+        L.qh_adam8bit_state_bytes.argtypes = [vp]
+        L.qh_adam8bit_get_state.argtypes = [vp, sz, vp, vp, vp, vp,
+                                            C.POINTER(C.c_uint64)]
+        L.qh_quantize_nf4_dev.argtypes = [vp, vp, sz, sz, sz, i32, vp, vp, vp, vp, vp]
+        L.qh_dequantize_dev.argtypes = [vp, C.POINTER(QWeight), vp, vp]
+        L.qh_matmul_dev.argtypes = [vp, i32, vp, vp, sz, sz, sz, vp, vp]
+        L.qh_qlora_forward_dev.argtypes = [vp, C.POINTER(QWeight), C.POINTER(Lora),
+                                           vp, i32, sz, vp, vp, vp]
+        L.qh_qlora_backward_dev.argtypes = [vp, C.POINTER(QWeight), C.POINTER(Lora),
+                                            vp, vp, i32, sz, vp, vp, vp, vp, vp]
+        _lib = L
+        return L
+
+
+def check(status: int) -> None:
+    if status == QH_OK:
+        return
+    msg = (load().qh_last_error() or b"").decode()
+    if status == QH_NO_DEVICE:
+        raise NoDevice(msg)
+    raise QloraError(status, msg)
+
+
+class Context:
+    """Owns one ``qh_ctx`` (a GPU device and stream)."""
+
+    def __init__(self):
+        L = load()
+        h = vp()
+        check(L.qh_ctx_create(C.byref(h)))
+        self.h = h
+        self.lib = L
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.qh_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def device_name(self) -> str:
+        buf = C.create_string_buffer(256)
+        check(self.lib.qh_ctx_device_name(self.h, buf, 256))
+        return buf.value.decode()
+
+    def synchronize(self):
+        check(self.lib.qh_ctx_synchronize(self.h))
+
+    def set_timing(self, on: bool):
+        check(self.lib.qh_ctx_set_timing(self.h, 1 if on else 0))
+
+    def timing_report(self, reset: bool = True) -> dict:
+        """{kernel: (launches, total_ms)} of the launches timed so far."""
+        buf = C.create_string_buffer(1 << 14)
+        check(self.lib.qh_ctx_timing_report(self.h, buf, len(buf), 1 if reset else 0))
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, cnt, ms = line.split()
+            out[name] = (int(cnt), float(ms))
+        return out
+
+
+_default_ctx = None
+
+
+def default_context() -> Context:
+    """Process-wide context (created on first use)."""
+    global _default_ctx
+    with _lock:
+        if _default_ctx is None:
+            _default_ctx = Context()
+        return _default_ctx

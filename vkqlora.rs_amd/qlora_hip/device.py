@@ -1,0 +1,139 @@
+"""Device-resident use of the C ABI from PyTorch (torch is only the HBM
+allocator and stream provider here; all compute is the library's kernels).
+
+``DeviceWeight`` keeps a packed NF4 weight in HBM (codes, i8 scale codes,
+fp32 absmax); ``forward`` / ``backward`` call the ``*_dev`` entry points on
+torch's current stream without synchronising.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import torch
+
+from ._lib import (Lora, QWeight, QH_BF16, QH_F32, QH_SCALES_DQ_INT8,
+                   QH_SCALES_F32, check, default_context)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+class DeviceWeight:
+    """A rows x cols NF4 weight resident in HBM."""
+
+    def __init__(self, rows, cols, block_size, codes, scales=None,
+                 scale_codes=None, absmax=None):
+        self.rows, self.cols, self.block_size = rows, cols, block_size
+        self.codes, self.scales = codes, scales
+        self.scale_codes, self.absmax = scale_codes, absmax
+
+    @property
+    def n(self) -> int:
+        return self.rows * self.cols
+
+    @property
+    def nbytes(self) -> int:
+        """Packed bytes (quant.rs:229-235 storage_bytes)."""
+        t = self.codes.numel()
+        if self.scales is not None:
+            return t + 4 * self.scales.numel()
+        return t + self.scale_codes.numel() + 4 * self.absmax.numel()
+
+    @classmethod
+    def quantize(cls, w: torch.Tensor, block_size: int = 64,
+                 double_quant: bool = True, ctx=None) -> "DeviceWeight":
+        """GPU quantize_nf4 of a (rows, cols) float32 CUDA tensor."""
+        ctx = ctx or default_context()
+        rows, cols = w.shape
+        w = w.contiguous()
+        n = rows * cols
+        nb = -(-n // block_size)
+        dev = w.device
+        codes = torch.empty((n + 1) // 2, dtype=torch.uint8, device=dev)
+        if double_quant:
+            sc = torch.empty(nb, dtype=torch.uint8, device=dev)
+            am = torch.empty(-(-nb // 256), dtype=torch.float32, device=dev)
+            check(ctx.lib.qh_quantize_nf4_dev(ctx.h, _p(w), rows, cols, block_size, 1,
+                                              _p(codes), None, _p(sc), _p(am),
+                                              C.c_void_p(_stream())))
+            return cls(rows, cols, block_size, codes, scale_codes=sc, absmax=am)
+        sf = torch.empty(nb, dtype=torch.float32, device=dev)
+        check(ctx.lib.qh_quantize_nf4_dev(ctx.h, _p(w), rows, cols, block_size, 0,
+                                          _p(codes), _p(sf), None, None,
+                                          C.c_void_p(_stream())))
+        return cls(rows, cols, block_size, codes, scales=sf)
+
+    def clone(self) -> "DeviceWeight":
+        c = lambda t: None if t is None else t.clone()  # noqa: E731
+        return DeviceWeight(self.rows, self.cols, self.block_size, c(self.codes),
+                            c(self.scales), c(self.scale_codes), c(self.absmax))
+
+    def struct(self) -> QWeight:
+        s = QWeight()
+        s.rows, s.cols, s.block_size = self.rows, self.cols, self.block_size
+        s.codes = self.codes.data_ptr()
+        if self.scales is not None:
+            s.scale_kind = QH_SCALES_F32
+            s.scales = self.scales.data_ptr()
+        else:
+            s.scale_kind = QH_SCALES_DQ_INT8
+            s.scale_codes = self.scale_codes.data_ptr()
+            s.absmax = self.absmax.data_ptr()
+        return s
+
+    def dequantize(self, ctx=None) -> torch.Tensor:
+        ctx = ctx or default_context()
+        out = torch.empty(self.n, dtype=torch.float32, device=self.codes.device)
+        s = self.struct()
+        check(ctx.lib.qh_dequantize_dev(ctx.h, C.byref(s), _p(out),
+                                        C.c_void_p(_stream())))
+        return out
+
+
+def lora_struct(a: Optional[torch.Tensor], b: Optional[torch.Tensor], r: int,
+                alpha: float):
+    if a is None:
+        return None
+    s = Lora()
+    s.a, s.a_len = a.data_ptr(), a.numel()
+    s.b, s.b_len = b.data_ptr(), b.numel()
+    s.r, s.alpha = r, alpha
+    return s
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return QH_F32
+    if t.dtype == torch.bfloat16:
+        return QH_BF16
+    raise TypeError(f"activations must be float32 or bfloat16, got {t.dtype}")
+
+
+def forward(w: DeviceWeight, lora, x: torch.Tensor, batch: int, y: torch.Tensor,
+            t1: Optional[torch.Tensor] = None, ctx=None, qw=None) -> None:
+    """Y = X.dequant(W)^T + (alpha/r) (X.A^T).B^T on the current stream.
+    ``lora`` is a ``Lora`` struct (or None); ``t1`` receives X.A^T."""
+    ctx = ctx or default_context()
+    s = qw if qw is not None else w.struct()
+    check(ctx.lib.qh_qlora_forward_dev(
+        ctx.h, C.byref(s), None if lora is None else C.byref(lora), _p(x), _dt(x),
+        batch, _p(y), _p(t1), C.c_void_p(_stream())))
+
+
+def backward(w: DeviceWeight, lora, x: torch.Tensor, dy: torch.Tensor, batch: int,
+             gx: torch.Tensor, ga: Optional[torch.Tensor] = None,
+             gb: Optional[torch.Tensor] = None, t1: Optional[torch.Tensor] = None,
+             ctx=None, qw=None) -> None:
+    ctx = ctx or default_context()
+    if x.dtype != dy.dtype:
+        raise TypeError("x and dy must share a dtype")
+    s = qw if qw is not None else w.struct()
+    check(ctx.lib.qh_qlora_backward_dev(
+        ctx.h, C.byref(s), None if lora is None else C.byref(lora), _p(x), _p(dy),
+        _dt(x), batch, _p(t1), _p(gx), _p(ga), _p(gb), C.c_void_p(_stream())))
