@@ -15,7 +15,7 @@
  *    `pollster::block_on` / `device.poll(Wait)`: qlora-wgpu/src/context.rs:34,
  *    kernels.rs:413).
  *  - `*_dev` entry points take device pointers that are already resident in
- *    HBM, enqueue on `stream` (a hipStream_t; NULL = the context's stream)
+ *    HBM, enqueue on `stream` (a hipStream_t; NULL = the HIP null stream)
  *    and return without synchronising.  Sizes are trusted.
  *  - The caller allocates every output at its exact size.  Opaque handles
  *    (qh_ctx, qh_adam8bit) are the only library-owned memory.

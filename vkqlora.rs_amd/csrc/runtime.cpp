@@ -194,8 +194,12 @@ struct qh_adam8bit {
 
 namespace {
 
+// Device-pointer entry points run on the caller's stream; NULL is the HIP
+// null stream (ordered with the caller's other default-stream work).  The
+// context's own stream serves only the blocking host-slice entry points.
 hipStream_t pick_stream(qh_ctx *ctx, void *stream) {
-  return stream ? (hipStream_t)stream : ctx->stream;
+  (void)ctx;
+  return (hipStream_t)stream;
 }
 
 DevQW make_devqw(const qh_qweight &w) {
@@ -881,9 +885,9 @@ qh_status qh_adam8bit_create(qh_ctx *ctx, const qh_adam_config *cfg,
     return fail(QH_ERR_INVALID_CONFIG, "betas must be in (0, 1)");
   if (cfg->block_size == 0 || cfg->max_resident_pages == 0)
     return fail(QH_ERR_INVALID_CONFIG, "block_size and max_resident_pages must be > 0");
-  if (cfg->block_size > 8192)
+  if (cfg->block_size > 4096)
     return fail(QH_ERR_INVALID_CONFIG,
-                "block_size > 8192 exceeds the GPU kernel's LDS staging");
+                "block_size > 4096 exceeds the GPU kernel's LDS staging");
   if (!ctx) return fail(QH_ERR_GPU, "context is NULL");
   qh_adam8bit *o = new (std::nothrow) qh_adam8bit();
   if (!o) return fail(QH_ERR_GPU, "host allocation failed");

@@ -75,7 +75,7 @@ class NoDevice(RuntimeError):
 
 
 _lib = None
-_lock = threading.Lock()
+_lock = threading.RLock()  # default_context() -> Context() -> load() nest
 
 vp, sz, f32, i32 = C.c_void_p, C.c_size_t, C.c_float, C.c_int
 
