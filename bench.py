@@ -78,72 +78,85 @@ def decode_bench(args, ctx, torch, dev, QD):
         xs = [torch.randn(batch, L["K"], device=dev, generator=g) for L in layers]
         ys = [torch.empty(batch, L["N"], device=dev) for L in layers]
 
-        def step(i, with_lora=True):
+        def step(i):
             for li, L in enumerate(layers):
                 c = (i * len(layers) + li) % copies
-                QD.forward(None, L["lora"] if with_lora else None, xs[li], batch,
-                           ys[li], ctx=ctx, qw=L["structs"][c])
+                QD.forward(None, L["lora"], xs[li], batch, ys[li], ctx=ctx,
+                           qw=L["structs"][c])
 
-        # eager reference result, then warm the scratch before capture
-        step(0)
-        torch.cuda.synchronize()
-        ref = [y.clone() for y in ys]
-        n_graph = copies  # one graph covers every copy once
-        graphs = {}
-        for lora_on in (True, False):
+        n_graph = copies  # one graph covers every weight copy once
+
+        def capture():
             gr = torch.cuda.CUDAGraph()
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):
-                step(0, lora_on)  # warm-up on the capture stream
+                step(0)  # warm-up on the capture stream
             torch.cuda.current_stream().wait_stream(s)
             torch.cuda.synchronize()
             with torch.cuda.graph(gr):
                 for i in range(n_graph):
-                    step(i, lora_on)
-            graphs[lora_on] = gr
+                    step(i)
+            return gr
+
+        # eager reference result (also sizes the library's scratch)
+        step(0)
+        torch.cuda.synchronize()
+        ref = [y.clone() for y in ys]
+        graph = capture()
         # the graph must reproduce the eager result on every replay
         for _ in range(2):
-            graphs[True].replay()
+            graph.replay()
             torch.cuda.synchronize()
             for y, rr in zip(ys, ref):
                 assert torch.equal(y, rr), "graph replay differs from eager run"
 
         reps = max(1, -(-args.steps // n_graph))
         wreps = max(1, -(-args.warmup // n_graph))
-        out = {}
-        for lora_on in (True, False):
-            for _ in range(wreps):
-                graphs[lora_on].replay()
+        for _ in range(wreps):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        wall_step = (time.perf_counter() - t0) / (reps * n_graph) * 1e3
+        ms_step = e0.elapsed_time(e1) / (reps * n_graph)
+
+        # Per-kernel durations: with timing on, the library launches each
+        # hot-path kernel with start/stop events that the GPU stamps at that
+        # kernel's own start and end (hipExtLaunchKernelGGL), so the eager
+        # launches here time the kernels alone, without host gaps.
+        ctx.set_timing(True)
+        for _ in range(2):  # the first pass warms up, the second is kept
+            for i in range(n_graph):
+                step(i)
             torch.cuda.synchronize()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            t0 = time.perf_counter()
-            e0.record()
-            for _ in range(reps):
-                graphs[lora_on].replay()
-            e1.record()
-            torch.cuda.synchronize()
-            wall = time.perf_counter() - t0
-            ms = e0.elapsed_time(e1)
-            out[lora_on] = (ms / (reps * n_graph), wall / (reps * n_graph) * 1e3)
-        ms_step, wall_step = out[True]
-        ms_gemv_pair = out[False][0]  # the two GEMV launches alone
+            rep = ctx.timing_report(reset=True)
+        ctx.set_timing(False)
+        kern = {k: dict(launches=v[0], avg_ms=v[1] / max(v[0], 1))
+                for k, v in rep.items()}
         gemv_bytes = sum(L["base"].nbytes + 4 * batch * (L["K"] + L["N"])
-                         for L in layers)
-        full_bytes = gemv_bytes + sum(4 * (L["a"].numel() + L["b"].numel())
-                                      for L in layers)
+                         + 4 * L["b"].numel() for L in layers)
+        full_bytes = gemv_bytes + sum(4 * L["a"].numel() for L in layers)
         flops = sum(2 * batch * L["N"] * L["K"] + 2 * batch * r * (L["N"] + L["K"])
                     for L in layers)
-        results[batch] = dict(
+        main = kern.get("decode") or kern.get("gemv") or kern.get("forward_gemm")
+        res = dict(
             ms_per_step=ms_step, wall_ms_per_step=wall_step,
             weight_gbs=wbytes / (ms_step * 1e6),
             total_gbs=full_bytes / (ms_step * 1e6),
             tflops=flops / (ms_step * 1e9),
-            gemv_ms_per_launch=ms_gemv_pair / 2,
-            gemv_achieved_gbs=gemv_bytes / (ms_gemv_pair * 1e6),
-            gemv_bytes_per_launch=gemv_bytes / 2,
-            steps=reps * n_graph)
+            kernels=kern, steps=reps * n_graph)
+        if main:
+            res.update(main_kernel_ms=main["avg_ms"],
+                       main_kernel_bytes=gemv_bytes / 2,
+                       main_kernel_gbs=gemv_bytes / 2 / (main["avg_ms"] * 1e6))
+        results[batch] = res
     return results, dict(copies=copies, packed_weight_bytes=wbytes, r=r,
                          alpha=alpha)
 
@@ -304,11 +317,14 @@ def main():
             prefill["cpu_baseline"] = cpu_pre
 
     d1 = dec[1]
-    roof = dict(bound="hbm", kernel="k_gemv (fused NF4 dequant-GEMV, batch 1)",
-                achieved=d1["gemv_achieved_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=d1["gemv_achieved_gbs"] / HBM_PEAK_GBS,
-                bytes_per_launch=d1["gemv_bytes_per_launch"],
-                avg_launch_ms=d1["gemv_ms_per_launch"], traffic=None)
+    roof = None
+    if "main_kernel_gbs" in d1:
+        roof = dict(bound="hbm",
+                    kernel="k_decode (fused NF4 dequant-GEMV + LoRA epilogue, batch 1)",
+                    achieved=d1["main_kernel_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=d1["main_kernel_gbs"] / HBM_PEAK_GBS,
+                    bytes_per_launch=d1["main_kernel_bytes"],
+                    avg_launch_ms=d1["main_kernel_ms"], traffic=None)
     line = {
         "metric": METRIC,
         "value": d1["weight_gbs"],

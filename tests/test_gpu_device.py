@@ -107,6 +107,45 @@ def test_decode_shape_forward_parity(ctx, QD, N, K, M):
     assert e < TOL_F32, e
 
 
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 2, 7, 16])
+def test_decode_path_ragged_rows_t1_and_dtypes(ctx, QD, act, M):
+    # batch <= 16 with in_dim % 256 == 0 takes the MFMA decode kernel;
+    # N = 300 is not a multiple of its 16-row tile
+    N, K, r, alpha = 300, 512, 8, 16.0
+    _say(f"decode path M={M} act={act}")
+    d = _setup(QD, ctx, N, K, r, M, SEED ^ (M + 77), act)
+    lora = QD.lora_struct(d["ta"], d["tb"], r, alpha)
+    y = torch.empty(M, N, device="cuda:0")
+    t1 = torch.empty(M, r, device="cuda:0")
+    QD.forward(d["W"], lora, d["tx"], M, y, t1=t1, ctx=ctx)
+    y0 = torch.empty(M, N, device="cuda:0")
+    QD.forward(d["W"], None, d["tx"], M, y0, ctx=ctx)
+    torch.cuda.synchronize()
+    wd = O.dequantize(O.quantize(d["w"]))
+    tol = TOL_F32 if act == torch.float32 else TOL_BF16
+    yo = O.qlora_forward(wd, N, K, d["a"], d["b"], r, alpha, d["x"], M)
+    assert nerr(y.cpu().numpy().ravel(), yo, K, d["x"], wd) < tol
+    y0o = O.qlora_forward(wd, N, K, None, None, 0, 0.0, d["x"], M)
+    assert nerr(y0.cpu().numpy().ravel(), y0o, K, d["x"], wd) < tol
+    t1o = O.matmul_trans_b(d["x"], d["a"], M, K, r)
+    assert nerr(t1.cpu().numpy().ravel(), t1o, K, d["x"], d["a"]) < tol
+
+
+def test_decode_path_f32_scales(ctx, QD):
+    N, K, M = 64, 1024, 3
+    g = O.Rng(12)
+    w, x = g.normal(N * K, 0.02), g.normal(M * K)
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).cuda().view(N, K),
+                                 double_quant=False, ctx=ctx)
+    y = torch.empty(M, N, device="cuda:0")
+    QD.forward(W, None, torch.from_numpy(x).cuda(), M, y, ctx=ctx)
+    torch.cuda.synchronize()
+    wd = O.dequantize(O.quantize(w, 64, False))
+    yo = O.qlora_forward(wd, N, K, None, None, 0, 0.0, x, M)
+    assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
+
+
 def test_smollm_block_projections_and_adam(ctx, QD):
     # config 4: seven projections fwd+bwd at 8x256 tokens, then one
     # PagedAdam step (max_resident_pages=4) over the 14 adapter tensors

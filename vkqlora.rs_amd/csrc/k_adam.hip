@@ -100,9 +100,8 @@ hipError_t launch_adam(const AdamTensor *tensors, int ntensors,
     if (blocks == 0) continue;
     for (int64_t b0 = 0; b0 < blocks; b0 += 65535) {
       int64_t nbk = blocks - b0 < 65535 ? blocks - b0 : 65535;
-      k_adam<<<dim3((unsigned)nbk), dim3(256), shmem, s>>>(B, b0, block_size, lr,
-                                                          beta1, beta2, eps);
-      hipError_t e = hipGetLastError();
+      hipError_t e = qh_launch(k_adam, dim3((unsigned)nbk), dim3(256), (uint32_t)shmem, s,
+                               B, b0, block_size, lr, beta1, beta2, eps);
       if (e != hipSuccess) return e;
     }
   }

@@ -2,6 +2,9 @@
 #include "qh_internal.h"
 
 namespace qh {
+
+thread_local LaunchTiming g_launch_timing;
+
 namespace {
 
 __global__ void k_axpy_inplace(float *__restrict__ y, const float *__restrict__ x,

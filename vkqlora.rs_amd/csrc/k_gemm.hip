@@ -413,8 +413,7 @@ hipError_t run(const GemmArgs &g0, float *partial, hipStream_t s) {
   }
   dim3 grid((unsigned)((g.N + BN - 1) / BN), (unsigned)((g.M + BM - 1) / BM),
             (unsigned)(g.splits > 1 ? g.splits : 1));
-  k_gemm<BM, BN, WM_, AF, AE, BF, BE, B2F><<<grid, dim3(NT), 0, s>>>(g);
-  hipError_t e = hipGetLastError();
+  hipError_t e = qh_launch(k_gemm<BM, BN, WM_, AF, AE, BF, BE, B2F>, grid, dim3(NT), 0, s, g);
   if (e != hipSuccess || g.splits <= 1) return e;
   const int64_t tot = g.M * g.N;
   k_reduce_splits<<<dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s>>>(

@@ -1,17 +1,25 @@
-// k_gemv.hip -- decode-shaped fused NF4 dequant-GEMV for gfx950.
+// k_gemv.hip -- decode-shaped fused NF4 dequant-GEMV for gfx950 (batch <= 4).
 //
 // Replaces, for small batches, the reference forward's dequant dispatch +
 // mm_nt (qlora-wgpu/src/kernels.rs:281-282, shaders/gemm.wgsl:68-98) and its
 // LoRA branch (kernels.rs:284-294):
 //
-//   y[m][n] = sum_b s_{n,b} * (sum_{k in b} x[m][k] * L[code_{n,k}])
-//           + s * sum_j t1[m][j] * B[n][j]
+//   y[m][n] = sum_b s_{n,b} (sum_{k in b} x[m][k] L[c_{n,k}])
+//           + (alpha/r) sum_j T1[m][j] B[n][j]
 //
-// HBM-bound on the packed weight stream: every code byte is read once, with
-// the per-block scale hoisted out of the inner product (one multiply per
-// 16 elements instead of one per element).  A workgroup owns R weight rows
-// and spreads their K range over all 256 threads, so each thread reuses the
-// x values it loaded for all R rows.
+// HBM-bound on the packed weight stream, so the kernel is shaped around
+// its loads:
+//  * coalescing: the 64 lanes of a wave read 64 consecutive 8-byte chunks
+//    of ONE weight row (512 contiguous bytes per load instruction);
+//  * reuse of x: a workgroup owns 16 rows and each thread keeps its x chunk
+//    in registers for all 16 rows;
+//  * no waits between loads: all code words and raw scale fields of an
+//    iteration are issued before any is used; scales are decoded after;
+//  * one multiply per 16 elements for the block scale (hoisting);
+//  * the LoRA epilogue reads T1 (from the prep kernel) and 16 rows of B that
+//    were staged in LDS by loads issued at kernel start.
+// The 16 per-thread row sums are reduced across the wave by recursive
+// halving (17 shuffles instead of 96), then across the 4 waves in LDS.
 #include "qh_internal.h"
 #include "qh_nf4.h"
 
@@ -20,18 +28,20 @@ namespace {
 
 __constant__ float c_lut[17] = QH_NF4_LUT17_INIT;
 
+constexpr int kRows = 16;
+
 __device__ __forceinline__ float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
 
-template <int M>
-__device__ __forceinline__ void load_x16(const void *x, int x_bf16, int64_t K,
-                                         int64_t k, float (&xv)[M][16]) {
+template <int M, int XBF16>
+__device__ __forceinline__ void load_x16(const void *x, int64_t K, int64_t k,
+                                         float (&xv)[M][16]) {
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    if (!x_bf16) {
+    if (!XBF16) {
       const float4 *p = (const float4 *)((const float *)x + m * K + k);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float4 t = p[q];
+        const float4 t = p[q];
         xv[m][4 * q + 0] = t.x; xv[m][4 * q + 1] = t.y;
         xv[m][4 * q + 2] = t.z; xv[m][4 * q + 3] = t.w;
       }
@@ -39,8 +49,8 @@ __device__ __forceinline__ void load_x16(const void *x, int x_bf16, int64_t K,
       const uint4 *p = (const uint4 *)((const uint16_t *)x + m * K + k);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        uint4 t = p[q];
-        uint32_t u[4] = {t.x, t.y, t.z, t.w};
+        const uint4 t = p[q];
+        const uint32_t u[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           xv[m][8 * q + 2 * i] = bf16f(u[i] & 0xffffu);
@@ -51,138 +61,169 @@ __device__ __forceinline__ void load_x16(const void *x, int x_bf16, int64_t K,
   }
 }
 
-template <int M, int R>
+// Sum 16 values over the 64 lanes of a wave; lane l returns the total of
+// value (l >> 2) & 15 (valid in lanes whose low two bits are 0).
+__device__ __forceinline__ float reduce16(float (&v)[16]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int half = 8, off = 32; half >= 1; half >>= 1, off >>= 1) {
+    const bool up = (lane & off) != 0;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float keep = up ? v[i + half] : v[i];
+      const float send = up ? v[i] : v[i + half];
+      v[i] = keep + __shfl_xor(send, off);
+    }
+  }
+  float s = v[0];
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 1);
+  return s;
+}
+
+template <int M, int XBF16, int KIND>
 __global__ __launch_bounds__(256) void k_gemv(DevQW w, const void *__restrict__ x,
-                                              int x_bf16,
                                               const float *__restrict__ t1,
-                                              const float *__restrict__ lb,
-                                              int r, float s, float *__restrict__ y) {
+                                              const float *__restrict__ lb, int r,
+                                              float s_lora, float *__restrict__ y) {
   __shared__ float lut[16];
-  __shared__ float red[4][M * R];
+  __shared__ float red[4][kRows * M];
+  __shared__ float lbs[kRows * 64];
+  __shared__ float t1s[4 * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t N = w.rows, K = w.cols, KB = K >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * kRows;
+
   if (tid < 16) lut[tid] = c_lut[tid];
   __syncthreads();
+  // LoRA operands: issued now, stored to LDS after the main loop.
+  float lbv[4], t1v = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int idx = tid + 256 * q;
+    lbv[q] = 0.0f;
+    if (idx < kRows * r) {
+      int64_t row = n0 + idx / r;
+      row = row < N ? row : N - 1;
+      lbv[q] = lb[row * r + idx % r];
+    }
+  }
+  if (tid < M * r) t1v = t1[tid];
 
-  const int64_t N = w.rows, K = w.cols;
-  const int64_t n0 = (int64_t)blockIdx.x * R;
+  float acc[kRows][M];
+#pragma unroll
+  for (int rr = 0; rr < kRows; ++rr)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[rr][m] = 0.0f;
+
   const int64_t nch = K >> 4;  // 16-element chunks per row
-  float acc[M][R];
-#pragma unroll
-  for (int m = 0; m < M; ++m)
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr) acc[m][rr] = 0.0f;
-
   for (int64_t c = tid; c < nch; c += 256) {
     const int64_t k = c << 4;
-    uint2 code[R];
-    float sc[R];
+    float xv[M][16];
+    load_x16<M, XBF16>(x, K, k, xv);  // first: used first
+    uint2 code[kRows];
+    float sa[kRows];
+    int32_t sq[kRows];
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
+    for (int rr = 0; rr < kRows; ++rr) {
       const int64_t n = n0 + rr < N ? n0 + rr : N - 1;
-      const int64_t e = n * K + k;
-      code[rr] = *(const uint2 *)(w.codes + (e >> 1));
-      const int64_t b = e >> 6;
-      if (w.kind == 0) {
-        sc[rr] = w.scales[b];
+      code[rr] = *(const uint2 *)(w.codes + ((n * K + k) >> 1));
+      const int64_t b = n * KB + (k >> 6);
+      if (KIND == 0) {
+        sa[rr] = w.scales[b];
+        sq[rr] = 0;
       } else {
-        sc[rr] = (float)(int8_t)w.scale_codes[b] / 127.0f * w.absmax[b >> 8];
+        sq[rr] = (int8_t)w.scale_codes[b];
+        sa[rr] = w.absmax[b >> 8];
       }
     }
-    float xv[M][16];
-    load_x16<M>(x, x_bf16, K, k, xv);
+    // Keep all of the iteration's loads ahead of their uses: without this
+    // fence the scheduler sinks each row's load next to its use and the 16
+    // memory latencies serialise.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      float lv[16];
+    for (int rr = 0; rr < kRows; ++rr) {
+      float p[M];
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        lv[e] = lut[((e < 8 ? code[rr].x : code[rr].y) >> (4 * (e & 7))) & 15u];
+      for (int m = 0; m < M; ++m) p[m] = 0.0f;
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        float p = 0.0f;
+      for (int e = 0; e < 16; ++e) {
+        const float lv = lut[((e < 8 ? code[rr].x : code[rr].y) >> (4 * (e & 7))) & 15u];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) p = fmaf(xv[m][e], lv[e], p);
-        acc[m][rr] = fmaf(p, sc[rr], acc[m][rr]);
+        for (int m = 0; m < M; ++m) p[m] = fmaf(xv[m][e], lv, p[m]);
       }
+      // block scale: within 1 ulp of quant.rs:218's decode; only this sum
+      // uses it, never a stored weight
+      const float sc = KIND == 0 ? sa[rr] : (float)sq[rr] * (sa[rr] * (1.0f / 127.0f));
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[rr][m] = fmaf(p[m], sc, acc[rr][m]);
     }
   }
 
+  // wave reduction: for each m, 16 row sums over 64 lanes
 #pragma unroll
-  for (int m = 0; m < M; ++m)
+  for (int m = 0; m < M; ++m) {
+    float v[16];
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      float v = acc[m][rr];
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-      if (lane == 0) red[wave][m * R + rr] = v;
-    }
+    for (int rr = 0; rr < kRows; ++rr) v[rr] = acc[rr][m];
+    const float s = reduce16(v);
+    if ((lane & 3) == 0) red[wave][m * kRows + (lane >> 2)] = s;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int idx = tid + 256 * q;
+    if (idx < kRows * r) lbs[idx] = lbv[q];
+  }
+  if (tid < M * r) t1s[tid] = t1v;
   __syncthreads();
-  if (tid < M * R) {
-    const int m = tid / R, rr = tid % R;
+  if (tid < kRows * M) {
+    const int m = tid / kRows, rr = tid % kRows;
     const int64_t n = n0 + rr;
     if (n < N) {
       float base = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
       if (r > 0) {
         float l = 0.0f;
-        for (int j = 0; j < r; ++j) l += t1[m * r + j] * lb[n * r + j];
-        base += s * l;
+        for (int j = 0; j < r; ++j) l += t1s[m * r + j] * lbs[rr * r + j];
+        base += s_lora * l;
       }
       y[m * N + n] = base;
     }
   }
 }
 
-// out[m][j] = sum_k x[m][k] * a[j][k]: one workgroup per (m, j).
-__global__ __launch_bounds__(256) void k_dot_rows(const void *__restrict__ x, int x_bf16,
-                                                  const float *__restrict__ a,
-                                                  int64_t K, int r,
-                                                  float *__restrict__ out) {
-  __shared__ float red[4];
-  const int j = blockIdx.x, m = blockIdx.y;
-  float acc = 0.0f;
-  for (int64_t k = threadIdx.x; k < K; k += 256) {
-    float xv = x_bf16 ? bf16f(((const uint16_t *)x)[m * K + k])
-                      : ((const float *)x)[m * K + k];
-    acc = fmaf(xv, a[(int64_t)j * K + k], acc);
-  }
-  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) out[m * r + j] = (red[0] + red[1]) + (red[2] + red[3]);
+template <int M, int XB>
+hipError_t run_gemv(const DevQW &w, const void *x, const float *t1, const float *lb,
+                    int64_t r, float s, float *y, hipStream_t st) {
+  const dim3 grid((unsigned)((w.rows + kRows - 1) / kRows));
+  if (w.kind == 0)
+    return qh_launch(k_gemv<M, XB, 0>, grid, dim3(256), 0, st, w, x, t1, lb, (int)r, s, y);
+  return qh_launch(k_gemv<M, XB, 1>, grid, dim3(256), 0, st, w, x, t1, lb, (int)r, s, y);
 }
 
 template <int M>
-hipError_t run_gemv(const DevQW &w, const void *x, int x_bf16, const float *t1,
-                    const float *lb, int64_t r, float s, float *y,
-                    hipStream_t st) {
-  constexpr int R = 4;
-  dim3 grid((unsigned)((w.rows + R - 1) / R));
-  k_gemv<M, R><<<grid, dim3(256), 0, st>>>(w, x, x_bf16, t1, lb, (int)r, s, y);
-  return hipGetLastError();
+hipError_t run_gemv_dt(const DevQW &w, const void *x, int xb, const float *t1,
+                       const float *lb, int64_t r, float s, float *y, hipStream_t st) {
+  if (xb) return run_gemv<M, 1>(w, x, t1, lb, r, s, y, st);
+  return run_gemv<M, 0>(w, x, t1, lb, r, s, y, st);
 }
 
 }  // namespace
 
 bool gemv_ok(const DevQW &w, int64_t M) {
-  return M >= 1 && M <= 4 && w.bs == 64 && w.cols % 64 == 0;
-}
-
-hipError_t launch_dot_rows(const void *x, int x_bf16, const float *a,
-                           int64_t M, int64_t K, int64_t r, float *out,
-                           hipStream_t st) {
-  if (M == 0 || r == 0) return hipSuccess;
-  k_dot_rows<<<dim3((unsigned)r, (unsigned)M), dim3(256), 0, st>>>(x, x_bf16, a, K,
-                                                                   (int)r, out);
-  return hipGetLastError();
+  return M >= 1 && M <= 4 && w.bs == 64 && w.cols % 64 == 0 &&
+         (((uintptr_t)w.codes) & 7) == 0;
 }
 
 hipError_t launch_gemv(const DevQW &w, const void *x, int x_bf16, int64_t M,
                        const float *t1, const float *lb, int64_t r, float s,
                        float *y, hipStream_t st) {
   if (w.rows == 0) return hipSuccess;
+  if (r > 64) return hipErrorInvalidValue;
   switch (M) {
-    case 1: return run_gemv<1>(w, x, x_bf16, t1, lb, r, s, y, st);
-    case 2: return run_gemv<2>(w, x, x_bf16, t1, lb, r, s, y, st);
-    case 3: return run_gemv<3>(w, x, x_bf16, t1, lb, r, s, y, st);
-    case 4: return run_gemv<4>(w, x, x_bf16, t1, lb, r, s, y, st);
+    case 1: return run_gemv_dt<1>(w, x, x_bf16, t1, lb, r, s, y, st);
+    case 2: return run_gemv_dt<2>(w, x, x_bf16, t1, lb, r, s, y, st);
+    case 3: return run_gemv_dt<3>(w, x, x_bf16, t1, lb, r, s, y, st);
+    case 4: return run_gemv_dt<4>(w, x, x_bf16, t1, lb, r, s, y, st);
     default: return hipErrorInvalidValue;
   }
 }

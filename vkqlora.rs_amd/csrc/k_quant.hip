@@ -210,10 +210,9 @@ hipError_t launch_quantize(const float *w, int64_t n, int64_t bs, int dq,
   const int64_t nb = (n + bs - 1) / bs;
   const int64_t codes_len = (n + 1) / 2;
   const int64_t nsb = (nb + 255) / 256;
-  if (bs == 64) {
-    k_quantize64<<<dim3((unsigned)nsb), dim3(256), 0, s>>>(
-        w, n, dq, codes, codes_len, scales, scale_codes, absmax, nb);
-    return hipGetLastError();
+  if (bs == 64 && (((uintptr_t)w) & 15) == 0 && (((uintptr_t)codes) & 3) == 0) {
+    return qh_launch(k_quantize64, dim3((unsigned)nsb), dim3(256), 0, s, w, n, dq, codes,
+                     codes_len, scales, scale_codes, absmax, nb);
   }
   float *am = dq ? scratch : scales;
   k_block_absmax<<<dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s>>>(
@@ -236,9 +235,8 @@ hipError_t launch_block_scales(const DevQW &w, float *out, hipStream_t s) {
 hipError_t launch_dequantize(const DevQW &w, float *out, hipStream_t s) {
   if (w.n == 0) return hipSuccess;
   int64_t threads = (w.n + 7) / 8;
-  k_dequantize<<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(
-      w, out);
-  return hipGetLastError();
+  return qh_launch(k_dequantize, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                   w, out);
 }
 
 }  // namespace qh

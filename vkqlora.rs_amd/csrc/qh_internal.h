@@ -1,11 +1,38 @@
 // qh_internal.h -- declarations shared by the runtime (runtime.cpp) and the
 // gfx950 kernels (k_*.hip).  Not part of the public ABI.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace qh {
+
+// Kernel timing: when the runtime arms `g_launch_timing` around a call, the
+// next kernel launched through qh_launch gets the two events stamped by the
+// GPU at that kernel's own start and end (hipExtLaunchKernelGGL), so host
+// launch gaps never enter the measurement.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local LaunchTiming g_launch_timing;
+
+template <typename... KArgs, typename... Args>
+hipError_t qh_launch(void (*k)(KArgs...), dim3 grid, dim3 block, uint32_t shmem,
+                     hipStream_t s, Args &&...args) {
+  static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+  if (g_launch_timing.start) {
+    const LaunchTiming t = g_launch_timing;
+    g_launch_timing = LaunchTiming();
+    hipExtLaunchKernelGGL(k, grid, block, shmem, s, t.start, t.stop, 0,
+                          static_cast<KArgs>(std::forward<Args>(args))...);
+  } else {
+    k<<<grid, block, shmem, s>>>(static_cast<KArgs>(std::forward<Args>(args))...);
+  }
+  return hipGetLastError();
+}
 
 // Device view of a quantized weight (rows x cols, flat row-major index).
 struct DevQW {
@@ -76,6 +103,21 @@ bool gemv_ok(const DevQW &w, int64_t M);
 hipError_t launch_dot_rows(const void *x, int x_bf16, const float *a,
                            int64_t M, int64_t K, int64_t r, float *out,
                            hipStream_t st);
+
+// ---- k_decode.hip ----
+// Decode path (batch <= 16): X split + T1 partials, then the MFMA GEMV with
+// the LoRA epilogue.  t1_out (optional) receives T1 = X A^T.
+bool decode_ok(const DevQW &w, int64_t M, int64_t r);
+size_t decode_scratch_bytes(int64_t M, int64_t K, int64_t r);
+hipError_t launch_decode_prep(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                              const float *a, int64_t r, float *t1_out, void *scratch,
+                              hipStream_t st);
+// T1 = X A^T for small batches (K % 8 == 0, 16-byte aligned rows).
+hipError_t launch_lora_t1(const void *x, int x_bf16, int64_t M, int64_t K, const float *a,
+                          int64_t r, float *t1, hipStream_t st);
+hipError_t launch_decode(const DevQW &w, int x_bf16, int64_t M, const float *lb,
+                         int64_t r, float s, float *y, const float *t1_out, void *scratch,
+                         hipStream_t st);
 
 // ---- k_elem.hip ----
 hipError_t launch_axpy_inplace(float *y, const float *x, int64_t n,

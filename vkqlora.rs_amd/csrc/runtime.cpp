@@ -138,21 +138,31 @@ hipEvent_t take_event(qh_ctx *c) {
   return e;
 }
 
-// Brackets one kernel launch with events on its stream while timing is on.
+// Arms the GPU-stamped start/stop events of the next qh_launch while timing
+// is on (never during stream capture).
 struct Timed {
   qh_ctx *c;
   const char *name;
-  hipStream_t s;
   hipEvent_t a = nullptr, b = nullptr;
-  Timed(qh_ctx *ctx, const char *n, hipStream_t st) : c(ctx), name(n), s(st) {
+  Timed(qh_ctx *ctx, const char *n, hipStream_t st) : c(ctx), name(n) {
     if (!c->timing) return;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return;
     a = take_event(c);
     b = take_event(c);
-    check(hipEventRecord(a, s), "hipEventRecord");
+    qh::g_launch_timing.start = a;
+    qh::g_launch_timing.stop = b;
   }
   ~Timed() {
     if (!a) return;
-    if (hipEventRecord(b, s) == hipSuccess) c->pending.push_back({name, a, b});
+    if (qh::g_launch_timing.start == nullptr) {
+      c->pending.push_back({name, a, b});  // consumed by a launch
+    } else {
+      qh::g_launch_timing = qh::LaunchTiming();
+      c->event_pool.push_back(a);
+      c->event_pool.push_back(b);
+    }
   }
 };
 
@@ -349,7 +359,42 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   const float sc = lora ? l->alpha / (float)l->r : 0.0f;  // lora.rs:64-66
   const int xe = xdt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
   const bool fast = qh::nf4_fast_ok(W);
-  const bool gemv = qh::gemv_ok(W, M);
+  // Small batches: VALU GEMV (batch <= 4) or MFMA decode kernel (<= 16).
+  // Both take T1 = X A^T from the prep kernel, which needs 16-byte aligned
+  // rows of X and A.
+  const bool aligned = (((uintptr_t)x) & 15) == 0 && (K % 8) == 0 &&
+                       (!lora || (((uintptr_t)l->a) & 15) == 0);
+  const bool gemv = aligned && r <= 64 && qh::gemv_ok(W, M);
+  const bool decode = aligned && !gemv && qh::decode_ok(W, M, r);
+
+  if (gemv) {
+    Carve cg;
+    size_t i_t1 = cg.add(lora && !t1_out ? (size_t)M * r * 4 : 0);
+    auto pg = cg.bind(ctx->scratch);
+    float *t1 = lora ? (t1_out ? t1_out : (float *)pg[i_t1]) : nullptr;
+    const int xb = xe == qh::E_BF16;
+    if (lora)
+      timed(ctx, "lora_t1", s, [&] { return qh::launch_lora_t1(x, xb, M, K, l->a, r, t1, s); });
+    timed(ctx, "gemv", s, [&] {
+      return qh::launch_gemv(W, x, xb, M, t1, lora ? l->b : nullptr, r, sc, y, s);
+    });
+    return;
+  }
+
+  if (decode) {
+    Carve cd;
+    size_t i_sc = cd.add(qh::decode_scratch_bytes(M, K, r));
+    auto pd = cd.bind(ctx->scratch);
+    const int xb = xe == qh::E_BF16;
+    timed(ctx, "decode_prep", s, [&] {
+      return qh::launch_decode_prep(W, x, xb, M, lora ? l->a : nullptr, r, t1_out, pd[i_sc],
+                                    s);
+    });
+    timed(ctx, "decode", s, [&] {
+      return qh::launch_decode(W, xb, M, lora ? l->b : nullptr, r, sc, y, t1_out, pd[i_sc], s);
+    });
+    return;
+  }
 
   GemmArgs gt1{}, gm{};
   if (lora) {
@@ -360,16 +405,11 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   Carve c;
   size_t i_t1 = c.add(lora && !t1_out ? (size_t)M * r * 4 : 0);
   size_t i_w32 = c.add(fast ? 0 : (size_t)W.n * 4);
-  size_t i_p1 = c.add(lora && !gemv ? partial_floats(gt1) * 4 : 0);
+  size_t i_p1 = c.add(lora ? partial_floats(gt1) * 4 : 0);
   size_t i_p2 = c.add(0);
   auto p = c.bind(ctx->scratch);
   float *t1 = lora ? (t1_out ? t1_out : (float *)p[i_t1]) : nullptr;
 
-  if (gemv) {
-    if (lora) timed(ctx, "t1", s, [&] { return qh::launch_dot_rows(x, xe == qh::E_BF16, l->a, M, K, r, t1, s); });
-    timed(ctx, "gemv", s, [&] { return qh::launch_gemv(W, x, xe == qh::E_BF16, M, t1, lora ? l->b : nullptr, r, sc, y, s); });
-    return;
-  }
   if (lora) {
     gt1.C = t1;
     timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(gt1, (float *)p[i_p1], s); });
@@ -503,6 +543,8 @@ qh_status guarded(qh_ctx *ctx, F &&f) {
     check(hipSetDevice(ctx->device), "hipSetDevice");
     return f();
   } catch (const GpuError &e) {
+    (void)hipGetLastError();  // do not leave the failure for the caller's next HIP call
+    qh::g_launch_timing = qh::LaunchTiming();
     return fail(QH_ERR_GPU, e.msg);
   } catch (const std::bad_alloc &) {
     return fail(QH_ERR_GPU, "host allocation failed");
