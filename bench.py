@@ -145,7 +145,9 @@ def decode_bench(args, ctx, torch, dev, QD):
         full_bytes = gemv_bytes + sum(4 * L["a"].numel() for L in layers)
         flops = sum(2 * batch * L["N"] * L["K"] + 2 * batch * r * (L["N"] + L["K"])
                     for L in layers)
-        main = kern.get("decode") or kern.get("gemv") or kern.get("forward_gemm")
+        main_name = next((k for k in ("decode_small", "decode", "gemv", "forward_gemm")
+                          if k in kern), None)
+        main = kern.get(main_name) if main_name else None
         res = dict(
             ms_per_step=ms_step, wall_ms_per_step=wall_step,
             weight_gbs=wbytes / (ms_step * 1e6),
@@ -153,7 +155,7 @@ def decode_bench(args, ctx, torch, dev, QD):
             tflops=flops / (ms_step * 1e9),
             kernels=kern, steps=reps * n_graph)
         if main:
-            res.update(main_kernel_ms=main["avg_ms"],
+            res.update(main_kernel=main_name, main_kernel_ms=main["avg_ms"],
                        main_kernel_bytes=gemv_bytes / 2,
                        main_kernel_gbs=gemv_bytes / 2 / (main["avg_ms"] * 1e6))
         results[batch] = res
@@ -320,7 +322,8 @@ def main():
     roof = None
     if "main_kernel_gbs" in d1:
         roof = dict(bound="hbm",
-                    kernel="k_decode (fused NF4 dequant-GEMV + LoRA epilogue, batch 1)",
+                    kernel=(f"{d1['main_kernel']} (fused NF4 dequant-GEMV + LoRA "
+                            "epilogue, batch 1, mean of the two layers)"),
                     achieved=d1["main_kernel_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=d1["main_kernel_gbs"] / HBM_PEAK_GBS,
                     bytes_per_launch=d1["main_kernel_bytes"],

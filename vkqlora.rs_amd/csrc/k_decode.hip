@@ -7,27 +7,29 @@
 //   y[m][n] = sum_b s_{n,b} sum_{k in b} x[m][k] L[c_{n,k}]
 //           + (alpha/r) sum_j T1[m][j] B[n][j],      T1 = X A^T.
 //
-// The weight stream is the only large input, so the kernel is built to keep
-// VALU work per packed byte small:
-//  * Codes are turned into MFMA operands by table lookup: a byte (two
-//    nibbles) indexes a 256-entry table whose entry holds the two codebook
-//    levels split into bf16 hi and lo parts (L = hi + lo + O(2^-18 L)).  The
-//    table is replicated 32 times in LDS so that lane l always reads the
-//    bank pair 2*(l%32): lookups are free of bank conflicts for any data.
-//  * x is split the same way (prep kernel), and three bf16 MFMAs
-//    (xh*Lh + xl*Lh + xh*Ll, fp32 accumulate) give each product to about
-//    2^-16 relative -- far inside the 1e-4 parity bar -- at bf16 MFMA rate.
-//  * The 64-element block scale is applied once per block to the MFMA
-//    partial (scale hoisting): lane l's outputs all belong to weight row
-//    l%16, so one scale decode per lane per block.
-// Layout of one wave's work unit: 16 weight rows (MFMA N) x 16 batch rows
-// (MFMA M, zero-padded) x one 64-element block (two K=32 MFMA steps).  Lane
-// group g = l/16 supplies elements {8g..8g+7} and {32+8g..32+8g+7} of the
-// block: two dword loads per lane.  A workgroup (8 waves) owns 16 rows and
-// interleaves the row's blocks over its waves; partial tiles are reduced in
-// LDS in a fixed order.
+// Two kernels:
+//  * k_dprep -- one workgroup per 256-element line of K.  It splits X into
+//    bf16 hi/lo parts laid out as MFMA A-fragments, computes the line's
+//    partial of T1, and the last workgroup to finish (atomic ticket, no
+//    waiting) sums the partials in line order: T1 is deterministic.
+//  * k_dmain -- the weight stream.  A workgroup owns 16 weight rows; its 4
+//    waves split K into contiguous line ranges.  Per line, lane (n, g)
+//    (n = lane % 16, g = lane / 16) loads bytes [16g, 16g+16) and
+//    [64+16g, 64+16g+16) of row n's 128-byte line: every load instruction
+//    reads 16 rows x 64 contiguous bytes.  Two v_permlane32_swap per 16 bytes
+//    regroup the dwords so that each K=32 MFMA step covers 32 elements of ONE
+//    64-element block (one scale per output column per step; k-slot order
+//    step_koff below).  Nibbles become bf16 hi/lo operands by LDS table
+//    lookup (L = Lh + Ll + O(2^-18 L)); three bf16 MFMAs
+//    (xh*Lh + xl*Lh + xh*Ll, fp32 accumulate) give each product to ~2^-16
+//    relative.  The block scale multiplies the per-block MFMA partial once.
+// The double-quant scale decode c*(absmax/127) is within 1 ulp of
+// quant.rs:218's fl(fl(c/127)*absmax); it only enters this sum, never a
+// stored weight.
+#include <algorithm>
+#include <type_traits>
+
 #include "qh_internal.h"
-#include "qh_nf4.h"
 
 namespace qh {
 namespace {
@@ -35,10 +37,8 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kCopies = 32;
-constexpr int kDepth = 4;  // blocks loaded together per wave
+constexpr int kLine = 256;  // elements per line (128 code bytes)
+constexpr int kWaves = 4;
 
 constexpr uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
 constexpr float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -47,43 +47,48 @@ constexpr uint32_t bf16_rne(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-struct PairTable {
-  uint32_t hi[256], lo[256];
+// Codebook (quant.rs:27-44) split into bf16 hi + lo parts.
+//  nib[c]  = Lh[c] | Ll[c] << 16                      (one nibble)
+//  pair[b] = {Lh[b&15] | Lh[b>>4] << 16, Ll[b&15] | Ll[b>>4] << 16}  (one byte)
+struct Tables {
+  uint32_t nib[16];
+  uint32_t pair[256][2];  // {hi, lo}: the LDS layout, copied as is
 };
 
-constexpr PairTable make_pair_table() {
-  PairTable t{};
+constexpr Tables make_tables() {
+  Tables t{};
   constexpr float L[16] = {
       -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
       -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
       0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
       0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
       0.7229568362236023f, 1.0f};
-  for (int v = 0; v < 256; ++v) {
-    uint32_t h[2] = {0, 0}, l[2] = {0, 0};
-    for (int q = 0; q < 2; ++q) {
-      const float x = L[q == 0 ? (v & 15) : (v >> 4)];
-      h[q] = bf16_rne(x);
-      l[q] = bf16_rne(x - u2f(h[q] << 16));
-    }
-    t.hi[v] = h[0] | (h[1] << 16);
-    t.lo[v] = l[0] | (l[1] << 16);
+  uint32_t h[16] = {}, l[16] = {};
+  for (int c = 0; c < 16; ++c) {
+    h[c] = bf16_rne(L[c]);
+    l[c] = bf16_rne(L[c] - u2f(h[c] << 16));
+    t.nib[c] = h[c] | (l[c] << 16);
+  }
+  for (int b = 0; b < 256; ++b) {
+    t.pair[b][0] = h[b & 15] | (h[b >> 4] << 16);
+    t.pair[b][1] = l[b & 15] | (l[b >> 4] << 16);
   }
   return t;
 }
 
-__constant__ PairTable c_pairs = make_pair_table();
+__constant__ Tables c_tab = make_tables();
+
+// Element offset, within its 256-element line, of the 8 k-slots that lane
+// group g supplies in MFMA step s (0..7): step s covers block s/2.
+__host__ __device__ constexpr int step_koff(int s, int g) {
+  return 64 * (s >> 1) + 32 * (g & 1) + 8 * (2 * (s & 1) + (g >> 1));
+}
 
 __device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
   const uint32_t u = __float_as_uint(f);
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// ---------------------------------------------------------------------------
-// Prep: X -> (Xh, Xl) bf16 split, and T1 = X A^T.  grid = (max(r,1), M),
-// 256 threads: workgroup (j, m) splits its 1/gridDim.x share of X row m and,
-// if r > 0, computes T1[m][j] over the whole K.  Loads are issued in
-// unconditional batches of 8 per thread (clamped index, zero weight).
 template <int XBF16>
 __device__ __forceinline__ float4 load_x4(const void *x, int64_t e) {
   if (XBF16) {
@@ -94,258 +99,953 @@ __device__ __forceinline__ float4 load_x4(const void *x, int64_t e) {
   return *(const float4 *)((const float *)x + e);
 }
 
-template <int XBF16>
-__global__ __launch_bounds__(256) void k_decode_prep(
-    const void *__restrict__ x, int M, int64_t K, const float *__restrict__ a,
-    int r, uint16_t *__restrict__ xh, uint16_t *__restrict__ xl,
-    float *__restrict__ t1) {
-  __shared__ float red[4];
-  const int j = blockIdx.x, J = gridDim.x, m = blockIdx.y, tid = threadIdx.x;
-  const int64_t units = K >> 3;  // 8-element units of row m
-  const int64_t u0 = units * j / J, u1 = xh ? units * (j + 1) / J : u0;
-  for (int64_t u = u0 + tid; u < u1; u += 256) {
-    const int64_t e = (int64_t)m * K + u * 8;
-    const float4 p0 = load_x4<XBF16>(x, e), p1 = load_x4<XBF16>(x, e + 4);
-    const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-    uint32_t hw[4], lw[4];
+// Sum 16 values over the 64 lanes of a wave; lane l returns the total of
+// value (l >> 2) & 15 (valid in lanes whose low two bits are 0).
+__device__ __forceinline__ float reduce16(float (&v)[16]) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t h0 = bf16_bits_rne(v[2 * q]), h1 = bf16_bits_rne(v[2 * q + 1]);
-      const uint32_t l0 = bf16_bits_rne(v[2 * q] - __uint_as_float(h0 << 16));
-      const uint32_t l1 = bf16_bits_rne(v[2 * q + 1] - __uint_as_float(h1 << 16));
-      hw[q] = h0 | (h1 << 16);
-      lw[q] = l0 | (l1 << 16);
+  for (int half = 8, off = 32; half >= 1; half >>= 1, off >>= 1) {
+    const bool up = (lane & off) != 0;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      // Select between two named values: written as array subscripts the
+      // compiler turns the select into a dynamic index over all 16.
+      const float lo = v[i], hi = v[i + half];
+      const float keep = up ? hi : lo;
+      const float send = up ? lo : hi;
+      v[i] = keep + __shfl_xor(send, off);
     }
-    *(uint4 *)(xh + e) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    *(uint4 *)(xl + e) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  }
+  float s = v[0];
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 1);
+  return s;
+}
+
+// Index (in uint4 units) of the A-fragment of (line, step, part, m, g);
+// part 0 = hi, 1 = lo.  One line holds kFragsPerLine * M uint4.
+constexpr int kFragsPerLine = 8 * 2 * 4;
+__device__ __forceinline__ int64_t frag_index(int64_t line, int s, int part, int M, int m, int g) {
+  return ((line * 8 + s) * 2 + part) * (int64_t)M * 4 + m * 4 + g;
+}
+
+// Device-coherent (agent scope) stores and loads: they reach the point of
+// coherence shared by all XCDs without writing back or invalidating whole
+// caches.  A producer's stores are complete once its `s_waitcnt` returns,
+// which happens before its ticket increment; a consumer loads only after
+// its own ticket increment returned the final count.
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+  return __uint_as_float(
+      __hip_atomic_load((unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+// Ends a workgroup's partial: waits for its device stores, then takes a
+// ticket; returns true in every thread of the last of `total` workgroups,
+// which also resets the counter for the next launch.
+__device__ __forceinline__ bool last_arrival(unsigned *counter, unsigned total, int *flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = atomicAdd(counter, 1u);
+    *flag = old == total - 1;
+    if (old == total - 1) atomicExch(counter, 0u);
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+
+constexpr int kRedFloats = 8192;  // LDS of the prep's final T1 reduction
+constexpr int kRedBatch = 16;     // loads in flight per thread there
+
+// ---------------------------------------------------------------------------
+// Prep: grid = K / 256 workgroups of 256 threads (workgroup c = line c).
+template <int XBF16>
+__global__ __launch_bounds__(256) void k_dprep(const void *__restrict__ x, int M, int64_t K,
+                                               const float *__restrict__ a, int r,
+                                               uint4 *__restrict__ xf, float *__restrict__ t1p,
+                                               float *__restrict__ t1,
+                                               unsigned *__restrict__ ticket) {
+  __shared__ int last;
+  __shared__ float red[kRedFloats];
+  const int c = blockIdx.x, P = gridDim.x, tid = threadIdx.x, lane = tid & 63,
+            wave = tid >> 6;
+  const int64_t k0 = (int64_t)c * kLine;
+  // 1. A-fragments of X for this line (bf16 X is its own hi part).
+  for (int idx = tid; idx < M * 32; idx += 256) {
+    const int m = idx >> 5, u = idx & 31, s = u >> 2, g = u & 3;
+    const int64_t e = (int64_t)m * K + k0 + step_koff(s, g);
+    uint4 hi, lo = make_uint4(0, 0, 0, 0);
+    if (XBF16) {
+      hi = *(const uint4 *)((const uint16_t *)x + e);
+    } else {
+      const float4 p0 = *(const float4 *)((const float *)x + e);
+      const float4 p1 = *(const float4 *)((const float *)x + e + 4);
+      const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t h0 = bf16_bits_rne(v[2 * q]), h1 = bf16_bits_rne(v[2 * q + 1]);
+        const uint32_t l0 = bf16_bits_rne(v[2 * q] - __uint_as_float(h0 << 16));
+        const uint32_t l1 = bf16_bits_rne(v[2 * q + 1] - __uint_as_float(h1 << 16));
+        hw[q] = h0 | (h1 << 16);
+        lw[q] = l0 | (l1 << 16);
+      }
+      hi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      lo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    }
+    xf[frag_index(c, s, 0, M, m, g)] = hi;
+    if (!XBF16) xf[frag_index(c, s, 1, M, m, g)] = lo;
   }
   if (r == 0) return;
-  const int64_t nk4 = K >> 2;
-  const float4 *a4 = (const float4 *)(a + (int64_t)j * K);
-  float s = 0.0f;
-  for (int64_t base = tid; base < nk4; base += 256 * 8) {
-    float4 xv[8], av[8];
-    float ok[8];
+  // 2. This line's partial of T1[m][j]: a lane covers 4 elements; rows j of
+  //    A are spread over the waves (all loads issued first); the 16 padded
+  //    batch rows are reduced at once.
+  float4 xv[16], av[16];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t k4 = base + 256 * q;
-      ok[q] = k4 < nk4 ? 1.0f : 0.0f;
-      const int64_t kc = k4 < nk4 ? k4 : 0;
-      av[q] = a4[kc];
-      xv[q] = load_x4<XBF16>(x, (int64_t)m * K + 4 * kc);
+  for (int m = 0; m < 16; ++m)
+    xv[m] = m < M ? load_x4<XBF16>(x, (int64_t)m * K + k0 + 4 * lane)
+                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int j = wave + kWaves * q;
+    av[q] = j < r ? *(const float4 *)(a + (int64_t)j * K + k0 + 4 * lane)
+                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int j = wave + kWaves * q;
+    if (kWaves * q >= r) break;  // uniform: q stays a compile-time index
+    float p[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      float t = xv[m].x * av[q].x;
+      t = fmaf(xv[m].y, av[q].y, t);
+      t = fmaf(xv[m].z, av[q].z, t);
+      p[m] = fmaf(xv[m].w, av[q].w, t);
     }
-    __builtin_amdgcn_sched_barrier(0);  // loads stay batched ahead of uses
+    const float s = reduce16(p);
+    const int m = lane >> 2;
+    if ((lane & 3) == 0 && m < M && j < r) st_dev(t1p + ((int64_t)c * M + m) * r + j, s);
+  }
+  // 3. The last workgroup to arrive sums the partials in line order.  The
+  //    partials go through LDS in output chunks; every thread issues its
+  //    loads of a chunk together.
+  if (!last_arrival(ticket, (unsigned)P, &last)) return;
+  const int MR = M * r;
+  const int oc = MR < kRedFloats / P ? MR : (kRedFloats / P > 0 ? kRedFloats / P : 1);
+  for (int o0 = 0; o0 < MR; o0 += oc) {
+    const int on = MR - o0 < oc ? MR - o0 : oc;
+    const int cnt = P * on;  // partial (cc, o) at red[cc * on + (o - o0)]
+    for (int base = 0; base < cnt; base += 256 * kRedBatch) {
+      float v[kRedBatch];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      float p = xv[q].x * av[q].x;
-      p = fmaf(xv[q].y, av[q].y, p);
-      p = fmaf(xv[q].z, av[q].z, p);
-      p = fmaf(xv[q].w, av[q].w, p);
-      s = fmaf(p, ok[q], s);
+      for (int q = 0; q < kRedBatch; ++q) {
+        int i = base + tid + 256 * q;
+        i = i < cnt ? i : cnt - 1;
+        v[q] = ld_dev(t1p + (int64_t)(i / on) * MR + o0 + i % on);
+      }
+#pragma unroll
+      for (int q = 0; q < kRedBatch; ++q) {
+        const int i = base + tid + 256 * q;
+        if (i < cnt) red[i] = v[q];
+      }
+    }
+    __syncthreads();
+    for (int o = tid; o < on; o += 256) {
+      float sum = 0.0f;
+      for (int cc = 0; cc < P; ++cc) sum += red[cc * on + o];
+      t1[o0 + o] = sum;
+    }
+    __syncthreads();
+  }
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and
+// lgkmcnt at their "no wait" maxima).
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Copies n 16-byte (W16) or 4-byte units from global to LDS with
+// global_load_lds: no VGPR round trip, so nothing for the compiler to sink
+// next to a use.  The LDS destination of a wave is its first lane's slot
+// (wave-uniform, in M0); the caller waits (vmcnt) and syncs before reading.
+// Straight-line code (at most MAXIT exec-masked copies per thread, 256
+// threads): a loop would hide the number of later loads from the
+// compiler's wait-count tracking.
+template <bool W16, int MAXIT>
+__device__ __forceinline__ void copy_to_lds(void *lds, const void *src, int n) {
+  using Unit = typename std::conditional<W16, uint4, uint32_t>::type;
+  typedef __attribute__((address_space(3))) void lds_void;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int q = 0; q < MAXIT; ++q) {
+    const int i = threadIdx.x + 256 * q;
+    if (i < n) {
+      const void *g = (const Unit *)src + i;
+      lds_void *l = (lds_void *)((Unit *)lds + (i - lane));
+      if (W16)
+        __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(g, l, 4, 0, 0);
     }
   }
-  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-  if ((tid & 63) == 0) red[tid >> 6] = s;
-  __syncthreads();
-  if (tid == 0) t1[m * r + j] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // ---------------------------------------------------------------------------
-template <int XLO, int KIND>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_decode(
-    DevQW w, int M, const uint16_t *__restrict__ xh,
-    const uint16_t *__restrict__ xl, const float *__restrict__ t1,
-    const float *__restrict__ lb, int r, float s_lora, float *__restrict__ y) {
-  __shared__ uint2 tab[256 * kCopies];  // 64 KB; reused for the epilogue
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t N = w.rows, K = w.cols, KB = K >> 6;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
+struct LineRegs {
+  uint4 c0, c1;  // code bytes [16g, 16g+16) and [64+16g, ...) of row n
+  uint4 sf;      // KIND 0: 4 fp32 block scales; KIND 1: .x = 4 int8 codes
+};
 
-  // Replicate the pair table: each thread writes copies of one byte's entry.
+template <int KIND>
+__device__ __forceinline__ void load_line(LineRegs &R, const DevQW &w, int64_t n, int64_t KB,
+                                          const uint8_t *crow, int64_t L, int g) {
+  R.c0 = *(const uint4 *)(crow + L * 128 + 16 * g);
+  R.c1 = *(const uint4 *)(crow + L * 128 + 64 + 16 * g);
+  const int64_t b = n * KB + 4 * L;
+  if (KIND == 0) {
+    R.sf = *(const uint4 *)(w.scales + b);
+  } else {
+    R.sf.x = *(const uint32_t *)(w.scale_codes + b);
+    R.sf.y = R.sf.z = R.sf.w = 0;
+  }
+}
+
+// LDS operands of one 64-element block (MFMA steps 2j and 2j+1).
+struct BlockOps {
+  uint32_t h[2][4], l[2][4];  // weight hi / lo bf16 pairs per step
+  uint4 xh[2], xl[2];         // A-fragments (X hi / lo) per step
+};
+
+template <int XLO, int TAB>
+__device__ __forceinline__ void fetch_block(BlockOps &o, const uint32_t (&sw)[8], int j,
+                                            const uint4 *xl, int part, int xo,
+                                            const uint32_t *tab1, const uint2 *tab2) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int s = 2 * j + t;
+    const uint32_t wd = sw[s];
+    if (TAB == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint2 e = tab2[(wd >> (8 * i)) & 255u];
+        o.h[t][i] = e.x;
+        o.l[t][i] = e.y;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t t0 = tab1[(wd >> (8 * i)) & 15u];
+        const uint32_t t1 = tab1[(wd >> (8 * i + 4)) & 15u];
+        o.h[t][i] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+        o.l[t][i] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+      }
+    }
+    o.xh[t] = xl[s * 2 * part + xo];
+    o.xl[t] = XLO ? xl[s * 2 * part + part + xo] : make_uint4(0, 0, 0, 0);
+  }
+}
+
+template <int XLO>
+__device__ __forceinline__ floatx4 mfma_block(const BlockOps &o) {
+  floatx4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const bf16x8 bh = __builtin_bit_cast(bf16x8, make_uint4(o.h[t][0], o.h[t][1], o.h[t][2], o.h[t][3]));
+    const bf16x8 bl = __builtin_bit_cast(bf16x8, make_uint4(o.l[t][0], o.l[t][1], o.l[t][2], o.l[t][3]));
+    const bf16x8 ah = __builtin_bit_cast(bf16x8, o.xh[t]);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, d, 0, 0, 0);
+    if (XLO) {
+      const bf16x8 al = __builtin_bit_cast(bf16x8, o.xl[t]);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, d, 0, 0, 0);
+    }
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, d, 0, 0, 0);
+  }
+  return d;
+}
+
+// One line of one 16-row group: xl points at the line's staged A-fragments
+// (hi parts at [s*2*M*4], lo parts M*4 further).  The LDS operands of block
+// j+1 are requested before block j's MFMAs so their latency overlaps.
+template <int XLO, int KIND, int TAB>
+__device__ __forceinline__ void compute_line(const LineRegs &R, float amax, const uint4 *xl,
+                                             int M, int xo, const uint32_t *tab1,
+                                             const uint2 *tab2, floatx4 &acc) {
+  uint32_t sw[8];
   {
-    constexpr int kPer = 256 * kCopies / kThreads;
-    const int v = tid / (kCopies / kPer), c0 = (tid % (kCopies / kPer)) * kPer;
-    const uint2 e = make_uint2(c_pairs.hi[v], c_pairs.lo[v]);
-#pragma unroll
-    for (int c = 0; c < kPer; ++c) tab[v * kCopies + c0 + c] = e;
+    auto p = __builtin_amdgcn_permlane32_swap(R.c0.x, R.c0.y, false, false);
+    sw[0] = p[0];
+    sw[2] = p[1];
+    p = __builtin_amdgcn_permlane32_swap(R.c0.z, R.c0.w, false, false);
+    sw[1] = p[0];
+    sw[3] = p[1];
+    p = __builtin_amdgcn_permlane32_swap(R.c1.x, R.c1.y, false, false);
+    sw[4] = p[0];
+    sw[6] = p[1];
+    p = __builtin_amdgcn_permlane32_swap(R.c1.z, R.c1.w, false, false);
+    sw[5] = p[0];
+    sw[7] = p[1];
   }
-  __syncthreads();
-  // LoRA epilogue operands (16 rows of B, and T1): loaded before the main
-  // loop, consumed after it, so their latency hides behind it.
-  float lbv[2] = {0.0f, 0.0f}, t1v[2] = {0.0f, 0.0f};
+  const float amax127 = amax * (1.0f / 127.0f);
+  const int part = M * 4;
+  BlockOps ops[2];
+  fetch_block<XLO, TAB>(ops[0], sw, 0, xl, part, xo, tab1, tab2);
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int idx = tid + q * kThreads;
-    if (idx < 16 * r) {
-      int64_t row = n0 + idx / r;
-      row = row < N ? row : N - 1;
-      lbv[q] = lb[row * r + idx % r];
+  for (int j = 0; j < 4; ++j) {
+    if (j < 3) fetch_block<XLO, TAB>(ops[(j + 1) & 1], sw, j + 1, xl, part, xo, tab1, tab2);
+    const floatx4 d = mfma_block<XLO>(ops[j & 1]);
+    float sc;
+    if (KIND == 0) {
+      sc = __uint_as_float(j == 0 ? R.sf.x : j == 1 ? R.sf.y : j == 2 ? R.sf.z : R.sf.w);
+    } else {
+      sc = (float)(int8_t)((R.sf.x >> (8 * j)) & 255u) * amax127;
     }
-    if (idx < M * r) t1v[q] = t1[idx];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = fmaf(sc, d[v], acc[v]);
   }
+}
 
-  const int i = lane & 15, g = lane >> 4;
-  const int64_t n = (n0 + i < N) ? n0 + i : N - 1;
-  const uint32_t *c32 = (const uint32_t *)w.codes + n * (K >> 3);
-  const int copy = lane & 31;
-  const bool xrow = i < M;
-  const uint16_t *xhr = xh + (int64_t)i * K + 8 * g;
-  const uint16_t *xlr = xl + (int64_t)i * K + 8 * g;
+constexpr int kRing = 4;       // code lines per wave, all loaded up front
+constexpr int kStage = 12;     // staged A-fragment uint4 per thread (48 KB)
+constexpr int kMaxSplits = 8;   // K split the grid-size target may ask for
+constexpr int kSplitBatch = 8;  // slice partials loaded together
 
+// Main: grid = ntiles * S workgroups of 256 threads; workgroup (tile, slice)
+// covers rows [16 tile, 16 tile + 16) and lines [NL slice / S, NL (slice+1) / S).
+// Dynamic LDS: the slice's A-fragments (lines * kFragsPerLine * M uint4),
+// reused by the epilogue.
+template <int XLO, int KIND, int TAB>
+__global__ __launch_bounds__(256) void k_dmain(DevQW w, int M, int S, const uint4 *__restrict__ xf,
+                                               const float *__restrict__ t1,
+                                               const float *__restrict__ lb, int r,
+                                               float s_lora, float *__restrict__ part,
+                                               unsigned *__restrict__ counters,
+                                               float *__restrict__ y) {
+  extern __shared__ uint4 xs[];
+  __shared__ uint2 tab2[TAB == 1 ? 256 : 1];
+  __shared__ uint32_t tab1[16];
+  __shared__ float lbs[16 * 64];  // rows n0.. of B (16 x r)
+  __shared__ float t1s[16 * 64];  // T1 (M x r)
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t N = w.rows, K = w.cols, KB = K >> 6, NL = K / kLine;
+  const int64_t ntiles = (N + 15) / 16;
+  const int64_t tile = blockIdx.x % ntiles, slice = blockIdx.x / ntiles;
+  const int64_t n0 = tile * 16;
+  const int64_t SL0 = NL * slice / S, SL1 = NL * (slice + 1) / S, nls = SL1 - SL0;
+  const int64_t wl0 = SL0 + nls * wave / kWaves, wl1 = SL0 + nls * (wave + 1) / kWaves;
+  const int64_t nw = wl1 - wl0;
+
+  const int nl = lane & 15, g = lane >> 4;
+  const int64_t n = n0 + nl < N ? n0 + nl : N - 1;
+  const uint8_t *crow = w.codes + n * (K >> 1);
+
+  // Load order matters: vmcnt retires loads in issue order.  The slice's
+  // A-fragments and the LoRA epilogue operands (L2-resident, small) go to
+  // LDS first, then every code line of this wave (<= kRing of them: each
+  // line's MFMAs wait only for its own bytes).
+  // Every LDS fill of the prologue is a global_load_lds: an ordinary LDS
+  // store here would make the compiler wait for all of them (and, in
+  // issue order, for the code lines behind them).
+  if (TAB == 1)
+    copy_to_lds<true, 1>(tab2, c_tab.pair, 128);
+  else
+    copy_to_lds<false, 1>(tab1, c_tab.nib, 16);
+  const int64_t per_line = kFragsPerLine * (int64_t)M;
+  copy_to_lds<true, kStage>(xs, xf + SL0 * per_line, (int)(nls * per_line));
+  const int nrows = (int)(N - n0 < 16 ? N - n0 : 16);
+  if (r > 0) {
+    copy_to_lds<false, 4>(lbs, lb + n0 * r, nrows * r);
+    copy_to_lds<false, 4>(t1s, t1, M * r);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the code loads stay behind the copies
+  // absmax: a 256-block group spans 64 lines of a row, so the wave's lines
+  // see at most two values (loaded before the lines: the first line needs
+  // them).
+  float am0 = 0.0f, am1 = 0.0f;
+  if (KIND == 1) {
+    const int64_t lf = nw > 0 ? wl0 : SL0, ll = nw > 0 ? wl1 - 1 : SL0;
+    am0 = w.absmax[(n * KB + 4 * lf) >> 8];
+    am1 = w.absmax[(n * KB + 4 * ll) >> 8];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  LineRegs R[kRing];
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) {
+    const int64_t L = wl0 + d;
+    load_line<KIND>(R[d], w, n, KB, crow, L < wl1 ? L : (nw > 0 ? wl1 - 1 : SL0), g);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Wait for the LDS copies only: the kAfter loads issued after them (the
+  // code lines) stay in flight through the barrier.
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(KIND == 1 ? 3 * kRing + 2 : 3 * kRing));
+  __builtin_amdgcn_s_barrier();  // no fence: a fence would wait for everything
+
+  // A-fragment rows m >= M only reach output rows that are discarded:
+  // those lanes read row M-1's fragment instead of branching.
+  const int xo = (nl < M ? nl : M - 1) * 4 + g;
   floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int64_t kb0 = wave; kb0 < KB; kb0 += kWaves * kDepth) {
-    // Issue every load of kDepth blocks before using any of them: raw scale
-    // fields are decoded only at use so no wait sits between the loads.
-    uint32_t cw[kDepth][2];
-    float sa[kDepth], okm[kDepth];
-    int32_t sq[kDepth];
-    uint4 ah[kDepth][2], al[kDepth][2];
+  const int64_t g0 = (n * KB + 4 * (nw > 0 ? wl0 : SL0)) >> 8;
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      const int64_t kb = kb0 + (int64_t)d * kWaves;
-      const bool ok = kb < KB;
-      const int64_t kbc = ok ? kb : 0;
-      okm[d] = ok ? 1.0f : 0.0f;
-      cw[d][0] = c32[kbc * 8 + g];
-      cw[d][1] = c32[kbc * 8 + 4 + g];
-      const int64_t b = n * KB + kbc;
-      if (KIND == 0) {
-        sa[d] = w.scales[b];
-        sq[d] = 0;
-      } else {
-        sq[d] = (int8_t)w.scale_codes[b];
-        sa[d] = w.absmax[b >> 8];
-      }
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        ah[d][t] = make_uint4(0, 0, 0, 0);
-        al[d][t] = make_uint4(0, 0, 0, 0);
-        if (xrow) {
-          ah[d][t] = *(const uint4 *)(xhr + kbc * 64 + 32 * t);
-          if (XLO) al[d][t] = *(const uint4 *)(xlr + kbc * 64 + 32 * t);
-        }
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);  // loads stay batched ahead of uses
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      floatx4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        uint32_t bh[4], bl[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint2 e = tab[((cw[d][t] >> (8 * q)) & 255u) * kCopies + copy];
-          bh[q] = e.x;
-          bl[q] = e.y;
-        }
-        const bf16x8 Bh = __builtin_bit_cast(bf16x8, make_uint4(bh[0], bh[1], bh[2], bh[3]));
-        const bf16x8 Bl = __builtin_bit_cast(bf16x8, make_uint4(bl[0], bl[1], bl[2], bl[3]));
-        const bf16x8 Ah = __builtin_bit_cast(bf16x8, ah[d][t]);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bh, c, 0, 0, 0);
-        if (XLO) {
-          const bf16x8 Al = __builtin_bit_cast(bf16x8, al[d][t]);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bh, c, 0, 0, 0);
-        }
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bl, c, 0, 0, 0);
-      }
-      // block scale (within 1 ulp of quant.rs:218's decode; only the GEMV
-      // sum depends on it, never a stored weight)
-      const float sc = (KIND == 0 ? sa[d] : (float)sq[d] * (sa[d] * (1.0f / 127.0f))) * okm[d];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] = fmaf(sc, c[v], acc[v]);
+  for (int d = 0; d < kRing; ++d) {
+    if (d < nw) {
+      const float amax = ((n * KB + 4 * (wl0 + d)) >> 8) == g0 ? am0 : am1;
+      compute_line<XLO, KIND, TAB>(R[d], amax, xs + (wl0 + d - SL0) * kFragsPerLine * M, M,
+                                   xo, tab1, tab2, acc);
     }
   }
 
-  // Lane holds D[batch 4g+v][row i]; reduce the waves in LDS (fixed order).
+  // Epilogue.  Lane holds D[batch 4g+v][row nl]; waves reduce in LDS in a
+  // fixed order.  The staged fragments are dead: reuse their LDS.
   __syncthreads();
-  float *red = (float *)tab;          // kWaves x 256 floats
-  float *lbs = red + kWaves * 256;    // 16 x r
-  float *t1s = lbs + 16 * 64;         // M x r
+  float *red = (float *)xs;  // kWaves x 256
 #pragma unroll
-  for (int v = 0; v < 4; ++v) red[wave * 256 + (4 * g + v) * 16 + i] = acc[v];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int idx = tid + q * kThreads;
-    if (idx < 16 * r) lbs[idx] = lbv[q];
-    if (idx < M * r) t1s[idx] = t1v[q];
-  }
+  for (int v = 0; v < 4; ++v) red[wave * 256 + (4 * g + v) * 16 + nl] = acc[v];
   __syncthreads();
-  if (tid < 256) {
-    const int bm = tid >> 4, ri = tid & 15;
-    const int64_t nn = n0 + ri;
-    if (bm < M && nn < N) {
-      float sum = 0.0f;
+  const int bm = tid >> 4, ri = tid & 15;
+  const int64_t nn = n0 + ri;
+  const bool mine = bm < M && nn < N;
+  float sum = 0.0f;
+  if (mine) sum = (red[tid] + red[256 + tid]) + (red[512 + tid] + red[768 + tid]);
+  if (S > 1) {
+    if (mine) st_dev(part + (slice * M + bm) * N + nn, sum);
+    if (!last_arrival(counters + tile, (unsigned)S, &last)) return;
+    if (!mine) return;
+    sum = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += kSplitBatch) {
+      float v[kSplitBatch];
 #pragma unroll
-      for (int wv = 0; wv < kWaves; ++wv) sum += red[wv * 256 + tid];
-      if (r > 0) {
-        float l = 0.0f;
-        for (int j = 0; j < r; ++j) l += t1s[bm * r + j] * lbs[ri * r + j];
-        sum += s_lora * l;
+      for (int q = 0; q < kSplitBatch; ++q) {
+        const int64_t sl = s0 + q < S ? s0 + q : S - 1;
+        v[q] = ld_dev(part + (sl * M + bm) * N + nn);
       }
-      y[(int64_t)bm * N + nn] = sum;
+#pragma unroll
+      for (int q = 0; q < kSplitBatch; ++q)
+        if (s0 + q < S) sum += v[q];
     }
   }
+  if (!mine) return;
+  if (r > 0) {
+    float l = 0.0f;
+    for (int j = 0; j < r; ++j) l = fmaf(t1s[bm * r + j], lbs[ri * r + j], l);
+    sum = fmaf(s_lora, l, sum);
+  }
+  y[(int64_t)bm * N + nn] = sum;
+}
+
+// ===========================================================================
+// Small-batch decode (at most 8 rows): k_t1p + k_dsmall.
+//
+// MFMA operand packing.  The A-fragment rows carry both bf16 parts of X:
+// row m < M holds hi(x_m) and row M+m holds lo(x_m) = bf16(x_m - hi).  The B
+// operand interleaves the weight's parts exactly as the byte-pair table
+// stores them, [Lh_a Lh_b Ll_a Ll_b Lh_c Lh_d Ll_c Ll_d] for elements a..d,
+// and the A slots repeat each element to match, [q_a q_b q_a q_b q_c q_d q_c
+// q_d].  One MFMA therefore accumulates q*(Lh+Ll) over 4 elements in every
+// row, and y[m] = D[m] + D[M+m] = (xh+xl)(Lh+Ll) minus the negligible
+// xl*Ll term: two MFMAs per 8 elements per lane, table entries used in place.
+//
+// k_t1p writes one partial of T1 = X A^T per 256-element line of K; the GEMV
+// kernel loads those partials in its prologue (after its code loads, so they
+// never delay the weight stream) and sums them in line order in its
+// epilogue.  Its workgroups are (16-row tile, K slice); a tile's last slice
+// to finish adds the slices (fixed order) and the LoRA term.
+constexpr int kFusedMaxM = 8;
+constexpr int kSmallRouteMaxM = 2;
+constexpr int kFusedUnits = 4;  // X-conversion units (4 elements) per thread
+// T1 partials prefetched per thread: covers NL * M * r <= 256 * 4M, i.e.
+// K <= 16384 at r = 16; the rest is read in the epilogue.
+template <int M>
+constexpr int t1_prefetch() { return 4 * M; }
+
+// Fragment index (uint4) of (line-in-slice ll, step s, half p, row rho, group g).
+__device__ __forceinline__ int ffrag(int ll, int s, int p, int M2, int rho, int g) {
+  return ((ll * 8 + s) * 2 + p) * (M2 * 4) + rho * 4 + g;
+}
+
+template <int XBF16>
+__device__ __forceinline__ void load_x4_any(const void *x, int64_t e, float (&v)[4]) {
+  const float4 t = load_x4<XBF16>(x, e);
+  v[0] = t.x;
+  v[1] = t.y;
+  v[2] = t.z;
+  v[3] = t.w;
+}
+
+template <int KIND>
+__device__ __forceinline__ void compute_line2(const LineRegs &R, float amax, float valid,
+                                              const uint4 *xl, int M2, int xo,
+                                              const uint2 *tab2, floatx4 &acc) {
+  uint32_t sw[8];
+  {
+    auto p = __builtin_amdgcn_permlane32_swap(R.c0.x, R.c0.y, false, false);
+    sw[0] = p[0];
+    sw[2] = p[1];
+    p = __builtin_amdgcn_permlane32_swap(R.c0.z, R.c0.w, false, false);
+    sw[1] = p[0];
+    sw[3] = p[1];
+    p = __builtin_amdgcn_permlane32_swap(R.c1.x, R.c1.y, false, false);
+    sw[4] = p[0];
+    sw[6] = p[1];
+    p = __builtin_amdgcn_permlane32_swap(R.c1.z, R.c1.w, false, false);
+    sw[5] = p[0];
+    sw[7] = p[1];
+  }
+  const float amax127 = amax * (1.0f / 127.0f) * valid;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    floatx4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int s = 2 * j + t;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const uint2 e0 = tab2[(sw[s] >> (16 * p)) & 255u];
+        const uint2 e1 = tab2[(sw[s] >> (16 * p + 8)) & 255u];
+        const bf16x8 b = __builtin_bit_cast(bf16x8, make_uint4(e0.x, e0.y, e1.x, e1.y));
+        const bf16x8 a = __builtin_bit_cast(bf16x8, xl[(s * 2 + p) * (M2 * 4) + xo]);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, d, 0, 0, 0);
+      }
+    }
+    float sc;
+    if (KIND == 0) {
+      sc = __uint_as_float(j == 0 ? R.sf.x : j == 1 ? R.sf.y : j == 2 ? R.sf.z : R.sf.w) *
+           valid;
+    } else {
+      sc = (float)(int8_t)((R.sf.x >> (8 * j)) & 255u) * amax127;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = fmaf(sc, d[v], acc[v]);
+  }
+}
+
+// T1 partial of line c (workgroup c of K / 256): a lane covers
+// 4 elements, rows j of A are spread over the waves; every load is issued
+// before the first use.
+template <int XBF16, int M>
+__global__ __launch_bounds__(256) void k_t1p(const void *__restrict__ x, int64_t K,
+                                             const float *__restrict__ a, int r,
+                                             float *__restrict__ t1p) {
+  const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t k = (int64_t)c * kLine + 4 * lane;
+  float4 xv[M], av[16];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xv[m] = load_x4<XBF16>(x, (int64_t)m * K + k);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int j = wave + kWaves * q;
+    av[q] = j < r ? *(const float4 *)(a + (int64_t)j * K + k)
+                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int j = wave + kWaves * q;
+    if (kWaves * q >= r) break;  // uniform: q stays a compile-time index
+    float p[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      p[m] = 0.0f;
+      if (m < M) {
+        float t = xv[m].x * av[q].x;
+        t = fmaf(xv[m].y, av[q].y, t);
+        t = fmaf(xv[m].z, av[q].z, t);
+        p[m] = fmaf(xv[m].w, av[q].w, t);
+      }
+    }
+    const float s = reduce16(p);
+    const int m = lane >> 2;
+    if ((lane & 3) == 0 && m < M && j < r) t1p[((int64_t)c * M + m) * r + j] = s;
+  }
+}
+
+// grid = ntiles * S workgroups of 256 threads.  Dynamic LDS: the slice's
+// A-fragments (lines * 128 * M uint4), reused by the epilogue.
+template <int XBF16, int KIND, int M>
+__global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__restrict__ x,
+                                                const float *__restrict__ t1p,
+                                                const float *__restrict__ lb, int r,
+                                                float s_lora, float *__restrict__ part,
+                                                unsigned *__restrict__ counters,
+                                                float *__restrict__ t1_out,
+                                                float *__restrict__ y) {
+  extern __shared__ uint4 xs[];
+  __shared__ uint2 tab2[256];
+  __shared__ float lbs[16 * 64];
+  __shared__ float t1s[kFusedMaxM * 64];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t N = w.rows, K = w.cols, KB = K >> 6, NL = K / kLine;
+  const int64_t ntiles = (N + 15) / 16;
+  const int64_t tile = blockIdx.x % ntiles, slice = blockIdx.x / ntiles;
+  const int64_t n0 = tile * 16;
+  const int64_t SL0 = NL * slice / S, SL1 = NL * (slice + 1) / S, nls = SL1 - SL0;
+  const int64_t wl0 = SL0 + nls * wave / kWaves, wl1 = SL0 + nls * (wave + 1) / kWaves;
+  const int64_t nw = wl1 - wl0;
+  const int M2 = 2 * M;
+  const int nl = lane & 15, g = lane >> 4;
+  const int64_t n = n0 + nl < N ? n0 + nl : N - 1;
+  const uint8_t *crow = w.codes + n * (K >> 1);
+
+  // Prologue, all straight-line: loads issue in the order their data is
+  // needed (vmcnt retires in order): codebook table and this slice's X,
+  // then the wave's code lines and scales, then the LoRA rows of B.
+  const uint2 tv = make_uint2(c_tab.pair[tid][0], c_tab.pair[tid][1]);
+  // Unit u = t * 4M + (m * 4 + gg) with t = 16 ll + 2 s + p: 4 elements of
+  // row m for lane group gg in half p of step s of line ll.
+  const int units = (int)(nls * 64) * M;
+  float xv[kFusedUnits][4];
+#pragma unroll
+  for (int q = 0; q < kFusedUnits; ++q) {
+    int u = tid + 256 * q;
+    u = u < units ? u : units - 1;
+    const int t = u / (4 * M), wi = u % (4 * M);
+    const int ll = t >> 4, s = (t >> 1) & 7, p = t & 1, m = wi >> 2, gg = wi & 3;
+    const int64_t e = (int64_t)m * K + (SL0 + ll) * kLine + step_koff(s, gg) + 4 * p;
+    load_x4_any<XBF16>(x, e, xv[q]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float am0 = 0.0f, am1 = 0.0f;
+  if (KIND == 1) {
+    const int64_t lf = nw > 0 ? wl0 : SL0, ll = nw > 0 ? wl1 - 1 : SL0;
+    am0 = w.absmax[(n * KB + 4 * lf) >> 8];
+    am1 = w.absmax[(n * KB + 4 * ll) >> 8];
+  }
+  LineRegs R[kRing];
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) {
+    const int64_t L = wl0 + d;
+    load_line<KIND>(R[d], w, n, KB, crow, L < wl1 ? L : (nw > 0 ? wl1 - 1 : SL0), g);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int rr = r > 0 ? r : 1;
+  float lbv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (r > 0) {  // without an adapter lb is NULL
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int idx = tid + 256 * q;
+      const int i16 = idx < 16 * r ? idx : 16 * r - 1;
+      int64_t row = n0 + i16 / r;
+      row = row < N ? row : N - 1;
+      lbv[q] = lb[row * r + i16 % r];
+    }
+  }
+  // T1 partials (P = NL lines x M*r): the first 256 * kT1Pre are loaded now.
+  const int MR = M * r, PMR = (int)NL * MR;
+  constexpr int kT1Pre = t1_prefetch<M>();
+  float t1v[kT1Pre];
+  if (r > 0) {
+#pragma unroll
+    for (int q = 0; q < kT1Pre; ++q) {
+      const int i = tid + 256 * q;
+      t1v[q] = t1p[i < PMR ? i : PMR - 1];
+    }
+  }
+  // Convert X: hi part to row m, lo part to row M+m, elements repeated in
+  // pairs to match the interleaved B operand.
+#pragma unroll
+  for (int q = 0; q < kFusedUnits; ++q) {
+    int u = tid + 256 * q;
+    u = u < units ? u : units - 1;
+    const int t = u / (4 * M), wi = u % (4 * M);
+    uint32_t h[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = bf16_bits_rne(xv[q][i]);
+      lo[i] = XBF16 ? 0u : bf16_bits_rne(xv[q][i] - __uint_as_float(h[i] << 16));
+    }
+    const uint32_t h01 = h[0] | (h[1] << 16), h23 = h[2] | (h[3] << 16);
+    const uint32_t l01 = lo[0] | (lo[1] << 16), l23 = lo[2] | (lo[3] << 16);
+    xs[t * (8 * M) + wi] = make_uint4(h01, h01, h23, h23);          // row m
+    xs[t * (8 * M) + 4 * M + wi] = make_uint4(l01, l01, l23, l23);  // row M + m
+  }
+  tab2[tid] = tv;
+  __syncthreads();
+
+  // A-fragment rows >= 2M only reach discarded output rows: read row 2M-1.
+  const int xo = (nl < M2 ? nl : M2 - 1) * 4 + g;
+  const int64_t g0 = (n * KB + 4 * (nw > 0 ? wl0 : SL0)) >> 8;
+  // Straight-line over the ring (no branch per line: a branch makes the
+  // compiler shuffle ring registers that still have loads in flight); a
+  // padded line past the wave's range contributes with scale 0.
+  floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) {
+    const int64_t L = d < nw ? wl0 + d : (nw > 0 ? wl1 - 1 : SL0);
+    const float amax = ((n * KB + 4 * L) >> 8) == g0 ? am0 : am1;
+    compute_line2<KIND>(R[d], amax, d < nw ? 1.0f : 0.0f,
+                        xs + ffrag((int)(L - SL0), 0, 0, M2, 0, 0), M2, xo, tab2, acc);
+  }
+
+  // Epilogue: waves reduce in LDS (fixed order), rows m and M+m add up.
+  __syncthreads();
+  float *red = (float *)xs;           // kWaves x 256
+  float *t1all = red + kWaves * 256;  // the prefetched T1 partials
+#pragma unroll
+  for (int v = 0; v < 4; ++v) red[wave * 256 + (4 * g + v) * 16 + nl] = acc[v];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int idx = tid + 256 * q;
+    lbs[idx < 16 * rr ? idx : 16 * rr - 1] = lbv[q];
+  }
+  if (r > 0) {
+#pragma unroll
+    for (int q = 0; q < kT1Pre; ++q) {
+      const int i = tid + 256 * q;
+      if (i < PMR) t1all[i] = t1v[q];
+    }
+  }
+  __syncthreads();
+  const int bm = tid >> 4, ri = tid & 15;
+  const int64_t nn = n0 + ri;
+  const bool mine = bm < M && nn < N;
+  float sum = 0.0f;
+  if (mine) {
+    const int hi = bm * 16 + ri, lo = (M + bm) * 16 + ri;
+    sum = ((red[hi] + red[256 + hi]) + (red[512 + hi] + red[768 + hi])) +
+          ((red[lo] + red[256 + lo]) + (red[512 + lo] + red[768 + lo]));
+  }
+  bool finisher = true;
+  if (S > 1) {
+    if (mine) st_dev(part + (slice * M + bm) * N + nn, sum);
+    finisher = last_arrival(counters + tile, (unsigned)S, &last);
+    if (finisher && mine) {
+      sum = 0.0f;
+      for (int s0 = 0; s0 < S; s0 += kSplitBatch) {
+        float v[kSplitBatch];
+#pragma unroll
+        for (int q = 0; q < kSplitBatch; ++q) {
+          const int64_t sl = s0 + q < S ? s0 + q : S - 1;
+          v[q] = ld_dev(part + (sl * M + bm) * N + nn);
+        }
+#pragma unroll
+        for (int q = 0; q < kSplitBatch; ++q)
+          if (s0 + q < S) sum += v[q];
+      }
+    }
+  }
+  if (!finisher) return;
+  if (r > 0) {
+    // T1[o] = sum of the NL line partials in line order (partials past the
+    // prefetched ones are read now).
+    if (tid < MR) {
+      float t = 0.0f;
+      for (int c = 0; c < (int)NL; ++c) {
+        const int i = c * MR + tid;
+        t += i < 256 * kT1Pre ? t1all[i] : t1p[i];
+      }
+      t1s[tid] = t;
+      if (t1_out && tile == 0) t1_out[tid] = t;
+    }
+    __syncthreads();
+    if (mine) {
+      float l = 0.0f;
+      for (int j = 0; j < r; ++j) l = fmaf(t1s[bm * r + j], lbs[ri * r + j], l);
+      sum = fmaf(s_lora, l, sum);
+    }
+  }
+  if (mine) y[(int64_t)bm * N + nn] = sum;
+}
+
+template <int M>
+hipError_t run_small(const DevQW &w, int x_bf16, int S, const void *x, const float *t1p,
+                     const float *lb, int r, float s, float *part, unsigned *counters,
+                     float *t1_out, float *y, dim3 grid, uint32_t lds, hipStream_t st) {
+  if (x_bf16) {
+    if (w.kind == 0)
+      return qh_launch(k_dsmall<1, 0, M>, grid, dim3(256), lds, st, w, S, x, t1p, lb, r, s,
+                       part, counters, t1_out, y);
+    return qh_launch(k_dsmall<1, 1, M>, grid, dim3(256), lds, st, w, S, x, t1p, lb, r, s, part,
+                     counters, t1_out, y);
+  }
+  if (w.kind == 0)
+    return qh_launch(k_dsmall<0, 0, M>, grid, dim3(256), lds, st, w, S, x, t1p, lb, r, s, part,
+                     counters, t1_out, y);
+  return qh_launch(k_dsmall<0, 1, M>, grid, dim3(256), lds, st, w, S, x, t1p, lb, r, s, part,
+                   counters, t1_out, y);
+}
+
+template <int M>
+hipError_t run_t1p(int x_bf16, const void *x, int64_t K, const float *a, int r, float *t1p,
+                   hipStream_t st) {
+  const dim3 grid((unsigned)(K / kLine));
+  if (x_bf16) return qh_launch(k_t1p<1, M>, grid, dim3(256), 0, st, x, K, a, r, t1p);
+  return qh_launch(k_t1p<0, M>, grid, dim3(256), 0, st, x, K, a, r, t1p);
+}
+
+int g_decode_table = 0;     // 0 = nibble table, 1 = byte-pair table
+int g_split_target = 512;  // workgroups the K split aims for
+
+// Split of K over workgroups: the grid reaches g_split_target workgroups
+// (at most kMaxSplits slices for that), and more slices are taken while a
+// slice's staged A-fragments exceed 256 * kStage uint4 of LDS or a wave
+// would own more than kRing lines.
+int64_t decode_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t NL = K / kLine, ntiles = (N + 15) / 16;
+  int64_t s = (g_split_target + ntiles - 1) / ntiles;
+  if (s > kMaxSplits) s = kMaxSplits;
+  if (s > NL) s = NL;
+  if (s < 1) s = 1;
+  while (s < NL && ((NL + s - 1) / s * kFragsPerLine * M > 256 * kStage ||
+                    (NL + s - 1) / s > kWaves * kRing))
+    ++s;
+  return s;
+}
+
+size_t main_lds_bytes(int64_t M, int64_t K, int64_t S) {
+  const int64_t NL = K / kLine;
+  const int64_t lines = (NL + S - 1) / S;
+  size_t b = (size_t)lines * kFragsPerLine * M * 16;
+  const size_t epi = kWaves * 256 * 4;  // wave reduction
+  return b > epi ? b : epi;
+}
+
+template <int XLO, int KIND>
+hipError_t run_main(const DevQW &w, int M, int S, const uint4 *xf, const float *t1,
+                    const float *lb, int r, float s, float *part, unsigned *counters, float *y,
+                    hipStream_t st) {
+  const int64_t ntiles = (w.rows + 15) / 16;
+  const dim3 grid((unsigned)(ntiles * S));
+  const uint32_t lds = (uint32_t)main_lds_bytes(M, w.cols, S);
+  if (g_decode_table == 1)
+    return qh_launch(k_dmain<XLO, KIND, 1>, grid, dim3(256), lds, st, w, M, S, xf, t1, lb, r, s,
+                     part, counters, y);
+  return qh_launch(k_dmain<XLO, KIND, 0>, grid, dim3(256), lds, st, w, M, S, xf, t1, lb, r, s,
+                   part, counters, y);
+}
+
+struct DecodeScratch {
+  uint4 *xf;
+  float *t1p, *t1, *part;
+};
+
+size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+DecodeScratch carve(void *scratch, int64_t M, int64_t N, int64_t K, int64_t r) {
+  const int64_t P = K / kLine;
+  const size_t xs = round256((size_t)P * kFragsPerLine * M * 16);
+  const size_t ps = round256((size_t)P * M * (r ? r : 1) * 4);
+  const size_t ts = round256((size_t)M * (r ? r : 1) * 4);
+  (void)N;
+  DecodeScratch d;
+  d.xf = (uint4 *)scratch;
+  d.t1p = (float *)((char *)scratch + xs);
+  d.t1 = (float *)((char *)scratch + xs + ps);
+  d.part = (float *)((char *)scratch + xs + ps + ts);
+  return d;
+}
+
+// Small-batch split: a slice's fragments (2 KB per line per batch row) stay
+// within 32 KB and its X conversion within kFusedUnits units per thread,
+// waves own at most kRing lines, and the grid aims at g_split_target.
+int64_t fused_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t NL = K / kLine, ntiles = (N + 15) / 16;
+  int64_t s = (g_split_target + ntiles - 1) / ntiles;
+  if (s > kMaxSplits) s = kMaxSplits;
+  if (s > NL) s = NL;
+  if (s < 1) s = 1;
+  while (s < NL && ((NL + s - 1) / s * M > 16 || (NL + s - 1) / s > kWaves * kRing)) ++s;
+  return s;
 }
 
 }  // namespace
 
+void set_decode_table(int t) { g_decode_table = t ? 1 : 0; }
+void set_decode_split_target(int t) { g_split_target = t > 0 ? t : 512; }
+
 bool decode_ok(const DevQW &w, int64_t M, int64_t r) {
-  return M >= 1 && M <= 16 && r <= 64 && w.bs == 64 && w.cols % 256 == 0 &&
-         (((uintptr_t)w.codes) & 3) == 0;
+  return M >= 1 && M <= 16 && r <= 64 && w.bs == 64 && w.cols % kLine == 0 &&
+         (w.rows + 15) / 16 <= kDecodeMaxTiles && (((uintptr_t)w.codes) & 15) == 0 &&
+         (w.kind == 0 ? (((uintptr_t)w.scales) & 15) == 0
+                      : (((uintptr_t)w.scale_codes) & 3) == 0);
 }
 
-size_t decode_scratch_bytes(int64_t M, int64_t K, int64_t r) {
-  const size_t xs = ((size_t)M * K * 2 + 255) / 256 * 256;
-  return 2 * xs + (size_t)M * (r ? r : 1) * 4 + 256;
+size_t decode_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t r) {
+  const int64_t P = K / kLine, S = decode_splits(M, N, K);
+  return round256((size_t)P * kFragsPerLine * M * 16) + round256((size_t)P * M * (r ? r : 1) * 4) +
+         round256((size_t)M * (r ? r : 1) * 4) + round256((size_t)S * M * N * 4);
+}
+
+bool decode_small_ok(const DevQW &w, int64_t M, int64_t r) {
+  // Batches of 3..8 rows are supported by the kernels but measured faster
+  // on the prep + main path, so the router only sends 1 and 2 here.
+  return decode_ok(w, M, r) && M <= kSmallRouteMaxM && M * r <= 256;
+}
+
+size_t decode_small_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t r) {
+  const int64_t NL = K / kLine, S = fused_splits(M, N, K);
+  return round256((size_t)NL * M * (r ? r : 1) * 4) + round256((size_t)S * M * N * 4);
+}
+
+#define QH_SMALL_CASES(F) \
+  F(1) F(2) F(3) F(4) F(5) F(6) F(7) F(8)
+
+hipError_t launch_decode_t1(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                            const float *a, int64_t r, void *scratch, hipStream_t st) {
+  if (r == 0) return hipSuccess;
+  float *t1p = (float *)scratch;
+  switch (M) {
+#define QH_CASE(m) \
+  case m: return run_t1p<m>(x_bf16, x, w.cols, a, (int)r, t1p, st);
+    QH_SMALL_CASES(QH_CASE)
+#undef QH_CASE
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_decode_small(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                               const float *lb, int64_t r, float s, float *y, float *t1_out,
+                               void *scratch, unsigned *tickets, hipStream_t st) {
+  const int64_t N = w.rows, K = w.cols, NL = K / kLine;
+  const int64_t S = fused_splits(M, N, K);
+  const float *t1p = (const float *)scratch;
+  float *part = (float *)((char *)scratch + round256((size_t)NL * M * (r ? r : 1) * 4));
+  const int64_t lines = (NL + S - 1) / S;
+  const size_t epi = (size_t)(kWaves * 256 + 256 * 4 * M) * 4;  // t1_prefetch<M>()
+  const uint32_t lds = (uint32_t)std::max<size_t>((size_t)lines * 128 * M * 16, epi);
+  const dim3 grid((unsigned)(((N + 15) / 16) * S));
+  unsigned *counters = tickets + kDecodeTileCounterBase;
+  switch (M) {
+#define QH_CASE(m) \
+  case m:          \
+    return run_small<m>(w, x_bf16, (int)S, x, t1p, lb, (int)r, s, part, counters, t1_out, y, grid, lds, st);
+    QH_SMALL_CASES(QH_CASE)
+#undef QH_CASE
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_decode_prep(const DevQW &w, const void *x, int x_bf16, int64_t M,
                               const float *a, int64_t r, float *t1_out, void *scratch,
-                              hipStream_t st) {
+                              unsigned *tickets, hipStream_t st) {
   const int64_t K = w.cols;
-  const size_t xs = ((size_t)M * K * 2 + 255) / 256 * 256;
-  uint16_t *xh = (uint16_t *)scratch;
-  uint16_t *xl = (uint16_t *)((char *)scratch + xs);
-  float *t1 = t1_out ? t1_out : (float *)((char *)scratch + 2 * xs);
-  const dim3 grid((unsigned)(r > 0 ? r : 8), (unsigned)M);
+  const DecodeScratch d = carve(scratch, M, w.rows, K, r);
+  float *t1 = t1_out ? t1_out : d.t1;
+  const dim3 grid((unsigned)(K / kLine));
   if (x_bf16)
-    return qh_launch(k_decode_prep<1>, grid, dim3(256), 0, st, x, (int)M, K, a, (int)r,
-                     xh, xl, t1);
-  return qh_launch(k_decode_prep<0>, grid, dim3(256), 0, st, x, (int)M, K, a, (int)r,
-                   xh, xl, t1);
+    return qh_launch(k_dprep<1>, grid, dim3(256), 0, st, x, (int)M, K, a, (int)r, d.xf,
+                     d.t1p, t1, tickets);
+  return qh_launch(k_dprep<0>, grid, dim3(256), 0, st, x, (int)M, K, a, (int)r, d.xf, d.t1p,
+                   t1, tickets);
 }
 
-hipError_t launch_lora_t1(const void *x, int x_bf16, int64_t M, int64_t K, const float *a,
-                          int64_t r, float *t1, hipStream_t st) {
-  if (M == 0 || r == 0) return hipSuccess;
-  const dim3 grid((unsigned)r, (unsigned)M);
-  uint16_t *none = nullptr;
-  if (x_bf16)
-    return qh_launch(k_decode_prep<1>, grid, dim3(256), 0, st, x, (int)M, K, a, (int)r,
-                     none, none, t1);
-  return qh_launch(k_decode_prep<0>, grid, dim3(256), 0, st, x, (int)M, K, a, (int)r,
-                   none, none, t1);
-}
-
-hipError_t launch_decode(const DevQW &w, int x_bf16, int64_t M, const float *lb,
-                         int64_t r, float s, float *y, const float *t1_out, void *scratch,
-                         hipStream_t st) {
-  const int64_t K = w.cols, N = w.rows;
-  const size_t xs = ((size_t)M * K * 2 + 255) / 256 * 256;
-  uint16_t *xh = (uint16_t *)scratch;
-  uint16_t *xl = (uint16_t *)((char *)scratch + xs);
-  const float *t1 = t1_out ? t1_out : (const float *)((char *)scratch + 2 * xs);
-  dim3 grid((unsigned)((N + 15) / 16));
-  const dim3 blk(kThreads);
+hipError_t launch_decode(const DevQW &w, int x_bf16, int64_t M, const float *lb, int64_t r,
+                         float s, float *y, const float *t1_out, void *scratch,
+                         unsigned *tickets, hipStream_t st) {
+  const DecodeScratch d = carve(scratch, M, w.rows, w.cols, r);
+  const float *t1 = t1_out ? t1_out : d.t1;
+  const int S = (int)decode_splits(M, w.rows, w.cols);
+  unsigned *counters = tickets + kDecodeTileCounterBase;
   if (x_bf16) {
     if (w.kind == 0)
-      return qh_launch(k_decode<0, 0>, grid, blk, 0, st, w, (int)M, xh, xl, t1, lb, (int)r, s, y);
-    return qh_launch(k_decode<0, 1>, grid, blk, 0, st, w, (int)M, xh, xl, t1, lb, (int)r, s, y);
+      return run_main<0, 0>(w, (int)M, S, d.xf, t1, lb, (int)r, s, d.part, counters, y, st);
+    return run_main<0, 1>(w, (int)M, S, d.xf, t1, lb, (int)r, s, d.part, counters, y, st);
   }
   if (w.kind == 0)
-    return qh_launch(k_decode<1, 0>, grid, blk, 0, st, w, (int)M, xh, xl, t1, lb, (int)r, s, y);
-  return qh_launch(k_decode<1, 1>, grid, blk, 0, st, w, (int)M, xh, xl, t1, lb, (int)r, s, y);
+    return run_main<1, 0>(w, (int)M, S, d.xf, t1, lb, (int)r, s, d.part, counters, y, st);
+  return run_main<1, 1>(w, (int)M, S, d.xf, t1, lb, (int)r, s, d.part, counters, y, st);
 }
 
 }  // namespace qh

@@ -70,8 +70,11 @@ __device__ __forceinline__ float reduce16(float (&v)[16]) {
     const bool up = (lane & off) != 0;
 #pragma unroll
     for (int i = 0; i < half; ++i) {
-      const float keep = up ? v[i + half] : v[i];
-      const float send = up ? v[i] : v[i + half];
+      // Select between two named values: written as array subscripts the
+      // compiler turns the select into a dynamic index over all 16.
+      const float lo = v[i], hi = v[i + half];
+      const float keep = up ? hi : lo;
+      const float send = up ? lo : hi;
       v[i] = keep + __shfl_xor(send, off);
     }
   }
@@ -191,6 +194,52 @@ __global__ __launch_bounds__(256) void k_gemv(DevQW w, const void *__restrict__ 
   }
 }
 
+// T1[m][j] = sum_k x[m][k] a[j][k] for the GEMV path: workgroup (j, m) owns
+// one output; loads are issued in unconditional batches of 8 per thread
+// (clamped index, zero weight).  Needs K % 4 == 0 and 16-byte aligned rows.
+template <int XBF16>
+__global__ __launch_bounds__(256) void k_lora_t1(const void *__restrict__ x, int64_t K,
+                                                 const float *__restrict__ a, int r,
+                                                 float *__restrict__ t1) {
+  __shared__ float red[4];
+  const int j = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+  const int64_t nk4 = K >> 2;
+  const float4 *a4 = (const float4 *)(a + (int64_t)j * K);
+  float s = 0.0f;
+  for (int64_t base = tid; base < nk4; base += 256 * 8) {
+    float4 xv[8], av[8];
+    float ok[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t k4 = base + 256 * q;
+      ok[q] = k4 < nk4 ? 1.0f : 0.0f;
+      const int64_t kc = k4 < nk4 ? k4 : 0;
+      av[q] = a4[kc];
+      const int64_t e = (int64_t)m * K + 4 * kc;
+      if (XBF16) {
+        const uint2 u = *(const uint2 *)((const uint16_t *)x + e);
+        xv[q] = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                            __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+      } else {
+        xv[q] = *(const float4 *)((const float *)x + e);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // loads stay batched ahead of uses
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float p = xv[q].x * av[q].x;
+      p = fmaf(xv[q].y, av[q].y, p);
+      p = fmaf(xv[q].z, av[q].z, p);
+      p = fmaf(xv[q].w, av[q].w, p);
+      s = fmaf(p, ok[q], s);
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) t1[m * r + j] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 template <int M, int XB>
 hipError_t run_gemv(const DevQW &w, const void *x, const float *t1, const float *lb,
                     int64_t r, float s, float *y, hipStream_t st) {
@@ -212,6 +261,14 @@ hipError_t run_gemv_dt(const DevQW &w, const void *x, int xb, const float *t1,
 bool gemv_ok(const DevQW &w, int64_t M) {
   return M >= 1 && M <= 4 && w.bs == 64 && w.cols % 64 == 0 &&
          (((uintptr_t)w.codes) & 7) == 0;
+}
+
+hipError_t launch_lora_t1(const void *x, int x_bf16, int64_t M, int64_t K, const float *a,
+                          int64_t r, float *t1, hipStream_t st) {
+  if (M == 0 || r == 0) return hipSuccess;
+  const dim3 grid((unsigned)r, (unsigned)M);
+  if (x_bf16) return qh_launch(k_lora_t1<1>, grid, dim3(256), 0, st, x, K, a, (int)r, t1);
+  return qh_launch(k_lora_t1<0>, grid, dim3(256), 0, st, x, K, a, (int)r, t1);
 }
 
 hipError_t launch_gemv(const DevQW &w, const void *x, int x_bf16, int64_t M,

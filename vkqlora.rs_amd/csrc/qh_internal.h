@@ -99,25 +99,41 @@ hipError_t launch_gemv(const DevQW &w, const void *x, int x_bf16, int64_t M,
                        const float *t1, const float *lb, int64_t r, float s,
                        float *y, hipStream_t st);
 bool gemv_ok(const DevQW &w, int64_t M);
-// out[m][j] = sum_k x[m][k] * a[j][k]  (T1 for small batches)
-hipError_t launch_dot_rows(const void *x, int x_bf16, const float *a,
-                           int64_t M, int64_t K, int64_t r, float *out,
-                           hipStream_t st);
-
-// ---- k_decode.hip ----
-// Decode path (batch <= 16): X split + T1 partials, then the MFMA GEMV with
-// the LoRA epilogue.  t1_out (optional) receives T1 = X A^T.
-bool decode_ok(const DevQW &w, int64_t M, int64_t r);
-size_t decode_scratch_bytes(int64_t M, int64_t K, int64_t r);
-hipError_t launch_decode_prep(const DevQW &w, const void *x, int x_bf16, int64_t M,
-                              const float *a, int64_t r, float *t1_out, void *scratch,
-                              hipStream_t st);
-// T1 = X A^T for small batches (K % 8 == 0, 16-byte aligned rows).
+// T1 = X A^T for the GEMV path (K % 4 == 0, 16-byte aligned rows).
 hipError_t launch_lora_t1(const void *x, int x_bf16, int64_t M, int64_t K, const float *a,
                           int64_t r, float *t1, hipStream_t st);
+
+// ---- k_decode.hip ----
+// Decode path (batch <= 16): X split into MFMA fragments + T1 (prep), then
+// the MFMA GEMV with the LoRA epilogue.  t1_out (optional) receives
+// T1 = X A^T.  `tickets` is the context's zero-initialised counter array of
+// kTicketWords words; every kernel leaves its counters at zero, and calls
+// sharing it must be stream-ordered.
+constexpr int kTicketWords = 16384;
+constexpr int kDecodeTileCounterBase = 64;
+constexpr int64_t kDecodeMaxTiles = kTicketWords - kDecodeTileCounterBase;
+bool decode_ok(const DevQW &w, int64_t M, int64_t r);
+size_t decode_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t r);
+hipError_t launch_decode_prep(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                              const float *a, int64_t r, float *t1_out, void *scratch,
+                              unsigned *tickets, hipStream_t st);
 hipError_t launch_decode(const DevQW &w, int x_bf16, int64_t M, const float *lb,
                          int64_t r, float s, float *y, const float *t1_out, void *scratch,
-                         hipStream_t st);
+                         unsigned *tickets, hipStream_t st);
+// Small-batch decode (batch <= 8, batch * r <= 256): T1 line partials
+// (launch_decode_t1, only when r > 0) then the packed-row MFMA GEMV.
+bool decode_small_ok(const DevQW &w, int64_t M, int64_t r);
+size_t decode_small_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t r);
+hipError_t launch_decode_t1(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                            const float *a, int64_t r, void *scratch, hipStream_t st);
+hipError_t launch_decode_small(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                               const float *lb, int64_t r, float s, float *y, float *t1_out,
+                               void *scratch, unsigned *tickets, hipStream_t st);
+// Tuning knobs of the decode GEMV: codebook table (0 = 16-entry nibble
+// table, 1 = 256-entry byte-pair table) and the workgroup count the K split
+// aims for.
+void set_decode_table(int t);
+void set_decode_split_target(int t);
 
 // ---- k_elem.hip ----
 hipError_t launch_axpy_inplace(float *y, const float *x, int64_t n,

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -24,6 +25,7 @@ using qh::Operand;
 namespace {
 
 thread_local std::string g_err;
+int g_decode_path = 0;  // 0 = fused decode where it applies, 1 = prep + main
 
 qh_status fail(qh_status st, const std::string &msg) {
   // Display formats of QloraError (qlora-core/src/error.rs:16-24).
@@ -118,6 +120,9 @@ struct qh_ctx {
   std::mutex mu;
   DevBuf stage[10];  // host-API staging
   DevBuf scratch;    // internal scratch of the fused paths
+  // Zero-initialised counters of kernels whose last workgroup finishes a
+  // reduction; each such kernel leaves its counter at zero again.
+  unsigned *tickets = nullptr;
   char name[256] = {0};
   bool timing = false;
   std::vector<TimedLaunch> pending;
@@ -359,13 +364,13 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   const float sc = lora ? l->alpha / (float)l->r : 0.0f;  // lora.rs:64-66
   const int xe = xdt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
   const bool fast = qh::nf4_fast_ok(W);
-  // Small batches: VALU GEMV (batch <= 4) or MFMA decode kernel (<= 16).
-  // Both take T1 = X A^T from the prep kernel, which needs 16-byte aligned
-  // rows of X and A.
+  // Small batches: the MFMA decode kernels (batch <= 16, K % 256 == 0), else
+  // the VALU GEMV (batch <= 4, K % 64 == 0).  Both take T1 = X A^T from a
+  // prep kernel, which needs 16-byte aligned rows of X and A.
   const bool aligned = (((uintptr_t)x) & 15) == 0 && (K % 8) == 0 &&
                        (!lora || (((uintptr_t)l->a) & 15) == 0);
-  const bool gemv = aligned && r <= 64 && qh::gemv_ok(W, M);
-  const bool decode = aligned && !gemv && qh::decode_ok(W, M, r);
+  const bool decode = aligned && qh::decode_ok(W, M, r);
+  const bool gemv = aligned && !decode && r <= 64 && qh::gemv_ok(W, M);
 
   if (gemv) {
     Carve cg;
@@ -381,17 +386,34 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     return;
   }
 
+  if (decode && g_decode_path == 0 && qh::decode_small_ok(W, M, r)) {
+    Carve cd;
+    size_t i_sc = cd.add(qh::decode_small_scratch_bytes(M, N, K, r));
+    auto pd = cd.bind(ctx->scratch);
+    const int xb = xe == qh::E_BF16;
+    if (lora)
+      timed(ctx, "decode_t1", s, [&] {
+        return qh::launch_decode_t1(W, x, xb, M, l->a, r, pd[i_sc], s);
+      });
+    timed(ctx, "decode_small", s, [&] {
+      return qh::launch_decode_small(W, x, xb, M, lora ? l->b : nullptr, r, sc, y, t1_out,
+                                     pd[i_sc], ctx->tickets, s);
+    });
+    return;
+  }
+
   if (decode) {
     Carve cd;
-    size_t i_sc = cd.add(qh::decode_scratch_bytes(M, K, r));
+    size_t i_sc = cd.add(qh::decode_scratch_bytes(M, N, K, r));
     auto pd = cd.bind(ctx->scratch);
     const int xb = xe == qh::E_BF16;
     timed(ctx, "decode_prep", s, [&] {
       return qh::launch_decode_prep(W, x, xb, M, lora ? l->a : nullptr, r, t1_out, pd[i_sc],
-                                    s);
+                                    ctx->tickets, s);
     });
     timed(ctx, "decode", s, [&] {
-      return qh::launch_decode(W, xb, M, lora ? l->b : nullptr, r, sc, y, t1_out, pd[i_sc], s);
+      return qh::launch_decode(W, xb, M, lora ? l->b : nullptr, r, sc, y, t1_out, pd[i_sc],
+                               ctx->tickets, s);
     });
     return;
   }
@@ -576,11 +598,19 @@ qh_status qh_ctx_create(qh_ctx **out) {
   qh_ctx *c = new (std::nothrow) qh_ctx();
   if (!c) return fail(QH_ERR_GPU, "host allocation failed");
   if (hipGetDevice(&c->device) != hipSuccess) c->device = 0;
+  if (const char *t = getenv("QH_DECODE_TABLE")) qh::set_decode_table(atoi(t));
+  if (const char *t = getenv("QH_DECODE_SPLIT_TARGET")) qh::set_decode_split_target(atoi(t));
+  if (const char *t = getenv("QH_DECODE_PATH")) g_decode_path = atoi(t);
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, c->device) == hipSuccess)
     snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
   if ((e = hipSetDevice(c->device)) != hipSuccess ||
-      (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+      (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipMalloc((void **)&c->tickets, qh::kTicketWords * 4)) != hipSuccess ||
+      (e = hipMemset(c->tickets, 0, qh::kTicketWords * 4)) != hipSuccess ||
+      (e = hipDeviceSynchronize()) != hipSuccess) {
+    if (c->tickets) (void)hipFree(c->tickets);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return fail(QH_ERR_GPU, hipGetErrorString(e));
   }
@@ -597,6 +627,7 @@ void qh_ctx_destroy(qh_ctx *ctx) {
   }
   for (auto &b : ctx->stage) b.release();
   ctx->scratch.release();
+  if (ctx->tickets) (void)hipFree(ctx->tickets);
   delete ctx;
 }
 
