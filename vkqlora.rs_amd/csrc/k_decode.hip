@@ -408,7 +408,8 @@ __device__ __forceinline__ void compute_line(const LineRegs &R, float amax, cons
   }
 }
 
-constexpr int kRing = 4;       // code lines per wave, all loaded up front
+constexpr int kRing = 4;       // code lines per wave (at most)
+constexpr int kInFlight = 2;   // of which in flight at once (small-batch path)
 constexpr int kStage = 12;     // staged A-fragment uint4 per thread (48 KB)
 constexpr int kMaxSplits = 8;   // K split the grid-size target may ask for
 constexpr int kSplitBatch = 8;  // slice partials loaded together
@@ -555,7 +556,6 @@ __global__ __launch_bounds__(256) void k_dmain(DevQW w, int M, int S, const uint
 // to finish adds the slices (fixed order) and the LoRA term.
 constexpr int kFusedMaxM = 8;
 constexpr int kSmallRouteMaxM = 2;
-constexpr int kFusedUnits = 4;  // X-conversion units (4 elements) per thread
 // T1 partials prefetched per thread: covers NL * M * r <= 256 * 4M, i.e.
 // K <= 16384 at r = 16; the rest is read in the epilogue.
 template <int M>
@@ -672,7 +672,7 @@ __global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__re
                                                 float *__restrict__ t1_out,
                                                 float *__restrict__ y) {
   extern __shared__ uint4 xs[];
-  __shared__ uint2 tab2[256];
+  __shared__ uint2 tabs[kWaves][256];  // one codebook table per wave
   __shared__ float lbs[16 * 64];
   __shared__ float t1s[kFusedMaxM * 64];
   __shared__ int last;
@@ -680,6 +680,11 @@ __global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__re
   const int64_t N = w.rows, K = w.cols, KB = K >> 6, NL = K / kLine;
   const int64_t ntiles = (N + 15) / 16;
   const int64_t tile = blockIdx.x % ntiles, slice = blockIdx.x / ntiles;
+  // Until the epilogue every wave works alone: its own table copy, its own
+  // lines' A-fragments in its own LDS region, no workgroup barrier, so it
+  // starts on its first line as soon as its own loads land.
+  uint4 *xw = xs + wave * (kRing * 128 * M);
+  uint2 *tab2 = tabs[wave];
   const int64_t n0 = tile * 16;
   const int64_t SL0 = NL * slice / S, SL1 = NL * (slice + 1) / S, nls = SL1 - SL0;
   const int64_t wl0 = SL0 + nls * wave / kWaves, wl1 = SL0 + nls * (wave + 1) / kWaves;
@@ -689,23 +694,55 @@ __global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__re
   const int64_t n = n0 + nl < N ? n0 + nl : N - 1;
   const uint8_t *crow = w.codes + n * (K >> 1);
 
-  // Prologue, all straight-line: loads issue in the order their data is
-  // needed (vmcnt retires in order): codebook table and this slice's X,
-  // then the wave's code lines and scales, then the LoRA rows of B.
-  const uint2 tv = make_uint2(c_tab.pair[tid][0], c_tab.pair[tid][1]);
-  // Unit u = t * 4M + (m * 4 + gg) with t = 16 ll + 2 s + p: 4 elements of
-  // row m for lane group gg in half p of step s of line ll.
-  const int units = (int)(nls * 64) * M;
-  float xv[kFusedUnits][4];
+  // Prologue, all straight-line.  Phase 1: the codebook table and this
+  // wave's X, converted into A-fragments.  Phase 2: the wave's code lines
+  // and scales, then the LoRA operands of the epilogue (vmcnt retires loads
+  // in issue order, so each line's MFMAs wait only for that line).
+  uint2 tv[4];
 #pragma unroll
-  for (int q = 0; q < kFusedUnits; ++q) {
-    int u = tid + 256 * q;
+  for (int q = 0; q < 4; ++q)
+    tv[q] = make_uint2(c_tab.pair[lane + 64 * q][0], c_tab.pair[lane + 64 * q][1]);
+  // Unit u = t * 4M + (m * 4 + gg) with t = 16 ll + 2 s + p: 4 elements of
+  // row m for lane group gg in half p of step s of the wave's line ll.
+  constexpr int kUnits = kRing * M;  // per lane
+  const int units = (int)(nw > 0 ? nw : 1) * 64 * M;
+  float xv[kUnits][4];
+#pragma unroll
+  for (int q = 0; q < kUnits; ++q) {
+    int u = lane + 64 * q;
     u = u < units ? u : units - 1;
     const int t = u / (4 * M), wi = u % (4 * M);
     const int ll = t >> 4, s = (t >> 1) & 7, p = t & 1, m = wi >> 2, gg = wi & 3;
-    const int64_t e = (int64_t)m * K + (SL0 + ll) * kLine + step_koff(s, gg) + 4 * p;
+    const int64_t L = nw > 0 ? wl0 + ll : SL0;
+    const int64_t e = (int64_t)m * K + L * kLine + step_koff(s, gg) + 4 * p;
     load_x4_any<XBF16>(x, e, xv[q]);
   }
+  // Phase 1 ends here: the table and X have landed (they were alone in
+  // the memory pipeline, so they come back fast); only now do the code
+  // lines go out.  Issued first, they would queue the small loads of every
+  // later wave behind the weight stream.
+  // Convert X: hi part to row m, lo part to row M+m, elements repeated in
+  // pairs to match the interleaved B operand.
+#pragma unroll
+  for (int q = 0; q < 4; ++q) tab2[lane + 64 * q] = tv[q];
+#pragma unroll
+  for (int q = 0; q < kUnits; ++q) {
+    int u = lane + 64 * q;
+    u = u < units ? u : units - 1;
+    const int t = u / (4 * M), wi = u % (4 * M);
+    uint32_t h[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = bf16_bits_rne(xv[q][i]);
+      lo[i] = XBF16 ? 0u : bf16_bits_rne(xv[q][i] - __uint_as_float(h[i] << 16));
+    }
+    const uint32_t h01 = h[0] | (h[1] << 16), h23 = h[2] | (h[3] << 16);
+    const uint32_t l01 = lo[0] | (lo[1] << 16), l23 = lo[2] | (lo[3] << 16);
+    xw[t * (8 * M) + wi] = make_uint4(h01, h01, h23, h23);          // row m
+    xw[t * (8 * M) + 4 * M + wi] = make_uint4(l01, l01, l23, l23);  // row M + m
+  }
+  // A wave's LDS operations complete in order: its lookups see its writes.
+  __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_sched_barrier(0);
   float am0 = 0.0f, am1 = 0.0f;
   if (KIND == 1) {
@@ -713,12 +750,14 @@ __global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__re
     am0 = w.absmax[(n * KB + 4 * lf) >> 8];
     am1 = w.absmax[(n * KB + 4 * ll) >> 8];
   }
-  LineRegs R[kRing];
+  // The wave's lines stream through a ring of kInFlight registers sets:
+  // enough to keep HBM busy, short enough to keep the memory queues short.
+  auto line_of = [&](int d) -> int64_t {
+    return d < nw ? wl0 + d : (nw > 0 ? wl1 - 1 : SL0);
+  };
+  LineRegs R[kInFlight];
 #pragma unroll
-  for (int d = 0; d < kRing; ++d) {
-    const int64_t L = wl0 + d;
-    load_line<KIND>(R[d], w, n, KB, crow, L < wl1 ? L : (nw > 0 ? wl1 - 1 : SL0), g);
-  }
+  for (int d = 0; d < kInFlight; ++d) load_line<KIND>(R[d], w, n, KB, crow, line_of(d), g);
   __builtin_amdgcn_sched_barrier(0);
   const int rr = r > 0 ? r : 1;
   float lbv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -743,26 +782,6 @@ __global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__re
       t1v[q] = t1p[i < PMR ? i : PMR - 1];
     }
   }
-  // Convert X: hi part to row m, lo part to row M+m, elements repeated in
-  // pairs to match the interleaved B operand.
-#pragma unroll
-  for (int q = 0; q < kFusedUnits; ++q) {
-    int u = tid + 256 * q;
-    u = u < units ? u : units - 1;
-    const int t = u / (4 * M), wi = u % (4 * M);
-    uint32_t h[4], lo[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h[i] = bf16_bits_rne(xv[q][i]);
-      lo[i] = XBF16 ? 0u : bf16_bits_rne(xv[q][i] - __uint_as_float(h[i] << 16));
-    }
-    const uint32_t h01 = h[0] | (h[1] << 16), h23 = h[2] | (h[3] << 16);
-    const uint32_t l01 = lo[0] | (lo[1] << 16), l23 = lo[2] | (lo[3] << 16);
-    xs[t * (8 * M) + wi] = make_uint4(h01, h01, h23, h23);          // row m
-    xs[t * (8 * M) + 4 * M + wi] = make_uint4(l01, l01, l23, l23);  // row M + m
-  }
-  tab2[tid] = tv;
-  __syncthreads();
 
   // A-fragment rows >= 2M only reach discarded output rows: read row 2M-1.
   const int xo = (nl < M2 ? nl : M2 - 1) * 4 + g;
@@ -773,10 +792,13 @@ __global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__re
   floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int d = 0; d < kRing; ++d) {
-    const int64_t L = d < nw ? wl0 + d : (nw > 0 ? wl1 - 1 : SL0);
+    const int64_t L = line_of(d);
     const float amax = ((n * KB + 4 * L) >> 8) == g0 ? am0 : am1;
-    compute_line2<KIND>(R[d], amax, d < nw ? 1.0f : 0.0f,
-                        xs + ffrag((int)(L - SL0), 0, 0, M2, 0, 0), M2, xo, tab2, acc);
+    compute_line2<KIND>(R[d % kInFlight], amax, d < nw ? 1.0f : 0.0f,
+                        xw + ffrag((int)(L - (nw > 0 ? wl0 : SL0)), 0, 0, M2, 0, 0), M2, xo,
+                        tab2, acc);
+    if (d + kInFlight < kRing)  // compile-time: unrolled
+      load_line<KIND>(R[d % kInFlight], w, n, KB, crow, line_of(d + kInFlight), g);
   }
 
   // Epilogue: waves reduce in LDS (fixed order), rows m and M+m add up.
@@ -828,16 +850,26 @@ __global__ __launch_bounds__(256) void k_dsmall(DevQW w, int S, const void *__re
   }
   if (!finisher) return;
   if (r > 0) {
-    // T1[o] = sum of the NL line partials in line order (partials past the
-    // prefetched ones are read now).
-    if (tid < MR) {
-      float t = 0.0f;
-      for (int c = 0; c < (int)NL; ++c) {
-        const int i = c * MR + tid;
+    // T1[o] = sum of the NL line partials, in a fixed order: thread (o, q)
+    // of G = 256 / MR threads per output adds lines q, q+G, ...; the G
+    // sums then add up in q order (partials past the prefetched ones are
+    // read now).
+    const int G = 256 / MR, o = tid % MR, q = tid / MR;
+    float t = 0.0f;
+    if (q < G) {
+      for (int c = q; c < (int)NL; c += G) {
+        const int i = c * MR + o;
         t += i < 256 * kT1Pre ? t1all[i] : t1p[i];
       }
-      t1s[tid] = t;
-      if (t1_out && tile == 0) t1_out[tid] = t;
+    }
+    __syncthreads();  // t1all is read; reuse red[] for the G sums
+    if (q < G) red[q * MR + o] = t;
+    __syncthreads();
+    if (tid < MR) {
+      float u = 0.0f;
+      for (int c = 0; c < G; ++c) u += red[c * MR + tid];
+      t1s[tid] = u;
+      if (t1_out && tile == 0) t1_out[tid] = u;
     }
     __syncthreads();
     if (mine) {
@@ -937,16 +969,15 @@ DecodeScratch carve(void *scratch, int64_t M, int64_t N, int64_t K, int64_t r) {
   return d;
 }
 
-// Small-batch split: a slice's fragments (2 KB per line per batch row) stay
-// within 32 KB and its X conversion within kFusedUnits units per thread,
-// waves own at most kRing lines, and the grid aims at g_split_target.
+// Small-batch split: waves own at most kRing lines and the grid aims at
+// g_split_target workgroups (at most kMaxSplits slices for that).
 int64_t fused_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t NL = K / kLine, ntiles = (N + 15) / 16;
   int64_t s = (g_split_target + ntiles - 1) / ntiles;
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > NL) s = NL;
   if (s < 1) s = 1;
-  while (s < NL && ((NL + s - 1) / s * M > 16 || (NL + s - 1) / s > kWaves * kRing)) ++s;
+  while (s < NL && (NL + s - 1) / s > kWaves * kRing) ++s;
   return s;
 }
 
@@ -1002,9 +1033,8 @@ hipError_t launch_decode_small(const DevQW &w, const void *x, int x_bf16, int64_
   const int64_t S = fused_splits(M, N, K);
   const float *t1p = (const float *)scratch;
   float *part = (float *)((char *)scratch + round256((size_t)NL * M * (r ? r : 1) * 4));
-  const int64_t lines = (NL + S - 1) / S;
   const size_t epi = (size_t)(kWaves * 256 + 256 * 4 * M) * 4;  // t1_prefetch<M>()
-  const uint32_t lds = (uint32_t)std::max<size_t>((size_t)lines * 128 * M * 16, epi);
+  const uint32_t lds = (uint32_t)std::max<size_t>((size_t)kWaves * kRing * 128 * M * 16, epi);
   const dim3 grid((unsigned)(((N + 15) / 16) * S));
   unsigned *counters = tickets + kDecodeTileCounterBase;
   switch (M) {
