@@ -145,7 +145,7 @@ def decode_bench(args, ctx, torch, dev, QD):
         full_bytes = gemv_bytes + sum(4 * L["a"].numel() for L in layers)
         flops = sum(2 * batch * L["N"] * L["K"] + 2 * batch * r * (L["N"] + L["K"])
                     for L in layers)
-        main_name = next((k for k in ("decode_small", "decode", "gemv", "forward_gemm")
+        main_name = next((k for k in ("decode_stream", "decode_small", "decode", "gemv", "forward_gemm")
                           if k in kern), None)
         main = kern.get(main_name) if main_name else None
         res = dict(

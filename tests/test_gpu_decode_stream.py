@@ -1,0 +1,144 @@
+"""GPU parity of the one-launch decode GEMV (batches of 1 and 2 tokens).
+
+The forward of a batch of 1 or 2 rows with in_dim a multiple of 256 (at
+least 2048) takes k_dstream: one workgroup per CU owning R row tiles and all
+of K, with T1 = X A^T computed in slices by every workgroup and summed in a
+fixed order.  These tests cover each compiled (tiles per workgroup, K-lines
+per wave) shape class, ragged row counts, bf16 activations, fp32 block
+scales, no adapter, the rank limits, the T1 output, and bit-for-bit
+repeatability across calls (the ticket counters must come back to zero).
+Every call checks from the context's kernel timing that k_dstream ran.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from parity import SEED, TOL_BF16, TOL_F32, bf16_round, nerr
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def QD(ctx):
+    from qlora_hip import device
+    return device
+
+
+def _forward(QD, ctx, W, lora, x, M, N, r):
+    dev = torch.device("cuda:0")
+    y = torch.empty(M, N, device=dev)
+    t1 = torch.empty(M, max(r, 1), device=dev)
+    ctx.set_timing(True)
+    try:
+        QD.forward(W, lora, x, M, y, t1=t1 if r > 0 else None, ctx=ctx)
+        torch.cuda.synchronize()
+        rep = ctx.timing_report()
+    finally:
+        ctx.set_timing(False)
+    return y, t1, rep
+
+
+# (N, K): tiles per workgroup R = ceil(ceil(N/16) / CUs), K-lines per wave
+# ceil(K/256/8): (3,2) (1,6) (2,2) ragged (4,2) (2,1)
+SHAPES = [(11008, 4096), (4096, 11008), (4100, 4096), (14336, 4096), (8000, 2048)]
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_stream_parity(ctx, QD, N, K):
+    r, alpha = 16, 32.0
+    g = O.Rng(SEED ^ (N * 31 + K))
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+    b = g.normal(N * r, 0.01)
+    dev = torch.device("cuda:0")
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    wd = O.dequantize(O.quantize(w))
+    lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r, alpha)
+    for M in (1, 2):
+        x = g.normal(M * K)
+        for act in (torch.float32, torch.bfloat16):
+            _say(f"stream N={N} K={K} M={M} act={act}")
+            xa = bf16_round(x) if act == torch.bfloat16 else x
+            y, t1, rep = _forward(QD, ctx, W, lora, torch.from_numpy(xa).to(dev).to(act), M, N, r)
+            assert "decode_stream" in rep, rep
+            tol = TOL_F32 if act == torch.float32 else TOL_BF16
+            yo = O.qlora_forward(wd, N, K, a, b, r, alpha, xa, M)
+            e = nerr(y.cpu().numpy().ravel(), yo, K, xa, wd)
+            t1o = O.matmul_trans_b(xa, a, M, K, r)
+            et = nerr(t1.cpu().numpy().ravel(), t1o, K, xa, a)
+            _say(f"  y {e:.2e} t1 {et:.2e}")
+            assert e < tol and et < tol, (e, et)
+
+
+def test_stream_f32_scales_no_adapter(ctx, QD):
+    N, K, M = 4096, 4096, 2
+    g = O.Rng(SEED ^ 91)
+    w, x = g.normal(N * K, 0.02), g.normal(M * K)
+    dev = torch.device("cuda:0")
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K),
+                                 double_quant=False, ctx=ctx)
+    y, _, rep = _forward(QD, ctx, W, None, torch.from_numpy(x).to(dev), M, N, 0)
+    assert "decode_stream" in rep, rep
+    wd = O.dequantize(O.quantize(w, 64, False))
+    yo = O.qlora_forward(wd, N, K, None, None, 0, 0.0, x, M)
+    assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
+
+
+@pytest.mark.parametrize("M,r,stream", [(1, 64, True), (2, 32, True), (2, 64, False),
+                                        (1, 1, True), (1, 5, True)])
+def test_stream_ranks(ctx, QD, M, r, stream):
+    # batch * r <= 64 runs in one launch; a larger adapter takes the
+    # two-kernel path, with the same result
+    N, K, alpha = 4096, 4096, 16.0
+    g = O.Rng(SEED ^ (100 + 7 * r + M))
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+    b = g.normal(N * r, 0.01)
+    x = g.normal(M * K)
+    dev = torch.device("cuda:0")
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r, alpha)
+    _say(f"stream ranks M={M} r={r}")
+    y, t1, rep = _forward(QD, ctx, W, lora, torch.from_numpy(x).to(dev), M, N, r)
+    assert ("decode_stream" in rep) == stream, rep
+    wd = O.dequantize(O.quantize(w))
+    yo = O.qlora_forward(wd, N, K, a, b, r, alpha, x, M)
+    assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
+    t1o = O.matmul_trans_b(x, a, M, K, r)
+    assert nerr(t1.cpu().numpy().ravel(), t1o, K, x, a) < TOL_F32
+
+
+def test_stream_repeatable(ctx, QD):
+    # Same inputs, same bits, call after call, with another shape's calls in
+    # between: the T1 slices are summed in a fixed order and the counters
+    # are back at zero after every launch.
+    dev = torch.device("cuda:0")
+    runs = []
+    for (N, K) in [(11008, 4096), (4096, 11008)]:
+        r, alpha, M = 16, 32.0, 1
+        g = O.Rng(SEED ^ (N + 5))
+        w = g.normal(N * K, 0.02)
+        a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+        b = g.normal(N * r, 0.01)
+        x = g.normal(M * K)
+        W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+        lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r,
+                              alpha)
+        runs.append((W, lora, torch.from_numpy(x).to(dev), M, N, r))
+    ref = [None, None]
+    for it in range(4):
+        for i, (W, lora, x, M, N, r) in enumerate(runs):
+            y, t1, rep = _forward(QD, ctx, W, lora, x, M, N, r)
+            assert "decode_stream" in rep, rep
+            got = (y.cpu().numpy().copy(), t1.cpu().numpy().copy())
+            if ref[i] is None:
+                ref[i] = got
+            else:
+                assert np.array_equal(got[0], ref[i][0]) and np.array_equal(got[1], ref[i][1])
+    _say("repeatable over 4 rounds")

@@ -1,0 +1,155 @@
+// decode_common.h -- pieces shared by the decode-shaped GEMV kernels
+// (k_decode.hip, k_dstream.hip): the NF4 codebook split into bf16 hi/lo
+// parts, the k-slot order of the packed-nibble MFMA steps, bf16 rounding,
+// wave reductions, device-coherent stores/loads and the per-line code loads.
+// Every definition lives in an anonymous namespace: each kernel file gets
+// its own copy.
+#pragma once
+#include <type_traits>
+
+#include "qh_internal.h"
+
+namespace qh {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLine = 256;  // elements per line (128 code bytes)
+
+constexpr uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+constexpr float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+constexpr uint32_t bf16_rne(float f) {
+  const uint32_t u = f2u(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Codebook (quant.rs:27-44) split into bf16 hi + lo parts.
+//  nib[c]  = Lh[c] | Ll[c] << 16                      (one nibble)
+//  pair[b] = {Lh[b&15] | Lh[b>>4] << 16, Ll[b&15] | Ll[b>>4] << 16}  (one byte)
+struct Tables {
+  uint32_t nib[16];
+  uint32_t pair[256][2];  // {hi, lo}: the LDS layout, copied as is
+};
+
+constexpr Tables make_tables() {
+  Tables t{};
+  constexpr float L[16] = {
+      -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+      -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+      0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
+      0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+      0.7229568362236023f, 1.0f};
+  uint32_t h[16] = {}, l[16] = {};
+  for (int c = 0; c < 16; ++c) {
+    h[c] = bf16_rne(L[c]);
+    l[c] = bf16_rne(L[c] - u2f(h[c] << 16));
+    t.nib[c] = h[c] | (l[c] << 16);
+  }
+  for (int b = 0; b < 256; ++b) {
+    t.pair[b][0] = h[b & 15] | (h[b >> 4] << 16);
+    t.pair[b][1] = l[b & 15] | (l[b >> 4] << 16);
+  }
+  return t;
+}
+
+__constant__ Tables c_tab = make_tables();
+
+// Element offset, within its 256-element line, of the 8 k-slots that lane
+// group g supplies in MFMA step s (0..7): step s covers block s/2.
+__host__ __device__ constexpr int step_koff(int s, int g) {
+  return 64 * (s >> 1) + 32 * (g & 1) + 8 * (2 * (s & 1) + (g >> 1));
+}
+
+__device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <int XBF16>
+__device__ __forceinline__ float4 load_x4(const void *x, int64_t e) {
+  if (XBF16) {
+    const uint2 q = *(const uint2 *)((const uint16_t *)x + e);
+    return make_float4(__uint_as_float(q.x << 16), __uint_as_float(q.x & 0xffff0000u),
+                       __uint_as_float(q.y << 16), __uint_as_float(q.y & 0xffff0000u));
+  }
+  return *(const float4 *)((const float *)x + e);
+}
+
+// Sum 16 values over the 64 lanes of a wave; lane l returns the total of
+// value (l >> 2) & 15 (valid in lanes whose low two bits are 0).
+__device__ __forceinline__ float reduce16(float (&v)[16]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int half = 8, off = 32; half >= 1; half >>= 1, off >>= 1) {
+    const bool up = (lane & off) != 0;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      // Select between two named values: written as array subscripts the
+      // compiler turns the select into a dynamic index over all 16.
+      const float lo = v[i], hi = v[i + half];
+      const float keep = up ? hi : lo;
+      const float send = up ? lo : hi;
+      v[i] = keep + __shfl_xor(send, off);
+    }
+  }
+  float s = v[0];
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 1);
+  return s;
+}
+
+// Device-coherent (agent scope) stores and loads: they reach the point of
+// coherence shared by all XCDs without writing back or invalidating whole
+// caches.  A producer's stores are complete once its `s_waitcnt` returns,
+// which happens before its ticket increment; a consumer loads only after
+// its own ticket increment returned the final count.
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+  return __uint_as_float(
+      __hip_atomic_load((unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+// Ends a workgroup's partial: waits for its device stores, then takes a
+// ticket; returns true in every thread of the last of `total` workgroups,
+// which also resets the counter for the next launch.
+__device__ __forceinline__ bool last_arrival(unsigned *counter, unsigned total, int *flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = atomicAdd(counter, 1u);
+    *flag = old == total - 1;
+    if (old == total - 1) atomicExch(counter, 0u);
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and
+// lgkmcnt at their "no wait" maxima).
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+struct LineRegs {
+  uint4 c0, c1;  // code bytes [16g, 16g+16) and [64+16g, ...) of row n
+  uint4 sf;      // KIND 0: 4 fp32 block scales; KIND 1: .x = 4 int8 codes
+};
+
+template <int KIND>
+__device__ __forceinline__ void load_line(LineRegs &R, const DevQW &w, int64_t n, int64_t KB,
+                                          const uint8_t *crow, int64_t L, int g) {
+  R.c0 = *(const uint4 *)(crow + L * 128 + 16 * g);
+  R.c1 = *(const uint4 *)(crow + L * 128 + 64 + 16 * g);
+  const int64_t b = n * KB + 4 * L;
+  if (KIND == 0) {
+    R.sf = *(const uint4 *)(w.scales + b);
+  } else {
+    R.sf.x = *(const uint32_t *)(w.scale_codes + b);
+    R.sf.y = R.sf.z = R.sf.w = 0;
+  }
+}
+
+}  // namespace
+}  // namespace qh

@@ -1,0 +1,534 @@
+// k_dstream.hip -- decode GEMV for batches of 1 and 2 tokens in ONE launch
+// per layer: the forward of qlora-wgpu/src/kernels.rs:262-296 (dequant +
+// mm_nt + LoRA mm_nt) for M <= 2,
+//
+//   y[m][n] = sum_b s_{n,b} sum_{k in b} x[m][k] L[c_{n,k}]
+//           + (alpha/r) sum_j T1[m][j] B[n][j],      T1 = X A^T.
+//
+// Grid: at most one workgroup per CU (each needs more than half of a CU's
+// LDS), 8 waves per workgroup.
+//  * Workgroup c owns R consecutive 16-row tiles and the whole of K.  Line
+//    wave w owns the K-lines [KL w / 8, KL (w+1) / 8) (a K-line = 256
+//    elements = 128 code bytes per row) of all R tiles, so each X fragment
+//    read from LDS feeds R MFMAs.  Every code line of a wave (R * KLW <= 8)
+//    is requested before the first one is used: the whole weight stream is
+//    in flight from the start, and each line's MFMAs wait for that line only.
+//  * Code loads, the permlane32 regrouping and the packed-row MFMA are those
+//    of the small-batch kernel in k_decode.hip: A-fragment rows m and M+m
+//    carry the bf16 hi and lo parts of x_m, the B operand interleaves the
+//    byte-pair table's hi and lo entries, y = D[m] + D[M+m].
+//  * The byte-pair codebook table sits in LDS 32 times, entry e of copy k at
+//    byte 256 e + 8 k; lane l reads copy l % 32.  The 32 lanes that one LDS
+//    cycle serves then hit 32 distinct bank pairs whatever the codes are
+//    (a single copy serves random bytes at about 2.5x the cycles).  One
+//    v_perm_b32 forms the address from the code byte and the lane's copy
+//    offset.
+//  * X fragments are stored once per K-line as (P_ab, P_cd) pairs; the read
+//    (ds_read_b64) duplicates them into the (P_ab, P_ab, P_cd, P_cd) A
+//    operand that the interleaved B operand needs.
+//  * Prologue order: every wave issues its small loads (X, the table source,
+//    LoRA B rows, T1 partials, absmax), the workgroup meets at a barrier,
+//    and only then do the code lines go out.  Vector-memory data returns in
+//    order, so a small load issued behind the weight stream waits for it
+//    (about 4 us at full HBM load).
+//  * T1 = X A^T comes from k_t1p (k_decode.hip), launched just before, as
+//    one partial per K-line; every workgroup sums the partials in line
+//    order in LDS, so T1 and y are identical in every workgroup and every
+//    run.  (Summing slices across workgroups inside this kernel costs
+//    several dependent memory round trips, each about 4 us while the weight
+//    stream is in flight.)
+// The block scale multiplies each block's MFMA partial once; the double-
+// quant decode c*(absmax/127) is within 1 ulp of quant.rs:218's
+// fl(fl(c/127)*absmax) and only enters this sum, never a stored weight.
+#include <algorithm>
+
+#include "decode_common.h"
+
+namespace qh {
+namespace {
+
+constexpr int kLW = 8;                    // line waves per workgroup
+constexpr int kThreads = kLW * 64;
+constexpr int kCopies = 32;               // codebook table copies
+constexpr uint32_t kTabBytes = 256u * kCopies * 8u;  // 64 KiB at LDS offset 0
+constexpr int kMaxLines = 8;   // code lines a wave holds in registers
+constexpr int kT1Loads = 4;    // T1 line partials per thread (NL * M * r <= 2048)
+constexpr int kLinesAhead = 3; // K-lines of loads a wave keeps in flight
+constexpr int kT1PerThread = 8; // line partials per thread in the T1 sum (NL <= 64)
+constexpr uint32_t kLdsLimit = 160u * 1024u;
+
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v2u lds_u2;
+typedef __attribute__((address_space(3))) v4u lds_u4;
+typedef __attribute__((address_space(3))) float lds_f;
+// LDS is addressed by byte offset: the kernel declares no __shared__ object,
+// so dynamic LDS starts at 0 and the table needs no base register.
+#define LDS_AT(T, off) ((T *)(uintptr_t)(off))
+
+// Barrier over LDS only: waits for this wave's LDS operations, not for its
+// global loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Table address of byte i of w for the lane whose copy offset is lo8:
+// bits 0..7 = lo8, bits 8..15 = the byte.
+__device__ __forceinline__ uint32_t tab_addr(uint32_t w, uint32_t lo8, int i) {
+  return __builtin_amdgcn_perm(w, lo8, 0x0C0C0000u | ((4u + (uint32_t)i) << 8));
+}
+
+// Regroups a code line's bytes so that dword s covers MFMA step s.
+__device__ __forceinline__ void regroup(const LineRegs &L, uint32_t (&sw)[8]) {
+  auto p = __builtin_amdgcn_permlane32_swap(L.c0.x, L.c0.y, false, false);
+  sw[0] = p[0];
+  sw[2] = p[1];
+  p = __builtin_amdgcn_permlane32_swap(L.c0.z, L.c0.w, false, false);
+  sw[1] = p[0];
+  sw[3] = p[1];
+  p = __builtin_amdgcn_permlane32_swap(L.c1.x, L.c1.y, false, false);
+  sw[4] = p[0];
+  sw[6] = p[1];
+  p = __builtin_amdgcn_permlane32_swap(L.c1.z, L.c1.w, false, false);
+  sw[5] = p[0];
+  sw[7] = p[1];
+}
+
+// LDS operands of one MFMA step (two K=32 halves p) for R tiles.
+template <int R>
+struct StepOps {
+  v2u xa[2];    // A-fragment pairs (P_ab, P_cd)
+  v2u e[R][4];  // table entries: bytes 2p, 2p+1 of the step's dword
+};
+
+template <int M, int R>
+__device__ __forceinline__ void fetch_step(StepOps<R> &o, const uint32_t (&sw)[R][8], int s,
+                                           uint32_t xf, int xo, uint32_t lo8) {
+  constexpr int M2 = 2 * M;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    o.xa[p] = *LDS_AT(const lds_u2, xf + ((s * 2 + p) * M2 * 4 + xo) * 8);
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+      o.e[t][2 * p] = *LDS_AT(const lds_u2, tab_addr(sw[t][s], lo8, 2 * p));
+      o.e[t][2 * p + 1] = *LDS_AT(const lds_u2, tab_addr(sw[t][s], lo8, 2 * p + 1));
+    }
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void mfma_step(const StepOps<R> &o, floatx4 (&d)[R]) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const bf16x8 av =
+        __builtin_bit_cast(bf16x8, v4u{o.xa[p].x, o.xa[p].x, o.xa[p].y, o.xa[p].y});
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+      const v2u e0 = o.e[t][2 * p], e1 = o.e[t][2 * p + 1];
+      const bf16x8 bv = __builtin_bit_cast(bf16x8, v4u{e0.x, e0.y, e1.x, e1.y});
+      d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, d[t], 0, 0, 0);
+    }
+  }
+}
+
+// X fragments of one K-line for this lane's unit (s, p, g4): hi part to
+// row m, lo part to row M + m, as (P_ab, P_cd) pairs.
+template <int XBF16, int M>
+__device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base, int ug) {
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float v[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
+    uint32_t h[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = bf16_bits_rne(v[i]);
+      lo[i] = XBF16 ? 0u : bf16_bits_rne(v[i] - __uint_as_float(h[i] << 16));
+    }
+    *LDS_AT(lds_u2, base + (uint32_t)(m * 4 + ug) * 8) =
+        v2u{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    *LDS_AT(lds_u2, base + (uint32_t)((M + m) * 4 + ug) * 8) =
+        v2u{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+  }
+}
+
+// grid = G workgroups of kThreads; workgroup c owns tiles [c R, c R + R).
+// t1p: the NL x M x r line partials of T1 (k_t1p, launched just before).
+// Dynamic LDS (byte offsets): [0, 64K) table | X fragments (KL M KiB, by
+// K-line) | lbs (16 R r floats) | T1 partials (NL M r floats) | red
+// (kLW R 16 M floats) | t1s (64 floats) | nib (16 words).
+template <int XBF16, int KIND, int M, int R, int KLW>
+__global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__restrict__ x,
+                                                      int r, const float *__restrict__ lb,
+                                                      float s_lora,
+                                                      const float *__restrict__ t1p,
+                                                      float *__restrict__ t1_out,
+                                                      float *__restrict__ y) {
+  static_assert(R * KLW <= kMaxLines, "code lines per wave");
+  constexpr int M2 = 2 * M;
+  constexpr uint32_t kFragLine = 16 * M2 * 4 * 8;  // bytes of X fragments per K-line
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t N = w.rows, K = w.cols, KB = K >> 6;
+  const int KL = (int)(K / kLine), c = blockIdx.x;
+  const int64_t n0 = (int64_t)c * R * 16;
+  const int MR = M * r, NMR = KL * MR;
+  const uint32_t o_x = kTabBytes;
+  const uint32_t o_lb = o_x + (uint32_t)KL * kFragLine;
+  const uint32_t o_tp = o_lb + (uint32_t)(16 * R * (r > 0 ? r : 1)) * 4;
+  const uint32_t o_red = o_tp + (uint32_t)(NMR > 0 ? NMR : 1) * 4;
+  const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
+  const uint32_t o_nib = o_t1 + 64 * 4;
+
+  const int kl0 = KL * wave / kLW, nkl = KL * (wave + 1) / kLW - kl0;
+  const int nl = lane & 15, g = lane >> 4;
+  int64_t nrow[R];
+  const uint8_t *crow[R];
+#pragma unroll
+  for (int t = 0; t < R; ++t) {
+    const int64_t n = n0 + 16 * t + nl;
+    nrow[t] = n < N ? n : N - 1;
+    crow[t] = w.codes + nrow[t] * (K >> 1);
+  }
+
+  // ---- the codebook table, from constants: no memory round trip --------
+  // Built before any load is issued: a wave issuing more loads than the
+  // vector-memory queue takes stalls at issue until data drains.
+  if (tid < 16) {
+    constexpr Tables kTab = make_tables();
+    uint32_t v = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v = tid == q ? kTab.nib[q] : v;
+    *LDS_AT(lds_f, o_nib + (uint32_t)tid * 4) = __uint_as_float(v);
+  }
+  lds_barrier();
+  {
+    // Entries e = (tid >> 4) + 32 i, copies 2 (tid & 15) + {0, 1}:
+    // pair[e] = {Lh[lo] | Lh[hi] << 16, Ll[lo] | Ll[hi] << 16}.
+    const uint32_t nlo =
+        __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)((tid >> 4) & 15) * 4));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = (tid >> 4) + 32 * i;
+      const uint32_t nhi = __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)(e >> 4) * 4));
+      const uint32_t ph = (nlo & 0xffffu) | (nhi << 16), pl = (nlo >> 16) | (nhi & 0xffff0000u);
+      *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
+    }
+  }
+  lds_barrier();  // B1: the table is in LDS
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- loads, in order of use (vector-memory data returns in order) ----
+  // absmax first, then per K-line the lane's unit (s, p, g4) of X and the R
+  // code lines; DL K-lines are in flight ahead of the one being computed.
+  float am0[R], am1[R];
+  if (KIND == 1) {
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+      am0[t] = w.absmax[(nrow[t] * KB + 4 * kl0) >> 8];
+      am1[t] = w.absmax[(nrow[t] * KB + 4 * (kl0 + nkl - 1)) >> 8];
+    }
+  }
+  const int us = lane >> 3, up = (lane >> 2) & 1, ug = lane & 3;
+  const int koff = step_koff(us, ug) + 4 * up;
+  float4 xv[KLW][M];
+  LineRegs L[KLW][R];
+  auto issue_line = [&](int kk) {
+    const int kl = kl0 + (kk < nkl ? kk : nkl - 1);
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      xv[kk][m] = load_x4<XBF16>(x, (int64_t)m * K + (int64_t)kl * kLine + koff);
+#pragma unroll
+    for (int t = 0; t < R; ++t) load_line<KIND>(L[kk][t], w, nrow[t], KB, crow[t], kl, g);
+  };
+  // The epilogue's operands (LoRA B rows of the workgroup's tiles, 16 R r
+  // <= 2 R * 512 floats, and the T1 line partials) go out first: they are
+  // small and arrive with the first code lines.
+  float lbv[2 * R], tpv[kT1Loads];
+  auto issue_tail = [&]() {
+    if (r > 0) {
+#pragma unroll
+      for (int q = 0; q < 2 * R; ++q) {
+        int idx = tid + 512 * q;
+        idx = idx < 16 * R * r ? idx : 16 * R * r - 1;
+        int64_t row = n0 + idx / r;
+        row = row < N ? row : N - 1;
+        lbv[q] = lb[row * r + idx % r];
+      }
+#pragma unroll
+      for (int q = 0; q < kT1Loads; ++q) {
+        const int i = tid + 512 * q;
+        tpv[q] = t1p[i < NMR ? i : NMR - 1];
+      }
+    }
+  };
+  constexpr int DL = KLW < kLinesAhead ? KLW : kLinesAhead;
+  issue_tail();
+#pragma unroll
+  for (int kk = 0; kk < DL; ++kk) issue_line(kk);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- the weight stream ----------------------------------------------
+  // Fragments of the wave's K-line kk (a padded line repeats the last one).
+  auto xfrag = [&](int kk) {
+    return o_x + (uint32_t)(kl0 + (kk < nkl ? kk : nkl - 1)) * kFragLine;
+  };
+  const uint32_t xunit = (uint32_t)(us * 2 + up) * M2 * 32;
+  {
+    const uint32_t lo8 = (uint32_t)(lane & 31) * 8u;
+    const int xo = (nl < M2 ? nl : M2 - 1) * 4 + g;
+    floatx4 acc[R];
+#pragma unroll
+    for (int t = 0; t < R; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Software pipeline over the wave's 8 KLW MFMA steps: the LDS operands
+    // of step i + D are requested before step i's MFMAs.  A line's X
+    // fragments are written and its code bytes regrouped when its first
+    // step is fetched (a wave's LDS operations complete in order).
+    constexpr int D = R == 1 ? 4 : 2;
+    constexpr int NS = KLW * 8;
+    uint32_t sw[2][R][8];
+    StepOps<R> ops[D + 1];
+    write_frags<XBF16, M>(xv[0], xfrag(0) + xunit, ug);
+#pragma unroll
+    for (int t = 0; t < R; ++t) regroup(L[0][t], sw[0][t]);
+#pragma unroll
+    for (int f = 0; f < D; ++f) fetch_step<M, R>(ops[f], sw[0], f, xfrag(0), xo, lo8);
+    floatx4 d[R];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int kk = i / 8, s = i % 8;
+      if (s == 0 && kk + DL < KLW) issue_line(kk + DL);
+      const int f = i + D;
+      if (f < NS) {
+        const int fk = f / 8, fs = f % 8;
+        if (fs == 0) {
+          write_frags<XBF16, M>(xv[fk], xfrag(fk) + xunit, ug);
+#pragma unroll
+          for (int t = 0; t < R; ++t) regroup(L[fk][t], sw[fk & 1][t]);
+        }
+        fetch_step<M, R>(ops[f % (D + 1)], sw[fk & 1], fs, xfrag(fk), xo, lo8);
+      }
+      if ((s & 1) == 0) {
+#pragma unroll
+        for (int t = 0; t < R; ++t) d[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      mfma_step<R>(ops[i % (D + 1)], d);
+      if (s & 1) {  // block j = s / 2 of line kk is complete
+        const int j = s >> 1, kl = kl0 + (kk < nkl ? kk : nkl - 1);
+        const float valid = kk < nkl ? 1.0f : 0.0f;
+#pragma unroll
+        for (int t = 0; t < R; ++t) {
+          float sc;
+          if (KIND == 0) {
+            const LineRegs &Lr = L[kk][t];
+            sc = __uint_as_float(j == 0 ? Lr.sf.x : j == 1 ? Lr.sf.y : j == 2 ? Lr.sf.z : Lr.sf.w) *
+                 valid;
+          } else {
+            const float amax = ((nrow[t] * KB + 4 * kl) >> 8) == ((nrow[t] * KB + 4 * kl0) >> 8)
+                                   ? am0[t]
+                                   : am1[t];
+            sc = (float)(int8_t)((L[kk][t].sf.x >> (8 * j)) & 255u) *
+                 (amax * (1.0f / 127.0f)) * valid;
+          }
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[t][v] = fmaf(sc, d[t][v], acc[t][v]);
+        }
+      }
+      // Keep the steps in order: hoisted early, a later line's regrouping
+      // would wait for that line's bytes.
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Lanes 0..15 hold D rows 0..3 of column nl: y_m = D[m] + D[M+m].
+    if (g == 0) {
+#pragma unroll
+      for (int t = 0; t < R; ++t)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          *LDS_AT(lds_f, o_red + (uint32_t)(((wave * R + t) * M + m) * 16 + nl) * 4) =
+              acc[t][m] + acc[t][M + m];
+    }
+  }
+  if (r > 0) {
+#pragma unroll
+    for (int q = 0; q < 2 * R; ++q) {
+      const int idx = tid + 512 * q;
+      if (idx < 16 * R * r) *LDS_AT(lds_f, o_lb + (uint32_t)idx * 4) = lbv[q];
+    }
+#pragma unroll
+    for (int q = 0; q < kT1Loads; ++q) {
+      const int i = tid + 512 * q;
+      if (i < NMR) *LDS_AT(lds_f, o_tp + (uint32_t)i * 4) = tpv[q];
+    }
+  }
+  lds_barrier();  // B2: partial sums, B rows and T1 partials are in LDS
+
+  // T1[o] = sum of the NL line partials, in the same fixed order in every
+  // workgroup: thread (o, q < 8) adds lines q, q + 8, ...; then the eight
+  // sums add up in q order.
+  const uint32_t o_q = o_x;  // the X fragments are dead: 8 x MR floats
+  if (r > 0) {
+    if (tid < 8 * MR) {
+      const int o = tid % MR, q = tid / MR;
+      float v[kT1PerThread];
+#pragma unroll
+      for (int i = 0; i < kT1PerThread; ++i) {
+        const int cl = q + 8 * i;
+        v[i] = *LDS_AT(const lds_f, o_tp + (uint32_t)((cl < KL ? cl : KL - 1) * MR + o) * 4);
+      }
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kT1PerThread; ++i) t += q + 8 * i < KL ? v[i] : 0.0f;
+      *LDS_AT(lds_f, o_q + (uint32_t)(q * MR + o) * 4) = t;
+    }
+    lds_barrier();
+    if (tid < MR) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = *LDS_AT(const lds_f, o_q + (uint32_t)(q * MR + tid) * 4);
+      const float t = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+      *LDS_AT(lds_f, o_t1 + (uint32_t)tid * 4) = t;
+      if (t1_out && c == 0) t1_out[tid] = t;
+    }
+    lds_barrier();  // B3: T1 is in LDS
+  }
+  if (tid < R * M * 16) {
+    const int t = tid / (M * 16), m = (tid / 16) % M, rn = tid % 16;
+    const int64_t n = n0 + 16 * t + rn;
+    float pv[kLW];
+#pragma unroll
+    for (int wv = 0; wv < kLW; ++wv)
+      pv[wv] = *LDS_AT(const lds_f, o_red + (uint32_t)(((wv * R + t) * M + m) * 16 + rn) * 4);
+    float sum = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < kLW; ++wv) sum += pv[wv];
+    if (r > 0) {
+      // LoRA dot in chunks of 16 terms whose LDS reads go out together.
+      float l = 0.0f;
+      for (int j0 = 0; j0 < r; j0 += 16) {
+        float ta[16], tb[16];
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          const int j = j0 + jj < r ? j0 + jj : r - 1;
+          ta[jj] = *LDS_AT(const lds_f, o_t1 + (uint32_t)(m * r + j) * 4);
+          tb[jj] = *LDS_AT(const lds_f, o_lb + (uint32_t)((16 * t + rn) * r + j) * 4);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj)
+          if (j0 + jj < r) l = fmaf(ta[jj], tb[jj], l);
+      }
+      sum = fmaf(s_lora, l, sum);
+    }
+    if (n < N) y[(int64_t)m * N + n] = sum;
+  }
+}
+
+// ---- host side --------------------------------------------------------------
+struct StreamPlan {
+  int R = 0, KLW = 0, G = 0;
+  uint32_t lds = 0;
+  bool ok = false;
+};
+
+int g_cus[64] = {};
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (g_cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    g_cus[dev] = v;
+  }
+  return g_cus[dev];
+}
+
+// (R, KLW) pairs that are compiled.
+#define QH_STREAM_SHAPES(F) \
+  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(1, 8) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2) F(4, 1) F(4, 2)
+
+bool shape_compiled(int R, int KLW) {
+#define QH_SHAPE_EQ(rr, kk) if (R == rr && KLW == kk) return true;
+  QH_STREAM_SHAPES(QH_SHAPE_EQ)
+#undef QH_SHAPE_EQ
+  return false;
+}
+
+StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
+  StreamPlan p;
+  const int cus = cu_count();
+  if (cus <= 0 || M < 1 || M > 2 || r < 0 || r > 64 || M * r > 64) return p;
+  if (w.bs != 64 || w.cols % kLine != 0) return p;
+  if ((((uintptr_t)w.codes) & 15) != 0) return p;
+  if (w.kind == 0 ? (((uintptr_t)w.scales) & 15) != 0 : (((uintptr_t)w.scale_codes) & 3) != 0)
+    return p;
+  const int64_t T = (w.rows + 15) / 16, KL = w.cols / kLine;
+  if (KL < kLW || KL > 8 * kT1PerThread || KL * M * r > (int64_t)kT1Loads * kThreads) return p;
+  const int64_t R = (T + cus - 1) / cus;
+  const int64_t KLW = (KL + kLW - 1) / kLW;
+  if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW)) return p;
+  const int64_t G = (T + R - 1) / R;
+  const size_t lds = kTabBytes + (size_t)KL * 16 * 2 * M * 4 * 8 +
+                     (size_t)16 * R * (r > 0 ? r : 1) * 4 +
+                     (size_t)(KL * M * r > 0 ? KL * M * r : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
+                     64 * 4 + 16 * 4;
+  if (lds > kLdsLimit) return p;
+  p.R = (int)R;
+  p.KLW = (int)KLW;
+  p.G = (int)G;
+  p.lds = (uint32_t)lds;
+  p.ok = true;
+  return p;
+}
+
+template <int XBF16, int KIND, int M, int R, int KLW>
+hipError_t run_stream(const DevQW &w, const void *x, int r, const float *lb, float s,
+                      const float *t1p, float *t1_out, float *y, const StreamPlan &p,
+                      hipStream_t st) {
+  auto k = k_dstream<XBF16, KIND, M, R, KLW>;
+  static bool attr = false;  // per instantiation; the attribute is per function
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void *)k,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)kLdsLimit);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  return qh_launch(k, dim3((unsigned)p.G), dim3(kThreads), p.lds, st, w, x, r, lb, s, t1p,
+                   t1_out, y);
+}
+
+template <int XBF16, int KIND, int M>
+hipError_t dispatch_shape(const DevQW &w, const void *x, int r, const float *lb, float s,
+                          const float *t1p, float *t1_out, float *y, const StreamPlan &p,
+                          hipStream_t st) {
+#define QH_SHAPE_CASE(rr, kk) \
+  if (p.R == rr && p.KLW == kk) \
+    return run_stream<XBF16, KIND, M, rr, kk>(w, x, r, lb, s, t1p, t1_out, y, p, st);
+  QH_STREAM_SHAPES(QH_SHAPE_CASE)
+#undef QH_SHAPE_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r) { return stream_plan(w, M, r).ok; }
+
+hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                                const float *lb, int64_t r, float s, float *y, float *t1_out,
+                                const void *scratch, hipStream_t st) {
+  const StreamPlan p = stream_plan(w, M, r);
+  if (!p.ok) return hipErrorInvalidValue;
+  const float *t1p = (const float *)scratch;
+  const int ri = (int)r;
+#define QH_ARGS w, x, ri, lb, s, t1p, t1_out, y, p, st
+  if (M == 1) {
+    if (x_bf16) return w.kind == 0 ? dispatch_shape<1, 0, 1>(QH_ARGS) : dispatch_shape<1, 1, 1>(QH_ARGS);
+    return w.kind == 0 ? dispatch_shape<0, 0, 1>(QH_ARGS) : dispatch_shape<0, 1, 1>(QH_ARGS);
+  }
+  if (x_bf16) return w.kind == 0 ? dispatch_shape<1, 0, 2>(QH_ARGS) : dispatch_shape<1, 1, 2>(QH_ARGS);
+  return w.kind == 0 ? dispatch_shape<0, 0, 2>(QH_ARGS) : dispatch_shape<0, 1, 2>(QH_ARGS);
+#undef QH_ARGS
+}
+
+}  // namespace qh

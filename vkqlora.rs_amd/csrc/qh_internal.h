@@ -129,6 +129,14 @@ hipError_t launch_decode_t1(const DevQW &w, const void *x, int x_bf16, int64_t M
 hipError_t launch_decode_small(const DevQW &w, const void *x, int x_bf16, int64_t M,
                                const float *lb, int64_t r, float s, float *y, float *t1_out,
                                void *scratch, unsigned *tickets, hipStream_t st);
+// ---- k_dstream.hip ----
+// Decode GEMV for batches of 1 and 2 rows in one launch per layer (at most
+// one workgroup per CU).  With an adapter, launch_decode_t1 runs first on
+// the same stream and `scratch` holds its T1 line partials.
+bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r);
+hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                                const float *lb, int64_t r, float s, float *y, float *t1_out,
+                                const void *scratch, hipStream_t st);
 // Tuning knobs of the decode GEMV: codebook table (0 = 16-entry nibble
 // table, 1 = 256-entry byte-pair table) and the workgroup count the K split
 // aims for.

@@ -25,7 +25,9 @@ using qh::Operand;
 namespace {
 
 thread_local std::string g_err;
-int g_decode_path = 0;  // 0 = fused decode where it applies, 1 = prep + main
+// 0 = one-launch decode where it applies, else the small-batch pair, else
+// prep + main; 1 = prep + main only; 2 = no one-launch decode.
+int g_decode_path = 0;
 
 qh_status fail(qh_status st, const std::string &msg) {
   // Display formats of QloraError (qlora-core/src/error.rs:16-24).
@@ -386,7 +388,23 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     return;
   }
 
-  if (decode && g_decode_path == 0 && qh::decode_small_ok(W, M, r)) {
+  if (decode && g_decode_path == 0 && qh::decode_stream_ok(W, M, r)) {
+    Carve cd;
+    size_t i_sc = cd.add(qh::decode_small_scratch_bytes(M, N, K, r));
+    auto pd = cd.bind(ctx->scratch);
+    const int xb = xe == qh::E_BF16;
+    if (lora)
+      timed(ctx, "decode_t1", s, [&] {
+        return qh::launch_decode_t1(W, x, xb, M, l->a, r, pd[i_sc], s);
+      });
+    timed(ctx, "decode_stream", s, [&] {
+      return qh::launch_decode_stream(W, x, xb, M, lora ? l->b : nullptr, r, sc, y, t1_out,
+                                      pd[i_sc], s);
+    });
+    return;
+  }
+
+  if (decode && g_decode_path != 1 && qh::decode_small_ok(W, M, r)) {
     Carve cd;
     size_t i_sc = cd.add(qh::decode_small_scratch_bytes(M, N, K, r));
     auto pd = cd.bind(ctx->scratch);

@@ -104,6 +104,7 @@ def lora_struct(a: Optional[torch.Tensor], b: Optional[torch.Tensor], r: int,
     s.a, s.a_len = a.data_ptr(), a.numel()
     s.b, s.b_len = b.data_ptr(), b.numel()
     s.r, s.alpha = r, alpha
+    s._refs = (a, b)  # the struct holds raw pointers: keep the tensors alive
     return s
 
 
