@@ -96,10 +96,21 @@ __device__ __forceinline__ void regroup(const LineRegs &L, uint32_t (&sw)[8]) {
   sw[7] = p[1];
 }
 
+// X fragments are stored with the (P_ab, P_ab, P_cd, P_cd) repetition the
+// interleaved B operand needs (16 bytes, read straight into the A operand)
+// when they fit, i.e. for batch 1; batch 2 stores (P_ab, P_cd) and
+// repeats the dwords in registers.
+template <int M>
+struct FragOf {
+  static constexpr bool kDup = M == 1;
+  static constexpr uint32_t kUnit = kDup ? 16 : 8;  // bytes per (step, half, row, group)
+  static constexpr uint32_t kLine = 16 * 2 * M * 4 * kUnit;
+};
+
 // LDS operands of one MFMA step (two K=32 halves p) for R tiles.
 template <int R>
 struct StepOps {
-  v2u xa[2];    // A-fragment pairs (P_ab, P_cd)
+  v4u xa[2];    // A operands
   v2u e[R][4];  // table entries: bytes 2p, 2p+1 of the step's dword
 };
 
@@ -107,9 +118,16 @@ template <int M, int R>
 __device__ __forceinline__ void fetch_step(StepOps<R> &o, const uint32_t (&sw)[R][8], int s,
                                            uint32_t xf, int xo, uint32_t lo8) {
   constexpr int M2 = 2 * M;
+  typedef FragOf<M> F;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    o.xa[p] = *LDS_AT(const lds_u2, xf + ((s * 2 + p) * M2 * 4 + xo) * 8);
+    const uint32_t a = xf + (uint32_t)((s * 2 + p) * M2 * 4 + xo) * F::kUnit;
+    if (F::kDup) {
+      o.xa[p] = *LDS_AT(const lds_u4, a);
+    } else {
+      const v2u q = *LDS_AT(const lds_u2, a);
+      o.xa[p] = v4u{q.x, q.x, q.y, q.y};
+    }
 #pragma unroll
     for (int t = 0; t < R; ++t) {
       o.e[t][2 * p] = *LDS_AT(const lds_u2, tab_addr(sw[t][s], lo8, 2 * p));
@@ -122,8 +140,7 @@ template <int R>
 __device__ __forceinline__ void mfma_step(const StepOps<R> &o, floatx4 (&d)[R]) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const bf16x8 av =
-        __builtin_bit_cast(bf16x8, v4u{o.xa[p].x, o.xa[p].x, o.xa[p].y, o.xa[p].y});
+    const bf16x8 av = __builtin_bit_cast(bf16x8, o.xa[p]);
 #pragma unroll
     for (int t = 0; t < R; ++t) {
       const v2u e0 = o.e[t][2 * p], e1 = o.e[t][2 * p + 1];
@@ -135,21 +152,35 @@ __device__ __forceinline__ void mfma_step(const StepOps<R> &o, floatx4 (&d)[R]) 
 
 // X fragments of one K-line for this lane's unit (s, p, g4): hi part to
 // row m, lo part to row M + m, as (P_ab, P_cd) pairs.
+// Two floats to a bf16 pair (round to nearest even: v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 h = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
 template <int XBF16, int M>
 __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base, int ug) {
+  typedef FragOf<M> F;
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    const float v[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
-    uint32_t h[4], lo[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h[i] = bf16_bits_rne(v[i]);
-      lo[i] = XBF16 ? 0u : bf16_bits_rne(v[i] - __uint_as_float(h[i] << 16));
+    const uint32_t h01 = bf16_pair(xv[m].x, xv[m].y), h23 = bf16_pair(xv[m].z, xv[m].w);
+    uint32_t l01 = 0, l23 = 0;
+    if (!XBF16) {
+      l01 = bf16_pair(xv[m].x - __uint_as_float(h01 << 16),
+                      xv[m].y - __uint_as_float(h01 & 0xffff0000u));
+      l23 = bf16_pair(xv[m].z - __uint_as_float(h23 << 16),
+                      xv[m].w - __uint_as_float(h23 & 0xffff0000u));
     }
-    *LDS_AT(lds_u2, base + (uint32_t)(m * 4 + ug) * 8) =
-        v2u{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-    *LDS_AT(lds_u2, base + (uint32_t)((M + m) * 4 + ug) * 8) =
-        v2u{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+    const uint32_t ah = base + (uint32_t)(m * 4 + ug) * F::kUnit;
+    const uint32_t al = base + (uint32_t)((M + m) * 4 + ug) * F::kUnit;
+    if (F::kDup) {
+      *LDS_AT(lds_u4, ah) = v4u{h01, h01, h23, h23};
+      *LDS_AT(lds_u4, al) = v4u{l01, l01, l23, l23};
+    } else {
+      *LDS_AT(lds_u2, ah) = v2u{h01, h23};
+      *LDS_AT(lds_u2, al) = v2u{l01, l23};
+    }
   }
 }
 
@@ -167,8 +198,9 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
                                                       float *__restrict__ y) {
   static_assert(R * KLW <= kMaxLines, "code lines per wave");
   constexpr int M2 = 2 * M;
-  constexpr uint32_t kFragLine = 16 * M2 * 4 * 8;  // bytes of X fragments per K-line
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr uint32_t kFragLine = FragOf<M>::kLine;  // bytes of X fragments per K-line
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar line indices
   const int64_t N = w.rows, K = w.cols, KB = K >> 6;
   const int KL = (int)(K / kLine), c = blockIdx.x;
   const int64_t n0 = (int64_t)c * R * 16;
@@ -190,33 +222,6 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     nrow[t] = n < N ? n : N - 1;
     crow[t] = w.codes + nrow[t] * (K >> 1);
   }
-
-  // ---- the codebook table, from constants: no memory round trip --------
-  // Built before any load is issued: a wave issuing more loads than the
-  // vector-memory queue takes stalls at issue until data drains.
-  if (tid < 16) {
-    constexpr Tables kTab = make_tables();
-    uint32_t v = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) v = tid == q ? kTab.nib[q] : v;
-    *LDS_AT(lds_f, o_nib + (uint32_t)tid * 4) = __uint_as_float(v);
-  }
-  lds_barrier();
-  {
-    // Entries e = (tid >> 4) + 32 i, copies 2 (tid & 15) + {0, 1}:
-    // pair[e] = {Lh[lo] | Lh[hi] << 16, Ll[lo] | Ll[hi] << 16}.
-    const uint32_t nlo =
-        __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)((tid >> 4) & 15) * 4));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = (tid >> 4) + 32 * i;
-      const uint32_t nhi = __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)(e >> 4) * 4));
-      const uint32_t ph = (nlo & 0xffffu) | (nhi << 16), pl = (nlo >> 16) | (nhi & 0xffff0000u);
-      *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
-    }
-  }
-  lds_barrier();  // B1: the table is in LDS
-  __builtin_amdgcn_sched_barrier(0);
 
   // ---- loads, in order of use (vector-memory data returns in order) ----
   // absmax first, then per K-line the lane's unit (s, p, g4) of X and the R
@@ -242,8 +247,8 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     for (int t = 0; t < R; ++t) load_line<KIND>(L[kk][t], w, nrow[t], KB, crow[t], kl, g);
   };
   // The epilogue's operands (LoRA B rows of the workgroup's tiles, 16 R r
-  // <= 2 R * 512 floats, and the T1 line partials) go out first: they are
-  // small and arrive with the first code lines.
+  // <= 2 R * 512 floats, and the T1 line partials) go out after the last
+  // code line: issued earlier, they would hold back every line behind them.
   float lbv[2 * R], tpv[kT1Loads];
   auto issue_tail = [&]() {
     if (r > 0) {
@@ -263,9 +268,42 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     }
   };
   constexpr int DL = KLW < kLinesAhead ? KLW : kLinesAhead;
-  issue_tail();
+  // The first K-line goes out before the table is built (a few loads per
+  // wave do not stall issue), the rest after it.
+  issue_line(0);
+  if (KLW == 1) issue_tail();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- the codebook table, from constants: no memory round trip --------
+  // Built before most loads are issued: a wave issuing more loads than the
+  // vector-memory queue takes stalls at issue until data drains.
+  if (tid < 16) {
+    constexpr Tables kTab = make_tables();
+    uint32_t v = 0;
 #pragma unroll
-  for (int kk = 0; kk < DL; ++kk) issue_line(kk);
+    for (int q = 0; q < 16; ++q) v = tid == q ? kTab.nib[q] : v;
+    *LDS_AT(lds_f, o_nib + (uint32_t)tid * 4) = __uint_as_float(v);
+  }
+  lds_barrier();
+  {
+    // Entries e = (tid >> 4) + 32 i, copies 2 (tid & 15) + {0, 1}:
+    // pair[e] = {Lh[lo] | Lh[hi] << 16, Ll[lo] | Ll[hi] << 16}.
+    const uint32_t nlo =
+        __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)((tid >> 4) & 15) * 4));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = (tid >> 4) + 32 * i;
+      const uint32_t nhi = __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)(e >> 4) * 4));
+      const uint32_t ph = (nlo & 0xffffu) | (nhi << 16), pl = (nlo >> 16) | (nhi & 0xffff0000u);
+      *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
+    }
+  }
+  lds_barrier();  // B1: the table is in LDS
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int kk = 1; kk < DL; ++kk) issue_line(kk);
+  if (DL == KLW && KLW > 1) issue_tail();
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- the weight stream ----------------------------------------------
@@ -273,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   auto xfrag = [&](int kk) {
     return o_x + (uint32_t)(kl0 + (kk < nkl ? kk : nkl - 1)) * kFragLine;
   };
-  const uint32_t xunit = (uint32_t)(us * 2 + up) * M2 * 32;
+  const uint32_t xunit = (uint32_t)(us * 2 + up) * M2 * 4 * FragOf<M>::kUnit;
   {
     const uint32_t lo8 = (uint32_t)(lane & 31) * 8u;
     const int xo = (nl < M2 ? nl : M2 - 1) * 4 + g;
@@ -297,7 +335,10 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int kk = i / 8, s = i % 8;
-      if (s == 0 && kk + DL < KLW) issue_line(kk + DL);
+      if (s == 0 && kk + DL < KLW) {
+        issue_line(kk + DL);
+        if (kk + DL == KLW - 1) issue_tail();
+      }
       const int f = i + D;
       if (f < NS) {
         const int fk = f / 8, fs = f % 8;
@@ -324,14 +365,17 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
             sc = __uint_as_float(j == 0 ? Lr.sf.x : j == 1 ? Lr.sf.y : j == 2 ? Lr.sf.z : Lr.sf.w) *
                  valid;
           } else {
+            // a 256-block absmax group spans 64 K-lines: a wave's lines see
+            // at most two groups
             const float amax = ((nrow[t] * KB + 4 * kl) >> 8) == ((nrow[t] * KB + 4 * kl0) >> 8)
                                    ? am0[t]
                                    : am1[t];
             sc = (float)(int8_t)((L[kk][t].sf.x >> (8 * j)) & 255u) *
-                 (amax * (1.0f / 127.0f)) * valid;
+                 (amax * (1.0f / 127.0f) * valid);
           }
+          // only D rows < 2M (lane group 0) carry output
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[t][v] = fmaf(sc, d[t][v], acc[t][v]);
+          for (int v = 0; v < M2; ++v) acc[t][v] = fmaf(sc, d[t][v], acc[t][v]);
         }
       }
       // Keep the steps in order: hoisted early, a later line's regrouping
@@ -468,7 +512,7 @@ StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
   const int64_t KLW = (KL + kLW - 1) / kLW;
   if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW)) return p;
   const int64_t G = (T + R - 1) / R;
-  const size_t lds = kTabBytes + (size_t)KL * 16 * 2 * M * 4 * 8 +
+  const size_t lds = kTabBytes + (size_t)KL * 16 * 2 * M * 4 * (M == 1 ? 16 : 8) +
                      (size_t)16 * R * (r > 0 ? r : 1) * 4 +
                      (size_t)(KL * M * r > 0 ? KL * M * r : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
                      64 * 4 + 16 * 4;
