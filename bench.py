@@ -47,7 +47,54 @@ def parse():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter probe: a few eager C2 batch-1 launches of each layer "
+                         "and a 256 MiB device copy (the HBM-traffic calibration), "
+                         "for rocprofv3 --pmc; prints no JSON line")
     return ap.parse_args()
+
+
+def probe(ctx, torch, dev, QD):
+    """Kernels for the HBM-traffic counters: each C2 layer's batch-1 forward
+    five times (eager, distinct weight copies) and a plain 256 MiB copy."""
+    r, alpha = 16, 32.0
+    g = torch.Generator(device="cuda").manual_seed(0x1234)
+    for N, K in [(11008, 4096), (4096, 11008)]:
+        w = torch.randn(N, K, device=dev, generator=g) * 0.02
+        base = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+        del w
+        a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) / math.sqrt(K)
+        b = torch.randn(N, r, device=dev, generator=g) * 0.01
+        lora = QD.lora_struct(a, b, r, alpha)
+        x = torch.randn(1, K, device=dev, generator=g)
+        y = torch.empty(1, N, device=dev)
+        copies = [base.clone() for _ in range(5)]
+        for c in copies:
+            QD.forward(c, lora, x, 1, y, ctx=ctx)
+        torch.cuda.synchronize()
+        del copies
+    src = torch.empty(64 << 20, device=dev)  # 256 MiB of fp32
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("# probe done", file=sys.stderr, flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed counter summary
+    (profiles/decode_c2_traffic.md: FETCH_SIZE + WRITE_SIZE per dispatch of
+    the decode kernel, scaled by the same counters on a copy of known size),
+    or None when that summary is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_c2_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -300,6 +347,9 @@ def main():
     dev = torch.device("cuda:0")
     ctx = qlora_hip.default_context()
     print(f"# device: {ctx.device_name()}", file=sys.stderr, flush=True)
+    if args.probe:
+        probe(ctx, torch, dev, QD)
+        return
 
     dec, dec_cfg = decode_bench(args, ctx, torch, dev, QD)
     print(f"# decode done: {json.dumps({b: round(v['weight_gbs'], 1) for b, v in dec.items()})}",
@@ -327,7 +377,7 @@ def main():
                     achieved=d1["main_kernel_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=d1["main_kernel_gbs"] / HBM_PEAK_GBS,
                     bytes_per_launch=d1["main_kernel_bytes"],
-                    avg_launch_ms=d1["main_kernel_ms"], traffic=None)
+                    avg_launch_ms=d1["main_kernel_ms"], traffic=measured_traffic())
     line = {
         "metric": METRIC,
         "value": d1["weight_gbs"],
