@@ -52,9 +52,15 @@ constexpr int kThreads = kLW * 64;
 constexpr int kCopies = 32;               // codebook table copies
 constexpr uint32_t kTabBytes = 256u * kCopies * 8u;  // 64 KiB at LDS offset 0
 constexpr int kMaxLines = 8;   // code lines a wave holds in registers
-constexpr int kT1Loads = 4;    // T1 line partials per thread (NL * M * r <= 2048)
+constexpr int kT1Words = 32;  // slices per lane of the summing wave
+constexpr int kT1Loads = 4;   // tagged T1 partials read per thread (P * M * r <= 2048)
 constexpr int kLinesAhead = 3; // K-lines of loads a wave keeps in flight
-constexpr int kT1PerThread = 8; // line partials per thread in the T1 sum (NL <= 64)
+constexpr int kMaxSlices = 128;  // T1 slices (producing workgroups)
+// float4 units of A per producer lane: the producer's loads are live
+// through the first code lines, so wide tiles (more registers per line) get
+// fewer of them.
+__host__ __device__ constexpr int t1_units(int R) { return R == 1 ? 6 : 2; }
+constexpr int kTagPolls = 64;    // re-reads of a stale tagged partial before the fallback
 constexpr uint32_t kLdsLimit = 160u * 1024u;
 
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
@@ -152,6 +158,79 @@ __device__ __forceinline__ void mfma_step(const StepOps<R> &o, floatx4 (&d)[R]) 
 
 // X fragments of one K-line for this lane's unit (s, p, g4): hi part to
 // row m, lo part to row M + m, as (P_ab, P_cd) pairs.
+// Number of T1 slices (producing workgroups) of a launch of G workgroups:
+// one wave sums the P * M * r tagged partials, lane (o, q) for output
+// o = l % MR and q = l / MR < 64 / MR taking slices q, q + 64 / MR, ...,
+// at most kT1Words of them.
+__host__ __device__ constexpr int t1_slices(int G, int MR) {
+  return MR <= 0 || MR > 64
+             ? 1
+             : (G < kMaxSlices ? G : kMaxSlices) < kT1Loads * kThreads / MR
+                   ? (G < kMaxSlices ? G : kMaxSlices)
+                   : kT1Loads * kThreads / MR;
+}
+
+// Largest power of two <= v (v >= 1).
+__device__ __forceinline__ int pow2_floor(int v) { return 1 << (31 - __clz(v)); }
+
+// T1 slice c of P: float4 units [U c / P, U (c+1) / P) of K.  Lane l covers
+// row j = l / LPJ of A and units u0 + (l % LPJ) + LPJ i.  load() issues the
+// loads; reduce() returns the slice's partial of (m, j) in the row's first
+// lane (the LPJ lanes of a row add by butterfly).  The same instructions run
+// in a producer and in the fallback, so a slice's bits do not depend on who
+// computes it.
+template <int XBF16, int M, int kT1Units>
+struct T1Slice {
+  float4 av[kT1Units], xv[kT1Units][M];
+  int64_t u0, u1;
+  int lpj, sub;
+  __device__ __forceinline__ void load(const void *x, const float *a, int64_t K, int r, int c,
+                                       int P, int lane) {
+    const int64_t U = K / 4;
+    u0 = U * c / P;
+    u1 = U * (c + 1) / P;
+    lpj = pow2_floor(64 / r);
+    const int j = lane / lpj, jj = j < r ? j : r - 1;
+    sub = lane % lpj;
+#pragma unroll
+    for (int i = 0; i < kT1Units; ++i) {
+      int64_t u = u0 + sub + (int64_t)lpj * i;
+      u = u < u1 ? u : u1 - 1;
+      av[i] = *(const float4 *)(a + (int64_t)jj * K + 4 * u);
+#pragma unroll
+      for (int m = 0; m < M; ++m) xv[i][m] = load_x4<XBF16>(x, (int64_t)m * K + 4 * u);
+    }
+  }
+  __device__ __forceinline__ void reduce(float (&p)[M]) const {
+#pragma unroll
+    for (int m = 0; m < M; ++m) p[m] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kT1Units; ++i) {
+      const bool ok = u0 + sub + (int64_t)lpj * i < u1;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float t = xv[i][m].x * av[i].x;
+        t = fmaf(xv[i][m].y, av[i].y, t);
+        t = fmaf(xv[i][m].z, av[i].z, t);
+        t = fmaf(xv[i][m].w, av[i].w, t);
+        p[m] += ok ? t : 0.0f;
+      }
+    }
+    for (int off = lpj >> 1; off >= 1; off >>= 1) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) p[m] += __shfl_xor(p[m], off);
+    }
+  }
+};
+
+__device__ __forceinline__ void st_dev64(uint64_t *p, uint64_t v) {
+  __hip_atomic_store((unsigned long long *)p, (unsigned long long)v, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev64(const uint64_t *p) {
+  return __hip_atomic_load((unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Two floats to a bf16 pair (round to nearest even: v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -185,15 +264,26 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 }
 
 // grid = G workgroups of kThreads; workgroup c owns tiles [c R, c R + R).
-// t1p: the NL x M x r line partials of T1 (k_t1p, launched just before).
+// T1 = X A^T in P slices (t1_slices): wave 0 of workgroup c < P computes
+// slice c near the start and stores it as (tag, value) words, tag =
+// epoch + 1, with no wait; every workgroup reads all P x M x r words with
+// its last code lines (a few per thread), re-reads a word whose tag is
+// stale, and wave 0 sums the slices in order.  The epoch numbers launches: 16 counters (epochs[s]),
+// each advanced by exactly 16 per launch (+1 by every workgroup c with
+// c % 16 == s at its end, the rest by workgroup s % G), so epoch =
+// counter / 16 read at a workgroup's start is the same in every workgroup
+// of a launch (its own contribution is not in yet) and new in every launch.
+// t1w: kMaxSlices * 64 words, zero before the first launch (tag 0 is never
+// current).
 // Dynamic LDS (byte offsets): [0, 64K) table | X fragments (KL M KiB, by
-// K-line) | lbs (16 R r floats) | T1 partials (NL M r floats) | red
-// (kLW R 16 M floats) | t1s (64 floats) | nib (16 words).
+// K-line) | lbs (16 R r floats) | red (kLW R 16 M floats) | t1s (64
+// floats) | nib (16 words) | flag | T1 slice partials (P M r floats).
 template <int XBF16, int KIND, int M, int R, int KLW>
 __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__restrict__ x,
-                                                      int r, const float *__restrict__ lb,
-                                                      float s_lora,
-                                                      const float *__restrict__ t1p,
+                                                      const float *__restrict__ a, int r,
+                                                      const float *__restrict__ lb,
+                                                      float s_lora, uint64_t *__restrict__ t1w,
+                                                      uint64_t *__restrict__ epochs,
                                                       float *__restrict__ t1_out,
                                                       float *__restrict__ y) {
   static_assert(R * KLW <= kMaxLines, "code lines per wave");
@@ -204,13 +294,15 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   const int64_t N = w.rows, K = w.cols, KB = K >> 6;
   const int KL = (int)(K / kLine), c = blockIdx.x;
   const int64_t n0 = (int64_t)c * R * 16;
-  const int MR = M * r, NMR = KL * MR;
+  const int MR = M * r;
+  const int G = gridDim.x, P = t1_slices(G, MR), NMR = P * MR;
   const uint32_t o_x = kTabBytes;
   const uint32_t o_lb = o_x + (uint32_t)KL * kFragLine;
-  const uint32_t o_tp = o_lb + (uint32_t)(16 * R * (r > 0 ? r : 1)) * 4;
-  const uint32_t o_red = o_tp + (uint32_t)(NMR > 0 ? NMR : 1) * 4;
+  const uint32_t o_red = o_lb + (uint32_t)(16 * R * (r > 0 ? r : 1)) * 4;
   const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
   const uint32_t o_nib = o_t1 + 64 * 4;
+  const uint32_t o_flag = o_nib + 16 * 4;  // set when a T1 slice never arrived
+  const uint32_t o_tp = o_flag + 16;        // T1 slice partials
 
   const int kl0 = KL * wave / kLW, nkl = KL * (wave + 1) / kLW - kl0;
   const int nl = lane & 15, g = lane >> 4;
@@ -246,24 +338,37 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
 #pragma unroll
     for (int t = 0; t < R; ++t) load_line<KIND>(L[kk][t], w, nrow[t], KB, crow[t], kl, g);
   };
-  // The epilogue's operands (LoRA B rows of the workgroup's tiles, 16 R r
-  // <= 2 R * 512 floats, and the T1 line partials) go out after the last
-  // code line: issued earlier, they would hold back every line behind them.
-  float lbv[2 * R], tpv[kT1Loads];
+  // The epilogue's operands: LoRA B rows of the workgroup's tiles (16 R r
+  // <= 2 R * 512 floats), the launch epoch and the tagged T1 partials.
+  float lbv[2 * R];
+  // Wave 0 produces slice c (c < P) and sums all slices.
+  const int LPO = MR > 0 ? 64 / MR : 1;              // lanes per T1 output
+  const int PP = kT1Words * LPO;                      // slice stride of the partials
+  const int to = lane % (MR > 0 ? MR : 1), tq = lane / (MR > 0 ? MR : 1);
+  const bool t1lane = tq < LPO;                       // lanes past LPO*MR idle
+  uint64_t tpv[kT1Loads];  // tagged partials tid + 512 q
+  const bool producer = r > 0 && wave == 0 && c < P;
+  T1Slice<XBF16, M, t1_units(R)> t1s;
+  uint64_t ev = 0;  // the epoch counter word (epoch = ev / 16)
+  int lbi[2 * R];  // element offsets into B, computed once (N r < 2^31)
+#pragma unroll
+  for (int q = 0; q < 2 * R; ++q) {
+    const int rr = r > 0 ? r : 1;
+    int idx = tid + 512 * q;
+    idx = idx < 16 * R * rr ? idx : 16 * R * rr - 1;
+    int64_t row = n0 + idx / rr;
+    row = row < N ? row : N - 1;
+    lbi[q] = (int)(row * rr + idx % rr);
+  }
   auto issue_tail = [&]() {
     if (r > 0) {
 #pragma unroll
-      for (int q = 0; q < 2 * R; ++q) {
-        int idx = tid + 512 * q;
-        idx = idx < 16 * R * r ? idx : 16 * R * r - 1;
-        int64_t row = n0 + idx / r;
-        row = row < N ? row : N - 1;
-        lbv[q] = lb[row * r + idx % r];
-      }
+      for (int q = 0; q < 2 * R; ++q) lbv[q] = lb[lbi[q]];
+      if (!producer) ev = ld_dev64(epochs + (c & 15));
 #pragma unroll
       for (int q = 0; q < kT1Loads; ++q) {
         const int i = tid + 512 * q;
-        tpv[q] = t1p[i < NMR ? i : NMR - 1];
+        tpv[q] = ld_dev64(t1w + (i < NMR ? i : NMR - 1));
       }
     }
   };
@@ -271,7 +376,6 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   // The first K-line goes out before the table is built (a few loads per
   // wave do not stall issue), the rest after it.
   issue_line(0);
-  if (KLW == 1) issue_tail();
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- the codebook table, from constants: no memory round trip --------
@@ -298,12 +402,34 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
     }
   }
+  if (tid == 0) *LDS_AT(lds_f, o_flag) = 0.0f;
   lds_barrier();  // B1: the table is in LDS
   __builtin_amdgcn_sched_barrier(0);
+  // A producer's T1 slice and the launch epoch go out right behind its
+  // first code line (the slice is computed when the second line is due).
+  if (producer) {
+    t1s.load(x, a, K, r, c, P, lane);
+    ev = ld_dev64(epochs + (c & 15));
+  }
+  auto publish = [&]() {
+    if (producer) {
+      float pm[M];
+      t1s.reduce(pm);
+      const int j = lane / t1s.lpj;
+      if (t1s.sub == 0 && j < r) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          st_dev64(t1w + (c * M + m) * r + j, ((ev >> 4) + 1) << 32 | __float_as_uint(pm[m]));
+      }
+    }
+  };
 
 #pragma unroll
   for (int kk = 1; kk < DL; ++kk) issue_line(kk);
-  if (DL == KLW && KLW > 1) issue_tail();
+  __builtin_amdgcn_sched_barrier(0);
+  // The slice is published as soon as its operands are in (they follow
+  // line 0, which the wave waits for next anyway).
+  publish();
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- the weight stream ----------------------------------------------
@@ -335,10 +461,10 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int kk = i / 8, s = i % 8;
-      if (s == 0 && kk + DL < KLW) {
-        issue_line(kk + DL);
-        if (kk + DL == KLW - 1) issue_tail();
-      }
+      if (s == 0 && kk + DL < KLW) issue_line(kk + DL);
+      // The epilogue's operands go out when the last line starts: the
+      // producers have published by then.
+      if (i == (KLW - 1) * 8) issue_tail();
       const int f = i + D;
       if (f < NS) {
         const int fk = f / 8, fs = f % 8;
@@ -398,43 +524,93 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       const int idx = tid + 512 * q;
       if (idx < 16 * R * r) *LDS_AT(lds_f, o_lb + (uint32_t)idx * 4) = lbv[q];
     }
+  }
+  if (r > 0) {
+    // Tagged partials: a word whose tag is not this launch's is re-read a
+    // bounded number of times; the values go to LDS.
+    const uint32_t want = (uint32_t)(ev >> 4) + 1;
+    bool stale = false;
 #pragma unroll
     for (int q = 0; q < kT1Loads; ++q) {
       const int i = tid + 512 * q;
-      if (i < NMR) *LDS_AT(lds_f, o_tp + (uint32_t)i * 4) = tpv[q];
+      if (i < NMR) {
+        uint64_t v = tpv[q];
+        for (int it = 0; it < kTagPolls && (uint32_t)(v >> 32) != want; ++it) {
+          __builtin_amdgcn_s_sleep(4);
+          v = ld_dev64(t1w + i);
+        }
+        stale |= (uint32_t)(v >> 32) != want;
+        // stored transposed, [output][slice], so a lane reads a run of slices
+        const int cc = i / MR, o = i - cc * MR;
+        *LDS_AT(lds_f, o_tp + (uint32_t)(o * PP + cc) * 4) = __uint_as_float((uint32_t)v);
+      }
     }
+    if (stale) *LDS_AT(lds_f, o_flag) = 1.0f;
   }
-  lds_barrier();  // B2: partial sums, B rows and T1 partials are in LDS
-
-  // T1[o] = sum of the NL line partials, in the same fixed order in every
-  // workgroup: thread (o, q < 8) adds lines q, q + 8, ...; then the eight
-  // sums add up in q order.
-  const uint32_t o_q = o_x;  // the X fragments are dead: 8 x MR floats
+  lds_barrier();  // B2: partial sums, B rows and T1 slice partials are in LDS
   if (r > 0) {
-    if (tid < 8 * MR) {
-      const int o = tid % MR, q = tid / MR;
-      float v[kT1PerThread];
+    if (*LDS_AT(const lds_f, o_flag) == 0.0f && wave == 0) {
+      // T1[o] = sum over slices in order: lane (o, q) adds slices
+      // [32 q, 32 q + 32) in order; lanes q = 0..LPO-1 of an output then add
+      // up in q order.
+      float v[kT1Words];
+      const uint32_t a0 = o_tp + (uint32_t)(to * PP + kT1Words * tq) * 4;
 #pragma unroll
-      for (int i = 0; i < kT1PerThread; ++i) {
-        const int cl = q + 8 * i;
-        v[i] = *LDS_AT(const lds_f, o_tp + (uint32_t)((cl < KL ? cl : KL - 1) * MR + o) * 4);
+      for (int k = 0; k < kT1Words; k += 4) {
+        const v4u q4 = *LDS_AT(const lds_u4, a0 + (uint32_t)k * 4);
+        v[k] = __uint_as_float(q4.x);
+        v[k + 1] = __uint_as_float(q4.y);
+        v[k + 2] = __uint_as_float(q4.z);
+        v[k + 3] = __uint_as_float(q4.w);
       }
       float t = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kT1PerThread; ++i) t += q + 8 * i < KL ? v[i] : 0.0f;
-      *LDS_AT(lds_f, o_q + (uint32_t)(q * MR + o) * 4) = t;
+      for (int k = 0; k < kT1Words; ++k) t += t1lane && kT1Words * tq + k < P ? v[k] : 0.0f;
+      float tot = t;
+      for (int q = 1; q < LPO; ++q) tot += __shfl(t, to + q * MR);
+      if (tq == 0 && t1lane) {
+        *LDS_AT(lds_f, o_t1 + (uint32_t)to * 4) = tot;
+        if (t1_out && c == 0) t1_out[to] = tot;
+      }
     }
-    lds_barrier();
-    if (tid < MR) {
-      float v[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = *LDS_AT(const lds_f, o_q + (uint32_t)(q * MR + tid) * 4);
-      const float t = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-      *LDS_AT(lds_f, o_t1 + (uint32_t)tid * 4) = t;
-      if (t1_out && c == 0) t1_out[tid] = t;
-    }
-    lds_barrier();  // B3: T1 is in LDS
   }
+  if (r > 0 && *LDS_AT(const lds_f, o_flag) != 0.0f) {
+    // Some slice never arrived (its workgroup not resident): wave 0 computes
+    // every slice with the producers' code and sums them in the same order.
+    if (wave == 0) {
+      float part[kT1Words];
+#pragma unroll
+      for (int k = 0; k < kT1Words; ++k) part[k] = 0.0f;
+      for (int cc = 0; cc < P; ++cc) {
+        T1Slice<XBF16, M, t1_units(R)> f;
+        f.load(x, a, K, r, cc, P, lane);
+        float pm[M];
+        f.reduce(pm);
+        // the slice's (m, j) value sits in lane j * lpj: hand it to lane (o, q)
+        const int o = to, m = o / r, j = o % r;
+        float v = 0.0f;
+#pragma unroll
+        for (int mm = 0; mm < M; ++mm) {
+          const float vm = __shfl(pm[mm], j * f.lpj);
+          v = mm == m ? vm : v;
+        }
+        const int k = cc - kT1Words * tq;
+#pragma unroll
+        for (int kk = 0; kk < kT1Words; ++kk)
+          if (t1lane && kk == k) part[kk] += v;
+      }
+      float t = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kT1Words; ++k) t += part[k];
+      float tot = t;
+      for (int q = 1; q < LPO; ++q) tot += __shfl(t, to + q * MR);
+      if (tq == 0 && t1lane) {
+        *LDS_AT(lds_f, o_t1 + (uint32_t)to * 4) = tot;
+        if (t1_out && c == 0) t1_out[to] = tot;
+      }
+    }
+  }
+  if (r > 0) lds_barrier();  // B3: T1 is in LDS
   if (tid < R * M * 16) {
     const int t = tid / (M * 16), m = (tid / 16) % M, rn = tid % 16;
     const int64_t n = n0 + 16 * t + rn;
@@ -463,6 +639,14 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       sum = fmaf(s_lora, l, sum);
     }
     if (n < N) y[(int64_t)m * N + n] = sum;
+  }
+  if (r > 0 && tid == 0) {
+    // This launch's share of the epoch counters (non-returning atomics).
+    atomicAdd((unsigned long long *)(epochs + (c & 15)), 1ull);
+    for (int sg = c; sg < 16; sg += G) {
+      const int ns = G / 16 + (sg < G % 16 ? 1 : 0);
+      if (16 - ns > 0) atomicAdd((unsigned long long *)(epochs + sg), (unsigned long long)(16 - ns));
+    }
   }
 }
 
@@ -507,15 +691,26 @@ StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
   if (w.kind == 0 ? (((uintptr_t)w.scales) & 15) != 0 : (((uintptr_t)w.scale_codes) & 3) != 0)
     return p;
   const int64_t T = (w.rows + 15) / 16, KL = w.cols / kLine;
-  if (KL < kLW || KL > 8 * kT1PerThread || KL * M * r > (int64_t)kT1Loads * kThreads) return p;
+  if (KL < kLW) return p;
   const int64_t R = (T + cus - 1) / cus;
   const int64_t KLW = (KL + kLW - 1) / kLW;
   if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW)) return p;
   const int64_t G = (T + R - 1) / R;
+  const int64_t P = t1_slices((int)G, (int)(M * r));
+  if (r > 0) {
+    // T1 slices: every producer lane covers at most kT1Units float4 units.
+    const int64_t lpj = (int64_t)1 << (63 - __builtin_clzll(64 / r));
+    const int64_t units = (w.cols / 4 + P - 1) / P;
+    if (w.cols / 4 < P || (units + lpj - 1) / lpj > t1_units((int)R)) return p;
+    if ((P + 64 / (M * r) - 1) / (64 / (M * r)) > kT1Words ||
+        P * M * r > (int64_t)kT1Loads * kThreads || P * M * r * 4 > (int64_t)kTabBytes)
+      return p;
+  }
+  // T1 slice partials: the summing wave reads kT1Words * 64 floats at most
+  const size_t t1_floats = r > 0 ? (size_t)kT1Words * (64 / (M * r)) * (M * r) + 4 : 0;
   const size_t lds = kTabBytes + (size_t)KL * 16 * 2 * M * 4 * (M == 1 ? 16 : 8) +
-                     (size_t)16 * R * (r > 0 ? r : 1) * 4 +
-                     (size_t)(KL * M * r > 0 ? KL * M * r : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
-                     64 * 4 + 16 * 4;
+                     (size_t)16 * R * (r > 0 ? r : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
+                     64 * 4 + 16 * 4 + 16 + t1_floats * 4;
   if (lds > kLdsLimit) return p;
   p.R = (int)R;
   p.KLW = (int)KLW;
@@ -526,9 +721,9 @@ StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
 }
 
 template <int XBF16, int KIND, int M, int R, int KLW>
-hipError_t run_stream(const DevQW &w, const void *x, int r, const float *lb, float s,
-                      const float *t1p, float *t1_out, float *y, const StreamPlan &p,
-                      hipStream_t st) {
+hipError_t run_stream(const DevQW &w, const void *x, const float *a, int r, const float *lb,
+                      float s, uint64_t *t1w, uint64_t *epochs, float *t1_out, float *y,
+                      const StreamPlan &p, hipStream_t st) {
   auto k = k_dstream<XBF16, KIND, M, R, KLW>;
   static bool attr = false;  // per instantiation; the attribute is per function
   if (!attr) {
@@ -538,17 +733,17 @@ hipError_t run_stream(const DevQW &w, const void *x, int r, const float *lb, flo
     if (e != hipSuccess) return e;
     attr = true;
   }
-  return qh_launch(k, dim3((unsigned)p.G), dim3(kThreads), p.lds, st, w, x, r, lb, s, t1p,
-                   t1_out, y);
+  return qh_launch(k, dim3((unsigned)p.G), dim3(kThreads), p.lds, st, w, x, a, r, lb, s, t1w,
+                   epochs, t1_out, y);
 }
 
 template <int XBF16, int KIND, int M>
-hipError_t dispatch_shape(const DevQW &w, const void *x, int r, const float *lb, float s,
-                          const float *t1p, float *t1_out, float *y, const StreamPlan &p,
-                          hipStream_t st) {
+hipError_t dispatch_shape(const DevQW &w, const void *x, const float *a, int r, const float *lb,
+                          float s, uint64_t *t1w, uint64_t *epochs, float *t1_out, float *y,
+                          const StreamPlan &p, hipStream_t st) {
 #define QH_SHAPE_CASE(rr, kk) \
   if (p.R == rr && p.KLW == kk) \
-    return run_stream<XBF16, KIND, M, rr, kk>(w, x, r, lb, s, t1p, t1_out, y, p, st);
+    return run_stream<XBF16, KIND, M, rr, kk>(w, x, a, r, lb, s, t1w, epochs, t1_out, y, p, st);
   QH_STREAM_SHAPES(QH_SHAPE_CASE)
 #undef QH_SHAPE_CASE
   return hipErrorInvalidValue;
@@ -559,13 +754,14 @@ hipError_t dispatch_shape(const DevQW &w, const void *x, int r, const float *lb,
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r) { return stream_plan(w, M, r).ok; }
 
 hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M,
-                                const float *lb, int64_t r, float s, float *y, float *t1_out,
-                                const void *scratch, hipStream_t st) {
+                                const float *a, int64_t r, const float *lb, float s, float *y,
+                                float *t1_out, unsigned *tickets, hipStream_t st) {
   const StreamPlan p = stream_plan(w, M, r);
   if (!p.ok) return hipErrorInvalidValue;
-  const float *t1p = (const float *)scratch;
+  uint64_t *epochs = (uint64_t *)(tickets + kStreamEpochWord);
+  uint64_t *t1w = (uint64_t *)(tickets + kTicketWords);
   const int ri = (int)r;
-#define QH_ARGS w, x, ri, lb, s, t1p, t1_out, y, p, st
+#define QH_ARGS w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st
   if (M == 1) {
     if (x_bf16) return w.kind == 0 ? dispatch_shape<1, 0, 1>(QH_ARGS) : dispatch_shape<1, 1, 1>(QH_ARGS);
     return w.kind == 0 ? dispatch_shape<0, 0, 1>(QH_ARGS) : dispatch_shape<0, 1, 1>(QH_ARGS);

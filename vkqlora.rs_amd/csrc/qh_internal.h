@@ -131,12 +131,17 @@ hipError_t launch_decode_small(const DevQW &w, const void *x, int x_bf16, int64_
                                void *scratch, unsigned *tickets, hipStream_t st);
 // ---- k_dstream.hip ----
 // Decode GEMV for batches of 1 and 2 rows in one launch per layer (at most
-// one workgroup per CU).  With an adapter, launch_decode_t1 runs first on
-// the same stream and `scratch` holds its T1 line partials.
+// one workgroup per CU), T1 = X A^T included.  It keeps 16 launch counters
+// (uint64) at tickets[kStreamEpochWord..] and tagged T1 partials in the
+// kStreamT1Words words after the kTicketWords counter words; both must be
+// zero before the first launch, and calls sharing them must be
+// stream-ordered.
+constexpr int kStreamEpochWord = 32;
+constexpr int kStreamT1Words = 128 * 64 * 2;
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r);
 hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M,
-                                const float *lb, int64_t r, float s, float *y, float *t1_out,
-                                const void *scratch, hipStream_t st);
+                                const float *a, int64_t r, const float *lb, float s, float *y,
+                                float *t1_out, unsigned *tickets, hipStream_t st);
 // Tuning knobs of the decode GEMV: codebook table (0 = 16-entry nibble
 // table, 1 = 256-entry byte-pair table) and the workgroup count the K split
 // aims for.

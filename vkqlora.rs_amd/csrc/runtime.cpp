@@ -389,17 +389,10 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   }
 
   if (decode && g_decode_path == 0 && qh::decode_stream_ok(W, M, r)) {
-    Carve cd;
-    size_t i_sc = cd.add(qh::decode_small_scratch_bytes(M, N, K, r));
-    auto pd = cd.bind(ctx->scratch);
     const int xb = xe == qh::E_BF16;
-    if (lora)
-      timed(ctx, "decode_t1", s, [&] {
-        return qh::launch_decode_t1(W, x, xb, M, l->a, r, pd[i_sc], s);
-      });
     timed(ctx, "decode_stream", s, [&] {
-      return qh::launch_decode_stream(W, x, xb, M, lora ? l->b : nullptr, r, sc, y, t1_out,
-                                      pd[i_sc], s);
+      return qh::launch_decode_stream(W, x, xb, M, lora ? l->a : nullptr, r,
+                                      lora ? l->b : nullptr, sc, y, t1_out, ctx->tickets, s);
     });
     return;
   }
@@ -624,8 +617,10 @@ qh_status qh_ctx_create(qh_ctx **out) {
     snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
   if ((e = hipSetDevice(c->device)) != hipSuccess ||
       (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
-      (e = hipMalloc((void **)&c->tickets, qh::kTicketWords * 4)) != hipSuccess ||
-      (e = hipMemset(c->tickets, 0, qh::kTicketWords * 4)) != hipSuccess ||
+      (e = hipMalloc((void **)&c->tickets, (qh::kTicketWords + qh::kStreamT1Words) * 4)) !=
+          hipSuccess ||
+      (e = hipMemset(c->tickets, 0, (qh::kTicketWords + qh::kStreamT1Words) * 4)) !=
+          hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
     if (c->tickets) (void)hipFree(c->tickets);
     if (c->stream) (void)hipStreamDestroy(c->stream);
