@@ -268,11 +268,13 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 // slice c near the start and stores it as (tag, value) words, tag =
 // epoch + 1, with no wait; every workgroup reads all P x M x r words with
 // its last code lines (a few per thread), re-reads a word whose tag is
-// stale, and wave 0 sums the slices in order.  The epoch numbers launches: 16 counters (epochs[s]),
-// each advanced by exactly 16 per launch (+1 by every workgroup c with
-// c % 16 == s at its end, the rest by workgroup s % G), so epoch =
-// counter / 16 read at a workgroup's start is the same in every workgroup
-// of a launch (its own contribution is not in yet) and new in every launch.
+// stale, and wave 0 sums the slices in order.
+// The epoch numbers launches: 16 counters (epochs[s]), each advanced by
+// exactly 16 per launch (+1 by every workgroup c with c % 16 == s, the rest
+// by workgroup s % G, each right after its own read of its counter), so
+// epoch = counter / 16 as read by a workgroup is the same in every
+// workgroup of a launch (its own contribution is not in yet) and new in
+// every launch.
 // t1w: kMaxSlices * 64 words, zero before the first launch (tag 0 is never
 // current).
 // Dynamic LDS (byte offsets): [0, 64K) table | X fragments (KL M KiB, by
@@ -302,6 +304,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
   const uint32_t o_nib = o_t1 + 64 * 4;
   const uint32_t o_flag = o_nib + 16 * 4;  // set when a T1 slice never arrived
+  const uint32_t o_ep = o_flag + 4;         // epoch + 1 (0: not yet known)
   const uint32_t o_tp = o_flag + 16;        // T1 slice partials
 
   const int kl0 = KL * wave / kLW, nkl = KL * (wave + 1) / kLW - kl0;
@@ -364,7 +367,6 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     if (r > 0) {
 #pragma unroll
       for (int q = 0; q < 2 * R; ++q) lbv[q] = lb[lbi[q]];
-      if (!producer) ev = ld_dev64(epochs + (c & 15));
 #pragma unroll
       for (int q = 0; q < kT1Loads; ++q) {
         const int i = tid + 512 * q;
@@ -373,6 +375,8 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     }
   };
   constexpr int DL = KLW < kLinesAhead ? KLW : kLinesAhead;
+  // Wave 0 reads the launch epoch first (it returns with line 0).
+  if (r > 0 && wave == 0) ev = ld_dev64(epochs + (c & 15));
   // The first K-line goes out before the table is built (a few loads per
   // wave do not stall issue), the rest after it.
   issue_line(0);
@@ -402,16 +406,31 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
     }
   }
-  if (tid == 0) *LDS_AT(lds_f, o_flag) = 0.0f;
+  if (tid == 0) {
+    *LDS_AT(lds_f, o_flag) = 0.0f;
+    *LDS_AT(lds_f, o_ep) = 0.0f;
+  }
   lds_barrier();  // B1: the table is in LDS
   __builtin_amdgcn_sched_barrier(0);
-  // A producer's T1 slice and the launch epoch go out right behind its
-  // first code line (the slice is computed when the second line is due).
-  if (producer) {
-    t1s.load(x, a, K, r, c, P, lane);
-    ev = ld_dev64(epochs + (c & 15));
-  }
+  // A producer's T1 slice goes out right behind its first code line (the
+  // slice is computed when the second line is due).
+  if (producer) t1s.load(x, a, K, r, c, P, lane);
   auto publish = [&]() {
+    if (r > 0 && wave == 0) {
+      // The epoch is in (it came back with line 0): hand it to the other
+      // waves, then add this workgroup's share to the counters (after its
+      // own read, which is all the epoch argument needs).
+      const uint32_t ep = (uint32_t)(ev >> 4);
+      if (lane == 0) {
+        *LDS_AT(lds_f, o_ep) = __uint_as_float(ep + 1);
+        atomicAdd((unsigned long long *)(epochs + (c & 15)), 1ull);
+        for (int sg = c; sg < 16; sg += G) {
+          const int ns = G / 16 + (sg < G % 16 ? 1 : 0);
+          if (16 - ns > 0)
+            atomicAdd((unsigned long long *)(epochs + sg), (unsigned long long)(16 - ns));
+        }
+      }
+    }
     if (producer) {
       float pm[M];
       t1s.reduce(pm);
@@ -528,8 +547,14 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   if (r > 0) {
     // Tagged partials: a word whose tag is not this launch's is re-read a
     // bounded number of times; the values go to LDS.
-    const uint32_t want = (uint32_t)(ev >> 4) + 1;
-    bool stale = false;
+    // this launch's tag, from wave 0 (written right after B1; a wave gets
+    // here much later, but the read is checked anyway)
+    uint32_t want = __float_as_uint(*LDS_AT(const lds_f, o_ep));
+    for (int it = 0; it < kTagPolls && want == 0; ++it) {
+      __builtin_amdgcn_s_sleep(4);
+      want = __float_as_uint(*(volatile lds_f *)(uintptr_t)o_ep);
+    }
+    bool stale = want == 0;
 #pragma unroll
     for (int q = 0; q < kT1Loads; ++q) {
       const int i = tid + 512 * q;
@@ -639,14 +664,6 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       sum = fmaf(s_lora, l, sum);
     }
     if (n < N) y[(int64_t)m * N + n] = sum;
-  }
-  if (r > 0 && tid == 0) {
-    // This launch's share of the epoch counters (non-returning atomics).
-    atomicAdd((unsigned long long *)(epochs + (c & 15)), 1ull);
-    for (int sg = c; sg < 16; sg += G) {
-      const int ns = G / 16 + (sg < G % 16 ? 1 : 0);
-      if (16 - ns > 0) atomicAdd((unsigned long long *)(epochs + sg), (unsigned long long)(16 - ns));
-    }
   }
 }
 
