@@ -72,6 +72,27 @@ typedef __attribute__((address_space(3))) float lds_f;
 // so dynamic LDS starts at 0 and the table needs no base register.
 #define LDS_AT(T, off) ((T *)(uintptr_t)(off))
 
+// Sum of a lane's kT1Words slice partials in a fixed tree order (the
+// padding past the last slice is zero, so it adds exactly nothing).
+__device__ __forceinline__ float sum_slices(const float (&v)[kT1Words]) {
+  float h[kT1Words / 2];
+#pragma unroll
+  for (int k = 0; k < kT1Words / 2; ++k) h[k] = v[2 * k] + v[2 * k + 1];
+#pragma unroll
+  for (int w = kT1Words / 4; w >= 1; w /= 2)
+#pragma unroll
+    for (int k = 0; k < w; ++k) h[k] = h[2 * k] + h[2 * k + 1];
+  return h[0];
+}
+
+// LDS visibility between lanes of one wave (its LDS operations complete in
+// order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 // Barrier over LDS only: waits for this wave's LDS operations, not for its
 // global loads in flight.
 __device__ __forceinline__ void lds_barrier() {
@@ -156,12 +177,26 @@ __device__ __forceinline__ void mfma_step(const StepOps<R> &o, floatx4 (&d)[R]) 
   }
 }
 
-// X fragments of one K-line for this lane's unit (s, p, g4): hi part to
-// row m, lo part to row M + m, as (P_ab, P_cd) pairs.
+// Launch constants of the T1 epilogue, computed on the host.
+struct StreamArgs {
+  int P;       // T1 slices (producing workgroups)
+  int LPO;     // lanes per T1 output in the summing wave: 64 / (M r)
+  int NQ;      // of those, lanes that hold slices: ceil(P / kT1Words) <= 4
+  int r16;     // r rounded up to a multiple of 16
+  int lps;     // log2 of the lanes per A row in a slice
+  float inv_r, inv_mr;  // 1 / r, 1 / (M r) (1 when r = 0)
+};
+
+// floor(v / d) for 0 <= v < 2^22 and d >= 1, with inv = fl(1 / d): (v + 1/2)
+// / d lies at least 1/(2d) from an integer and the two roundings move it by
+// less than (v + 1/2) / d * 2^-23 < 1/(2d).
+__device__ __forceinline__ int div_small(int v, float inv) {
+  return (int)(((float)v + 0.5f) * inv);
+}
+
 // Number of T1 slices (producing workgroups) of a launch of G workgroups:
 // one wave sums the P * M * r tagged partials, lane (o, q) for output
-// o = l % MR and q = l / MR < 64 / MR taking slices q, q + 64 / MR, ...,
-// at most kT1Words of them.
+// o = l % MR and q = l / MR < 64 / MR taking slices [32 q, 32 q + 32).
 __host__ __device__ constexpr int t1_slices(int G, int MR) {
   return MR <= 0 || MR > 64
              ? 1
@@ -169,9 +204,6 @@ __host__ __device__ constexpr int t1_slices(int G, int MR) {
                    ? (G < kMaxSlices ? G : kMaxSlices)
                    : kT1Loads * kThreads / MR;
 }
-
-// Largest power of two <= v (v >= 1).
-__device__ __forceinline__ int pow2_floor(int v) { return 1 << (31 - __clz(v)); }
 
 // T1 slice c of P: float4 units [U c / P, U (c+1) / P) of K.  Lane l covers
 // row j = l / LPJ of A and units u0 + (l % LPJ) + LPJ i.  load() issues the
@@ -182,23 +214,24 @@ __device__ __forceinline__ int pow2_floor(int v) { return 1 << (31 - __clz(v)); 
 template <int XBF16, int M, int kT1Units>
 struct T1Slice {
   float4 av[kT1Units], xv[kT1Units][M];
-  int64_t u0, u1;
+  int u0, u1;
   int lpj, sub;
+  // lps = log2(LPJ), LPJ = the largest power of two <= 64 / r
   __device__ __forceinline__ void load(const void *x, const float *a, int64_t K, int r, int c,
-                                       int P, int lane) {
-    const int64_t U = K / 4;
+                                       int P, int lps, int lane) {
+    const int U = (int)(K / 4);  // K < 2^24: U c < 2^29
     u0 = U * c / P;
     u1 = U * (c + 1) / P;
-    lpj = pow2_floor(64 / r);
-    const int j = lane / lpj, jj = j < r ? j : r - 1;
-    sub = lane % lpj;
+    lpj = 1 << lps;
+    const int j = lane >> lps, jj = j < r ? j : r - 1;
+    sub = lane & (lpj - 1);
 #pragma unroll
     for (int i = 0; i < kT1Units; ++i) {
-      int64_t u = u0 + sub + (int64_t)lpj * i;
+      int u = u0 + sub + lpj * i;
       u = u < u1 ? u : u1 - 1;
-      av[i] = *(const float4 *)(a + (int64_t)jj * K + 4 * u);
+      av[i] = *(const float4 *)(a + (int64_t)jj * K + 4 * (int64_t)u);
 #pragma unroll
-      for (int m = 0; m < M; ++m) xv[i][m] = load_x4<XBF16>(x, (int64_t)m * K + 4 * u);
+      for (int m = 0; m < M; ++m) xv[i][m] = load_x4<XBF16>(x, (int64_t)m * K + 4 * (int64_t)u);
     }
   }
   __device__ __forceinline__ void reduce(float (&p)[M]) const {
@@ -206,7 +239,7 @@ struct T1Slice {
     for (int m = 0; m < M; ++m) p[m] = 0.0f;
 #pragma unroll
     for (int i = 0; i < kT1Units; ++i) {
-      const bool ok = u0 + sub + (int64_t)lpj * i < u1;
+      const bool ok = u0 + sub + lpj * i < u1;
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         float t = xv[i][m].x * av[i].x;
@@ -278,8 +311,9 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 // t1w: kMaxSlices * 64 words, zero before the first launch (tag 0 is never
 // current).
 // Dynamic LDS (byte offsets): [0, 64K) table | X fragments (KL M KiB, by
-// K-line) | lbs (16 R r floats) | red (kLW R 16 M floats) | t1s (64
-// floats) | nib (16 words) | flag | T1 slice partials (P M r floats).
+// K-line) | lbs (16 R r16 floats) | red (kLW R 16 M floats) | t1s (64
+// floats, M r16 used) | flag, epoch | T1 slice partials (M r x 32 LPO
+// floats, zero past slice P).
 template <int XBF16, int KIND, int M, int R, int KLW>
 __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__restrict__ x,
                                                       const float *__restrict__ a, int r,
@@ -287,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
                                                       float s_lora, uint64_t *__restrict__ t1w,
                                                       uint64_t *__restrict__ epochs,
                                                       float *__restrict__ t1_out,
-                                                      float *__restrict__ y) {
+                                                      float *__restrict__ y, StreamArgs sa) {
   static_assert(R * KLW <= kMaxLines, "code lines per wave");
   constexpr int M2 = 2 * M;
   constexpr uint32_t kFragLine = FragOf<M>::kLine;  // bytes of X fragments per K-line
@@ -296,17 +330,6 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   const int64_t N = w.rows, K = w.cols, KB = K >> 6;
   const int KL = (int)(K / kLine), c = blockIdx.x;
   const int64_t n0 = (int64_t)c * R * 16;
-  const int MR = M * r;
-  const int G = gridDim.x, P = t1_slices(G, MR), NMR = P * MR;
-  const uint32_t o_x = kTabBytes;
-  const uint32_t o_lb = o_x + (uint32_t)KL * kFragLine;
-  const uint32_t o_red = o_lb + (uint32_t)(16 * R * (r > 0 ? r : 1)) * 4;
-  const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
-  const uint32_t o_nib = o_t1 + 64 * 4;
-  const uint32_t o_flag = o_nib + 16 * 4;  // set when a T1 slice never arrived
-  const uint32_t o_ep = o_flag + 4;         // epoch + 1 (0: not yet known)
-  const uint32_t o_tp = o_flag + 16;        // T1 slice partials
-
   const int kl0 = KL * wave / kLW, nkl = KL * (wave + 1) / kLW - kl0;
   const int nl = lane & 15, g = lane >> 4;
   int64_t nrow[R];
@@ -319,16 +342,9 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   }
 
   // ---- loads, in order of use (vector-memory data returns in order) ----
-  // absmax first, then per K-line the lane's unit (s, p, g4) of X and the R
-  // code lines; DL K-lines are in flight ahead of the one being computed.
-  float am0[R], am1[R];
-  if (KIND == 1) {
-#pragma unroll
-    for (int t = 0; t < R; ++t) {
-      am0[t] = w.absmax[(nrow[t] * KB + 4 * kl0) >> 8];
-      am1[t] = w.absmax[(nrow[t] * KB + 4 * (kl0 + nkl - 1)) >> 8];
-    }
-  }
+  // Per K-line the lane's unit (s, p, g4) of X and the R code lines; DL
+  // K-lines are in flight ahead of the one being computed.  The first goes
+  // out before anything else is computed (only its addresses precede it).
   const int us = lane >> 3, up = (lane >> 2) & 1, ug = lane & 3;
   const int koff = step_koff(us, ug) + 4 * up;
   float4 xv[KLW][M];
@@ -341,27 +357,104 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
 #pragma unroll
     for (int t = 0; t < R; ++t) load_line<KIND>(L[kk][t], w, nrow[t], KB, crow[t], kl, g);
   };
-  // The epilogue's operands: LoRA B rows of the workgroup's tiles (16 R r
-  // <= 2 R * 512 floats), the launch epoch and the tagged T1 partials.
-  float lbv[2 * R];
+  constexpr int DL = KLW < kLinesAhead ? KLW : kLinesAhead;
+  issue_line(0);
+  __builtin_amdgcn_sched_barrier(0);
+  // absmax (first used at line 0's first block scale) and, in wave 0, the
+  // launch epoch
+  float am0[R], am1[R];
+  if (KIND == 1) {
+#pragma unroll
+    for (int t = 0; t < R; ++t) {
+      am0[t] = w.absmax[(nrow[t] * KB + 4 * kl0) >> 8];
+      am1[t] = w.absmax[(nrow[t] * KB + 4 * (kl0 + nkl - 1)) >> 8];
+    }
+  }
+  uint64_t ev = 0;  // the epoch counter word (epoch = ev / 16)
+  if (r > 0 && wave == 0) ev = ld_dev64(epochs + (c & 15));
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int G = gridDim.x, MR = M * r, P = sa.P, NMR = P * MR, r16 = sa.r16;
+  // B rows and T1 have rows of r16 floats, zero past r
+  const uint32_t o_x = kTabBytes;
+  const uint32_t o_lb = o_x + (uint32_t)KL * kFragLine;
+  const uint32_t o_red = o_lb + (uint32_t)(16 * R * (r > 0 ? r16 : 1)) * 4;
+  const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
+  const uint32_t o_flag = o_t1 + 64 * 4;  // set when a T1 slice never arrived
+  const uint32_t o_ep = o_flag + 4;       // epoch + 1 (0: not yet known)
+  const uint32_t o_tp = o_flag + 16;      // T1 slice partials
+
+  // ---- the codebook table, from constants: no memory round trip --------
+  // Built before most loads are issued: a wave issuing more loads than the
+  // vector-memory queue takes stalls at issue until data drains.  Thread
+  // tid writes entries e = (tid >> 4) + 32 i, copies 2 (tid & 15) + {0, 1}:
+  // pair[e] = {Lh[lo] | Lh[hi] << 16, Ll[lo] | Ll[hi] << 16} with nib[q] =
+  // Lh[q] | Ll[q] << 16, lo = 4 (wave & 3) + lane / 16 and hi = wave / 4 +
+  // 2 i (uniform in the wave).  nib goes into lane q of a register from
+  // immediates (indexed selects would become a constant-memory load).
+  {
+    constexpr Tables kTab = make_tables();
+    int nv = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+      asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(nv) : "s"((int)kTab.nib[q]), "n"(q));
+    const uint32_t nlo =
+        (uint32_t)__builtin_amdgcn_ds_bpermute((4 * (wave & 3) + (lane >> 4)) * 4, nv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = (tid >> 4) + 32 * i;
+      const uint32_t nhi = (uint32_t)__builtin_amdgcn_readlane(nv, (wave >> 2) + 2 * i);
+      const uint32_t ph = (nlo & 0xffffu) | (nhi << 16), pl = (nlo >> 16) | (nhi & 0xffff0000u);
+      *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
+    }
+  }
   // Wave 0 produces slice c (c < P) and sums all slices.
-  const int LPO = MR > 0 ? 64 / MR : 1;              // lanes per T1 output
-  const int PP = kT1Words * LPO;                      // slice stride of the partials
-  const int to = lane % (MR > 0 ? MR : 1), tq = lane / (MR > 0 ? MR : 1);
-  const bool t1lane = tq < LPO;                       // lanes past LPO*MR idle
-  uint64_t tpv[kT1Loads];  // tagged partials tid + 512 q
+  const int LPO = sa.LPO;                 // lanes per T1 output
+  const int PP = kT1Words * LPO;          // slice stride of the partials
+  const int NQ = sa.NQ;                   // lanes per output with slices (<= 4)
+  const int tq = div_small(lane, sa.inv_mr), to = lane - tq * (MR > 0 ? MR : 1);
+  const bool t1lane = tq < LPO;           // lanes past LPO*MR idle
+  if (tid == 0) {
+    *LDS_AT(lds_f, o_flag) = 0.0f;
+    *LDS_AT(lds_f, o_ep) = 0.0f;
+  }
+  if (r > 0) {
+    // zero padding of lbs, t1s and the slice partials
+    const v4u z4 = {0u, 0u, 0u, 0u};
+    for (int i = tid; i < 4 * R * r16; i += kThreads) *LDS_AT(lds_u4, o_lb + (uint32_t)i * 16) = z4;
+    if (tid < 16) *LDS_AT(lds_u4, o_t1 + (uint32_t)tid * 16) = z4;
+    for (int i = tid; i < MR * PP / 4; i += kThreads) *LDS_AT(lds_u4, o_tp + (uint32_t)i * 16) = z4;
+  }
+  lds_barrier();  // B1: the table is in LDS
+  __builtin_amdgcn_sched_barrier(0);
+  // A producer's T1 slice goes out right behind its first code line (the
+  // slice is computed when the second line is due).
   const bool producer = r > 0 && wave == 0 && c < P;
   T1Slice<XBF16, M, t1_units(R)> t1s;
-  uint64_t ev = 0;  // the epoch counter word (epoch = ev / 16)
-  int lbi[2 * R];  // element offsets into B, computed once (N r < 2^31)
+  if (producer) t1s.load(x, a, K, r, c, P, sa.lps, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  // The epilogue's operands: LoRA B rows of the workgroup's tiles (16 R r
+  // <= 2 R * 512 floats) and the tagged T1 partials.
+  float lbv[2 * R];
+  uint64_t tpv[kT1Loads];  // tagged partials tid + 512 q
+  // T1 element to of this lane, (m, j) = (to / r, to % r), at m r16 + j
+  int t1slot = 0;
+  if (r > 0) {
+    const int m = div_small(to, sa.inv_r);
+    t1slot = m * r16 + (to - m * r);
+  }
+  // element offsets into B (N r < 2^31) and into lbs (-1: none), computed once
+  int lbi[2 * R], lbo[2 * R];
 #pragma unroll
   for (int q = 0; q < 2 * R; ++q) {
     const int rr = r > 0 ? r : 1;
-    int idx = tid + 512 * q;
-    idx = idx < 16 * R * rr ? idx : 16 * R * rr - 1;
-    int64_t row = n0 + idx / rr;
+    const int idx = tid + 512 * q;
+    const int ic = idx < 16 * R * rr ? idx : 16 * R * rr - 1;
+    const int tr = div_small(ic, sa.inv_r), j = ic - tr * rr;
+    int64_t row = n0 + tr;
     row = row < N ? row : N - 1;
-    lbi[q] = (int)(row * rr + idx % rr);
+    lbi[q] = (int)(row * rr + j);
+    lbo[q] = idx < 16 * R * rr ? tr * r16 + j : -1;
   }
   auto issue_tail = [&]() {
     if (r > 0) {
@@ -374,47 +467,6 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       }
     }
   };
-  constexpr int DL = KLW < kLinesAhead ? KLW : kLinesAhead;
-  // Wave 0 reads the launch epoch first (it returns with line 0).
-  if (r > 0 && wave == 0) ev = ld_dev64(epochs + (c & 15));
-  // The first K-line goes out before the table is built (a few loads per
-  // wave do not stall issue), the rest after it.
-  issue_line(0);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- the codebook table, from constants: no memory round trip --------
-  // Built before most loads are issued: a wave issuing more loads than the
-  // vector-memory queue takes stalls at issue until data drains.
-  if (tid < 16) {
-    constexpr Tables kTab = make_tables();
-    uint32_t v = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) v = tid == q ? kTab.nib[q] : v;
-    *LDS_AT(lds_f, o_nib + (uint32_t)tid * 4) = __uint_as_float(v);
-  }
-  lds_barrier();
-  {
-    // Entries e = (tid >> 4) + 32 i, copies 2 (tid & 15) + {0, 1}:
-    // pair[e] = {Lh[lo] | Lh[hi] << 16, Ll[lo] | Ll[hi] << 16}.
-    const uint32_t nlo =
-        __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)((tid >> 4) & 15) * 4));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = (tid >> 4) + 32 * i;
-      const uint32_t nhi = __float_as_uint(*LDS_AT(const lds_f, o_nib + (uint32_t)(e >> 4) * 4));
-      const uint32_t ph = (nlo & 0xffffu) | (nhi << 16), pl = (nlo >> 16) | (nhi & 0xffff0000u);
-      *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
-    }
-  }
-  if (tid == 0) {
-    *LDS_AT(lds_f, o_flag) = 0.0f;
-    *LDS_AT(lds_f, o_ep) = 0.0f;
-  }
-  lds_barrier();  // B1: the table is in LDS
-  __builtin_amdgcn_sched_barrier(0);
-  // A producer's T1 slice goes out right behind its first code line (the
-  // slice is computed when the second line is due).
-  if (producer) t1s.load(x, a, K, r, c, P, lane);
   auto publish = [&]() {
     if (r > 0 && wave == 0) {
       // The epoch is in (it came back with line 0): hand it to the other
@@ -539,10 +591,8 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   }
   if (r > 0) {
 #pragma unroll
-    for (int q = 0; q < 2 * R; ++q) {
-      const int idx = tid + 512 * q;
-      if (idx < 16 * R * r) *LDS_AT(lds_f, o_lb + (uint32_t)idx * 4) = lbv[q];
-    }
+    for (int q = 0; q < 2 * R; ++q)
+      if (lbo[q] >= 0) *LDS_AT(lds_f, o_lb + (uint32_t)lbo[q] * 4) = lbv[q];
   }
   if (r > 0) {
     // Tagged partials: a word whose tag is not this launch's is re-read a
@@ -573,13 +623,12 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     if (stale) *LDS_AT(lds_f, o_flag) = 1.0f;
   }
   lds_barrier();  // B2: partial sums, B rows and T1 slice partials are in LDS
-  if (r > 0) {
-    if (*LDS_AT(const lds_f, o_flag) == 0.0f && wave == 0) {
-      // T1[o] = sum over slices in order: lane (o, q) adds slices
-      // [32 q, 32 q + 32) in order; lanes q = 0..LPO-1 of an output then add
-      // up in q order.
-      float v[kT1Words];
-      const uint32_t a0 = o_tp + (uint32_t)(to * PP + kT1Words * tq) * 4;
+  if (r > 0 && wave == 0) {
+    // T1[o] = the sum of its P slices: lane (o, q) adds slices [32 q, 32 q +
+    // 32) in a fixed tree, then lanes q = 0..NQ-1 of an output add in q order.
+    float v[kT1Words];
+    if (*LDS_AT(const lds_f, o_flag) == 0.0f) {
+      const uint32_t a0 = o_tp + (uint32_t)(to * PP + kT1Words * (t1lane ? tq : 0)) * 4;
 #pragma unroll
       for (int k = 0; k < kT1Words; k += 4) {
         const v4u q4 = *LDS_AT(const lds_u4, a0 + (uint32_t)k * 4);
@@ -588,54 +637,53 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
         v[k + 2] = __uint_as_float(q4.z);
         v[k + 3] = __uint_as_float(q4.w);
       }
-      float t = 0.0f;
+    } else {
+      // Some slice never arrived (its workgroup not resident): wave 0
+      // computes every slice with the producers' code, into the same places.
 #pragma unroll
-      for (int k = 0; k < kT1Words; ++k) t += t1lane && kT1Words * tq + k < P ? v[k] : 0.0f;
-      float tot = t;
-      for (int q = 1; q < LPO; ++q) tot += __shfl(t, to + q * MR);
-      if (tq == 0 && t1lane) {
-        *LDS_AT(lds_f, o_t1 + (uint32_t)to * 4) = tot;
-        if (t1_out && c == 0) t1_out[to] = tot;
-      }
-    }
-  }
-  if (r > 0 && *LDS_AT(const lds_f, o_flag) != 0.0f) {
-    // Some slice never arrived (its workgroup not resident): wave 0 computes
-    // every slice with the producers' code and sums them in the same order.
-    if (wave == 0) {
-      float part[kT1Words];
-#pragma unroll
-      for (int k = 0; k < kT1Words; ++k) part[k] = 0.0f;
+      for (int k = 0; k < kT1Words; ++k) v[k] = 0.0f;
       for (int cc = 0; cc < P; ++cc) {
         T1Slice<XBF16, M, t1_units(R)> f;
-        f.load(x, a, K, r, cc, P, lane);
+        f.load(x, a, K, r, cc, P, sa.lps, lane);
         float pm[M];
         f.reduce(pm);
         // the slice's (m, j) value sits in lane j * lpj: hand it to lane (o, q)
-        const int o = to, m = o / r, j = o % r;
-        float v = 0.0f;
+        const int m = div_small(to, sa.inv_r), j = to - m * r;
+        float u = 0.0f;
 #pragma unroll
         for (int mm = 0; mm < M; ++mm) {
           const float vm = __shfl(pm[mm], j * f.lpj);
-          v = mm == m ? vm : v;
+          u = mm == m ? vm : u;
         }
         const int k = cc - kT1Words * tq;
 #pragma unroll
         for (int kk = 0; kk < kT1Words; ++kk)
-          if (t1lane && kk == k) part[kk] += v;
-      }
-      float t = 0.0f;
-#pragma unroll
-      for (int k = 0; k < kT1Words; ++k) t += part[k];
-      float tot = t;
-      for (int q = 1; q < LPO; ++q) tot += __shfl(t, to + q * MR);
-      if (tq == 0 && t1lane) {
-        *LDS_AT(lds_f, o_t1 + (uint32_t)to * 4) = tot;
-        if (t1_out && c == 0) t1_out[to] = tot;
+          if (t1lane && kk == k) v[kk] = u;
       }
     }
+    const float t = sum_slices(v);
+    float u[3];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      const int src = to + q * MR;
+      u[q - 1] = __shfl(t, src < 64 ? src : lane);
+    }
+    float tot = t;
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (q < NQ) tot += u[q - 1];
+    if (tq == 0 && t1lane) {
+      *LDS_AT(lds_f, o_t1 + (uint32_t)t1slot * 4) = tot;
+      if (t1_out && c == 0) t1_out[to] = tot;
+    }
   }
-  if (r > 0) lds_barrier();  // B3: T1 is in LDS
+  // T1 is in LDS: the output lanes are wave 0's alone, or a barrier (B3)
+  if (r > 0) {
+    if (R * M * 16 <= 64)
+      wave_lds_fence();
+    else
+      lds_barrier();
+  }
   if (tid < R * M * 16) {
     const int t = tid / (M * 16), m = (tid / 16) % M, rn = tid % 16;
     const int64_t n = n0 + 16 * t + rn;
@@ -647,21 +695,26 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
 #pragma unroll
     for (int wv = 0; wv < kLW; ++wv) sum += pv[wv];
     if (r > 0) {
-      // LoRA dot in chunks of 16 terms whose LDS reads go out together.
-      float l = 0.0f;
-      for (int j0 = 0; j0 < r; j0 += 16) {
-        float ta[16], tb[16];
+      // LoRA dot over the zero-padded rows, 16 terms per step in four chains
+      const uint32_t ta = o_t1 + (uint32_t)(m * r16) * 4;
+      const uint32_t tb = o_lb + (uint32_t)((16 * t + rn) * r16) * 4;
+      float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int j0 = 0; j0 < r16; j0 += 16) {
+        v4u A[4], B[4];
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-          const int j = j0 + jj < r ? j0 + jj : r - 1;
-          ta[jj] = *LDS_AT(const lds_f, o_t1 + (uint32_t)(m * r + j) * 4);
-          tb[jj] = *LDS_AT(const lds_f, o_lb + (uint32_t)((16 * t + rn) * r + j) * 4);
+        for (int i = 0; i < 4; ++i) {
+          A[i] = *LDS_AT(const lds_u4, ta + (uint32_t)(j0 + 4 * i) * 4);
+          B[i] = *LDS_AT(const lds_u4, tb + (uint32_t)(j0 + 4 * i) * 4);
         }
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj)
-          if (j0 + jj < r) l = fmaf(ta[jj], tb[jj], l);
+        for (int i = 0; i < 4; ++i) {
+          l[0] = fmaf(__uint_as_float(A[i].x), __uint_as_float(B[i].x), l[0]);
+          l[1] = fmaf(__uint_as_float(A[i].y), __uint_as_float(B[i].y), l[1]);
+          l[2] = fmaf(__uint_as_float(A[i].z), __uint_as_float(B[i].z), l[2]);
+          l[3] = fmaf(__uint_as_float(A[i].w), __uint_as_float(B[i].w), l[3]);
+        }
       }
-      sum = fmaf(s_lora, l, sum);
+      sum = fmaf(s_lora, (l[0] + l[1]) + (l[2] + l[3]), sum);
     }
     if (n < N) y[(int64_t)m * N + n] = sum;
   }
@@ -671,6 +724,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
 struct StreamPlan {
   int R = 0, KLW = 0, G = 0;
   uint32_t lds = 0;
+  StreamArgs sa{};
   bool ok = false;
 };
 
@@ -702,8 +756,9 @@ bool shape_compiled(int R, int KLW) {
 StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
   StreamPlan p;
   const int cus = cu_count();
-  if (cus <= 0 || M < 1 || M > 2 || r < 0 || r > 64 || M * r > 64) return p;
-  if (w.bs != 64 || w.cols % kLine != 0) return p;
+  const int64_t r16 = (r + 15) & ~(int64_t)15;
+  if (cus <= 0 || M < 1 || M > 2 || r < 0 || r > 64 || M * r16 > 64) return p;
+  if (w.bs != 64 || w.cols % kLine != 0 || w.cols >= (int64_t)1 << 24) return p;
   if ((((uintptr_t)w.codes) & 15) != 0) return p;
   if (w.kind == 0 ? (((uintptr_t)w.scales) & 15) != 0 : (((uintptr_t)w.scale_codes) & 3) != 0)
     return p;
@@ -726,9 +781,16 @@ StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
   // T1 slice partials: the summing wave reads kT1Words * 64 floats at most
   const size_t t1_floats = r > 0 ? (size_t)kT1Words * (64 / (M * r)) * (M * r) + 4 : 0;
   const size_t lds = kTabBytes + (size_t)KL * 16 * 2 * M * 4 * (M == 1 ? 16 : 8) +
-                     (size_t)16 * R * (r > 0 ? r : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
-                     64 * 4 + 16 * 4 + 16 + t1_floats * 4;
+                     (size_t)16 * R * (r > 0 ? r16 : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
+                     64 * 4 + 16 + t1_floats * 4;
   if (lds > kLdsLimit) return p;
+  p.sa.P = (int)P;
+  p.sa.LPO = r > 0 ? (int)(64 / (M * r)) : 1;
+  p.sa.NQ = (int)((P + kT1Words - 1) / kT1Words);
+  p.sa.r16 = (int)r16;
+  p.sa.lps = r > 0 ? 63 - __builtin_clzll((unsigned long long)(64 / r)) : 0;
+  p.sa.inv_r = r > 0 ? 1.0f / (float)r : 1.0f;
+  p.sa.inv_mr = r > 0 ? 1.0f / (float)(M * r) : 1.0f;
   p.R = (int)R;
   p.KLW = (int)KLW;
   p.G = (int)G;
@@ -751,7 +813,7 @@ hipError_t run_stream(const DevQW &w, const void *x, const float *a, int r, cons
     attr = true;
   }
   return qh_launch(k, dim3((unsigned)p.G), dim3(kThreads), p.lds, st, w, x, a, r, lb, s, t1w,
-                   epochs, t1_out, y);
+                   epochs, t1_out, y, p.sa);
 }
 
 template <int XBF16, int KIND, int M>
