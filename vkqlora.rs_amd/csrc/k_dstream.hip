@@ -453,18 +453,19 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     const int tr = div_small(ic, sa.inv_r), j = ic - tr * rr;
     int64_t row = n0 + tr;
     row = row < N ? row : N - 1;
-    lbi[q] = (int)(row * rr + j);
+    lbi[q] = r > 0 ? (int)(row * rr + j) : 0;
     lbo[q] = idx < 16 * R * rr ? tr * r16 + j : -1;
   }
+  // Branch-free, so later waits count these loads exactly; with no adapter
+  // they read valid words that go unused.
+  const float *lbp = r > 0 ? lb : (const float *)t1w;
   auto issue_tail = [&]() {
-    if (r > 0) {
 #pragma unroll
-      for (int q = 0; q < 2 * R; ++q) lbv[q] = lb[lbi[q]];
+    for (int q = 0; q < 2 * R; ++q) lbv[q] = lbp[lbi[q]];
 #pragma unroll
-      for (int q = 0; q < kT1Loads; ++q) {
-        const int i = tid + 512 * q;
-        tpv[q] = ld_dev64(t1w + (i < NMR ? i : NMR - 1));
-      }
+    for (int q = 0; q < kT1Loads; ++q) {
+      const int i = tid + 512 * q;
+      tpv[q] = ld_dev64(t1w + (i < NMR ? i : (NMR > 0 ? NMR - 1 : 0)));
     }
   };
   auto publish = [&]() {
@@ -534,7 +535,8 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       const int kk = i / 8, s = i % 8;
       if (s == 0 && kk + DL < KLW) issue_line(kk + DL);
       // The epilogue's operands go out when the last line starts: the
-      // producers have published by then.
+      // producers have published by then.  (Issued earlier, right behind
+      // the last line's loads, they measured no faster.)
       if (i == (KLW - 1) * 8) issue_tail();
       const int f = i + D;
       if (f < NS) {
@@ -573,6 +575,8 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
           // only D rows < 2M (lane group 0) carry output
 #pragma unroll
           for (int v = 0; v < M2; ++v) acc[t][v] = fmaf(sc, d[t][v], acc[t][v]);
+          // here, not sunk past the loop into the lanes that store it
+          asm volatile("" : "+v"(acc[t]));
         }
       }
       // Keep the steps in order: hoisted early, a later line's regrouping
