@@ -10,11 +10,14 @@
 //  * Workgroup c owns R consecutive 16-row tiles and the whole of K.  Line
 //    wave w owns the K-lines [KL w / 8, KL (w+1) / 8) (a K-line = 256
 //    elements = 128 code bytes per row) of all R tiles, so each X fragment
-//    read from LDS feeds R MFMAs.  Every code line of a wave (R * KLW <= 8)
-//    is requested before the first one is used: the whole weight stream is
-//    in flight from the start, and each line's MFMAs wait for that line only.
-//  * Code loads, the permlane32 regrouping and the packed-row MFMA are those
-//    of the small-batch kernel in k_decode.hip: A-fragment rows m and M+m
+//    read from LDS feeds R MFMAs.  A wave keeps DL = min(KLW, 3) K-lines of
+//    loads in flight: the first one (two when R = 1) goes out before
+//    anything else is computed, the rest once the table is built, and line
+//    kk + DL when line kk's MFMAs start.  Vector-memory data returns in
+//    issue order, so every small load is placed behind the code lines it
+//    must not delay.
+//  * Code loads, the permlane32 regrouping and the packed-row MFMA follow
+//    the small-batch kernel in k_decode.hip: A-fragment rows m and M+m
 //    carry the bf16 hi and lo parts of x_m, the B operand interleaves the
 //    byte-pair table's hi and lo entries, y = D[m] + D[M+m].
 //  * The byte-pair codebook table sits in LDS 32 times, entry e of copy k at
@@ -22,21 +25,21 @@
 //    cycle serves then hit 32 distinct bank pairs whatever the codes are
 //    (a single copy serves random bytes at about 2.5x the cycles).  One
 //    v_perm_b32 forms the address from the code byte and the lane's copy
-//    offset.
-//  * X fragments are stored once per K-line as (P_ab, P_cd) pairs; the read
-//    (ds_read_b64) duplicates them into the (P_ab, P_ab, P_cd, P_cd) A
-//    operand that the interleaved B operand needs.
-//  * Prologue order: every wave issues its small loads (X, the table source,
-//    LoRA B rows, T1 partials, absmax), the workgroup meets at a barrier,
-//    and only then do the code lines go out.  Vector-memory data returns in
-//    order, so a small load issued behind the weight stream waits for it
-//    (about 4 us at full HBM load).
-//  * T1 = X A^T comes from k_t1p (k_decode.hip), launched just before, as
-//    one partial per K-line; every workgroup sums the partials in line
-//    order in LDS, so T1 and y are identical in every workgroup and every
-//    run.  (Summing slices across workgroups inside this kernel costs
-//    several dependent memory round trips, each about 4 us while the weight
-//    stream is in flight.)
+//    offset.  The table is written from immediates at kernel start (no
+//    memory round trip).
+//  * X fragments are written per K-line by the wave that owns it: batch 1
+//    stores the (P_ab, P_ab, P_cd, P_cd) A operand itself (one ds_read_b128
+//    per MFMA pair), batch 2 stores (P_ab, P_cd) and repeats the dwords in
+//    registers.
+//  * T1 = X A^T is computed in the same launch: the first P workgroups each
+//    publish one K slice of it as epoch-tagged words, every workgroup reads
+//    all of them with its last code line and sums them in one fixed order
+//    (the protocol is described above the kernel).  A workgroup whose
+//    slices do not arrive within a bounded number of re-reads computes them
+//    itself with the same instructions, so T1 and y are the same bits in
+//    every workgroup and every run.
+//  * Epilogue: the waves' partial sums are added in LDS in wave order, then
+//    the LoRA dot runs over zero-padded rows of T1 and B in fixed trees.
 // The block scale multiplies each block's MFMA partial once; the double-
 // quant decode c*(absmax/127) is within 1 ulp of quant.rs:218's
 // fl(fl(c/127)*absmax) and only enters this sum, never a stored weight.
@@ -358,7 +361,11 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     for (int t = 0; t < R; ++t) load_line<KIND>(L[kk][t], w, nrow[t], KB, crow[t], kl, g);
   };
   constexpr int DL = KLW < kLinesAhead ? KLW : kLinesAhead;
-  issue_line(0);
+  // K-lines issued before the table is built: two for one tile (8 loads),
+  // one for wider tiles (more loads stall issue behind a full queue).
+  constexpr int DE = R == 1 && DL > 1 ? 2 : 1;
+#pragma unroll
+  for (int kk = 0; kk < DE; ++kk) issue_line(kk);
   __builtin_amdgcn_sched_barrier(0);
   // absmax (first used at line 0's first block scale) and, in wave 0, the
   // launch epoch
@@ -497,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   };
 
 #pragma unroll
-  for (int kk = 1; kk < DL; ++kk) issue_line(kk);
+  for (int kk = DE; kk < DL; ++kk) issue_line(kk);
   __builtin_amdgcn_sched_barrier(0);
   // The slice is published as soon as its operands are in (they follow
   // line 0, which the wave waits for next anyway).
