@@ -207,7 +207,36 @@ def decode_bench(args, ctx, torch, dev, QD):
                        main_kernel_gbs=gemv_bytes / 2 / (main["avg_ms"] * 1e6))
         results[batch] = res
     return results, dict(copies=copies, packed_weight_bytes=wbytes, r=r,
-                         alpha=alpha)
+                         alpha=alpha, host_path=host_path_bench(ctx, torch, layers, r, alpha))
+
+
+def host_path_bench(ctx, torch, layers, r, alpha, reps=5):
+    """The host-slice entry point (qh_qlora_forward, the reference's
+    gpu_qlora_forward signature): host buffers in and out, so every call
+    moves W, X, the adapters and Y over PCIe.  Reported beside the
+    device-resident figure, never as it."""
+    import numpy as np
+    from qlora_hip import api
+    rng = np.random.default_rng(0x5EED)
+    host = []
+    for L in layers:
+        b0 = L["base"]
+        q = dict(rows=b0.rows, cols=b0.cols, block_size=b0.block_size, n=b0.n,
+                 codes=b0.codes.cpu().numpy(), scale_codes=b0.scale_codes.cpu().numpy(),
+                 absmax=b0.absmax.cpu().numpy())
+        host.append((q, L["a"].cpu().numpy().ravel(), L["b"].cpu().numpy().ravel(),
+                     rng.standard_normal(L["K"]).astype(np.float32)))
+    for q, a, b, x in host:  # warm-up (staging buffers)
+        api.forward(q, a, b, r, alpha, x, 1, ctx=ctx)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for q, a, b, x in host:
+            api.forward(q, a, b, r, alpha, x, 1, ctx=ctx)
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    wbytes = sum(L["base"].nbytes for L in layers)
+    return dict(ms_per_step=ms, weight_gbs=wbytes / (ms * 1e6), reps=reps,
+                note="batch 1, both C2 layers through qh_qlora_forward with host "
+                     "buffers: PCIe transfers included")
 
 
 # ---------------------------------------------------------------------------
@@ -403,6 +432,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu_dec,
         "decode_batches": {str(b): {k: v for k, v in r_.items()} for b, r_ in dec.items()},
+        "decode_host_path": dec_cfg["host_path"],
         "prefill": prefill,
     }
     print(json.dumps(line))
