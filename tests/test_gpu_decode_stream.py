@@ -1,4 +1,4 @@
-"""GPU parity of the one-launch decode GEMV (batches of 1 and 2 tokens).
+"""GPU parity of the one-launch decode GEMV (batches of 1 to 16 tokens).
 
 The forward of a batch of 1 or 2 rows with in_dim a multiple of 256 (at
 least 2048) takes k_dstream: one workgroup per CU owning R row tiles and all
@@ -8,8 +8,11 @@ every workgroup.  These tests cover each compiled (tiles per workgroup,
 K-lines per wave) shape class, ragged row counts, bf16 activations, fp32
 block scales, no adapter, the rank limits, the T1 output, and bit-for-bit
 repeatability across calls of two shapes in turn (the epoch counters must
-give every launch new tags).  Every call checks from the context's kernel
-timing that k_dstream ran.
+give every launch new tags).  Batches of 3 to 16 rows take T1 from a
+kernel launched just before and run one launch per 8 rows: their tests
+cover chunking, ragged rows, ranks 0-64, both scale stores and repeatability
+next to batch-1 calls.  Every call checks from the context's kernel timing
+that k_dstream ran.
 """
 import numpy as np
 import pytest
@@ -148,3 +151,96 @@ def test_stream_repeatable(ctx, QD):
             else:
                 assert np.array_equal(got[0], ref[i][0]) and np.array_equal(got[1], ref[i][1])
     _say("repeatable over 4 rounds")
+
+
+# Batches of 3-16 rows: k_lora_t1 computes T1 first, then one launch per 8
+# rows (templates of 4 and 8 rows, the last chunk padded by repeating its
+# last row).  (N, K, M): chunk shapes 4, 8, 8+8, 8+3 over one-tile and
+# three-tile workgroups, ragged rows.
+WIDE = [(4096, 4096, 3), (4096, 4096, 4), (11008, 4096, 5), (4100, 2048, 8),
+        (4096, 11008, 11), (11008, 4096, 16)]
+
+
+@pytest.mark.parametrize("N,K,M", WIDE)
+def test_stream_wide_parity(ctx, QD, N, K, M):
+    r, alpha = 16, 32.0
+    g = O.Rng(SEED ^ (N * 7 + K * 3 + M))
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+    b = g.normal(N * r, 0.01)
+    x = g.normal(M * K)
+    dev = torch.device("cuda:0")
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    wd = O.dequantize(O.quantize(w))
+    lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r, alpha)
+    yo = O.qlora_forward(wd, N, K, a, b, r, alpha, x, M)
+    t1o = O.matmul_trans_b(x, a, M, K, r)
+    for act in (torch.float32, torch.bfloat16):
+        _say(f"stream wide N={N} K={K} M={M} act={act}")
+        xa = bf16_round(x) if act == torch.bfloat16 else x
+        if act == torch.bfloat16:
+            yo_a = O.qlora_forward(wd, N, K, a, b, r, alpha, xa, M)
+            t1o_a = O.matmul_trans_b(xa, a, M, K, r)
+        else:
+            yo_a, t1o_a = yo, t1o
+        y, t1, rep = _forward(QD, ctx, W, lora, torch.from_numpy(xa).to(dev).to(act), M, N, r)
+        assert "decode_stream" in rep and "decode_stream_t1" in rep, rep
+        tol = TOL_F32 if act == torch.float32 else TOL_BF16
+        e = nerr(y.cpu().numpy().ravel(), yo_a, K, xa, wd)
+        et = nerr(t1.cpu().numpy().ravel(), t1o_a, K, xa, a)
+        _say(f"  y {e:.2e} t1 {et:.2e}")
+        assert e < tol and et < tol, (e, et)
+
+
+@pytest.mark.parametrize("M,r", [(4, 0), (6, 1), (8, 5), (12, 64), (16, 8)])
+def test_stream_wide_ranks(ctx, QD, M, r):
+    # no adapter, odd ranks, the largest rank; f32 block scales for one case
+    N, K, alpha = 4096, 4096, 16.0
+    dq = r != 5
+    g = O.Rng(SEED ^ (300 + 11 * r + M))
+    w = g.normal(N * K, 0.02)
+    x = g.normal(M * K)
+    dev = torch.device("cuda:0")
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), double_quant=dq,
+                                 ctx=ctx)
+    wd = O.dequantize(O.quantize(w, 64, dq))
+    if r > 0:
+        a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+        b = g.normal(N * r, 0.01)
+        lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r,
+                              alpha)
+    else:
+        a = b = None
+        lora = None
+    _say(f"stream wide ranks M={M} r={r} dq={dq}")
+    y, t1, rep = _forward(QD, ctx, W, lora, torch.from_numpy(x).to(dev), M, N, r)
+    assert "decode_stream" in rep, rep
+    yo = O.qlora_forward(wd, N, K, a, b, r, alpha, x, M)
+    assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
+    if r > 0:
+        t1o = O.matmul_trans_b(x, a, M, K, r)
+        assert nerr(t1.cpu().numpy().ravel(), t1o, K, x, a) < TOL_F32
+
+
+def test_stream_wide_repeatable(ctx, QD):
+    # batch 16 after batch 1 and back: the chunked launches and the batch-1
+    # launches share the context's counters and T1 words
+    dev = torch.device("cuda:0")
+    N, K, r, alpha = 4096, 4096, 16, 32.0
+    g = O.Rng(SEED ^ 777)
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+    b = g.normal(N * r, 0.01)
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r, alpha)
+    xs = {M: torch.from_numpy(g.normal(M * K)).to(dev) for M in (1, 16)}
+    ref = {}
+    for it in range(3):
+        for M in (1, 16, 1):
+            y, t1, rep = _forward(QD, ctx, W, lora, xs[M], M, N, r)
+            got = (y.cpu().numpy().copy(), t1.cpu().numpy().copy())
+            if M not in ref:
+                ref[M] = got
+            else:
+                assert np.array_equal(got[0], ref[M][0]) and np.array_equal(got[1], ref[M][1])
+    _say("wide repeatable")

@@ -32,9 +32,15 @@ COMMON = [
 ]
 
 
+# Per-file flags: the decode stream kernel's step loop (8 steps per K-line,
+# up to 48 steps) must unroll fully, past the default pragma size limit, so
+# that its per-line register arrays stay in registers.
+EXTRA = {"k_dstream.hip": ["-mllvm", "-pragma-unroll-threshold=100000"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, src + ".o")
-    cmd = [HIPCC, *COMMON]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, [])]
     if src.endswith(".cpp"):
         cmd += ["-x", "hip"]
     cmd += ["-c", os.path.join(CSRC, src), "-o", obj]

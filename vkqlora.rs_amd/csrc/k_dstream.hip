@@ -128,8 +128,8 @@ __device__ __forceinline__ void regroup(const LineRegs &L, uint32_t (&sw)[8]) {
 
 // X fragments are stored with the (P_ab, P_ab, P_cd, P_cd) repetition the
 // interleaved B operand needs (16 bytes, read straight into the A operand)
-// when they fit, i.e. for batch 1; batch 2 stores (P_ab, P_cd) and
-// repeats the dwords in registers.
+// for batch 1; wider batches store (P_ab, P_cd) and repeat the dwords in
+// registers.
 template <int M>
 struct FragOf {
   static constexpr bool kDup = M == 1;
@@ -188,6 +188,8 @@ struct StreamArgs {
   int r16;     // r rounded up to a multiple of 16
   int lps;     // log2 of the lanes per A row in a slice
   float inv_r, inv_mr;  // 1 / r, 1 / (M r) (1 when r = 0)
+  int mact;    // rows of X in this launch (<= M; the rest repeat the last)
+  const float *t1ext;  // batches of 4 and 8: T1 (mact x r), computed before
 };
 
 // floor(v / d) for 0 <= v < 2^22 and d >= 1, with inv = fl(1 / d): (v + 1/2)
@@ -326,7 +328,12 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
                                                       float *__restrict__ t1_out,
                                                       float *__restrict__ y, StreamArgs sa) {
   static_assert(R * KLW <= kMaxLines, "code lines per wave");
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "batch rows");
   constexpr int M2 = 2 * M;
+  // T1 is computed in this launch for batches of 1 and 2 and read from
+  // sa.t1ext for 4 and 8 (their slices would not fit a producer lane)
+  constexpr bool kT1In = M <= 2;
+  constexpr int kT1Floats = kT1In ? 64 : 64 * M;  // T1 in LDS: M r16 <= this
   constexpr uint32_t kFragLine = FragOf<M>::kLine;  // bytes of X fragments per K-line
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar line indices
@@ -356,11 +363,14 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     const int kl = kl0 + (kk < nkl ? kk : nkl - 1);
 #pragma unroll
     for (int m = 0; m < M; ++m)
-      xv[kk][m] = load_x4<XBF16>(x, (int64_t)m * K + (int64_t)kl * kLine + koff);
+      xv[kk][m] = load_x4<XBF16>(x, (int64_t)(m < sa.mact ? m : sa.mact - 1) * K +
+                                        (int64_t)kl * kLine + koff);
 #pragma unroll
     for (int t = 0; t < R; ++t) load_line<KIND>(L[kk][t], w, nrow[t], KB, crow[t], kl, g);
   };
-  constexpr int DL = KLW < kLinesAhead ? KLW : kLinesAhead;
+  // lines in flight: each holds M float4 of X per lane besides its codes
+  constexpr int kAhead = M >= 8 ? 2 : kLinesAhead;
+  constexpr int DL = KLW < kAhead ? KLW : kAhead;
   // K-lines issued before the table is built: two for one tile (8 loads),
   // one for wider tiles (more loads stall issue behind a full queue).
   constexpr int DE = R == 1 && DL > 1 ? 2 : 1;
@@ -378,16 +388,16 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     }
   }
   uint64_t ev = 0;  // the epoch counter word (epoch = ev / 16)
-  if (r > 0 && wave == 0) ev = ld_dev64(epochs + (c & 15));
+  if (kT1In && r > 0 && wave == 0) ev = ld_dev64(epochs + (c & 15));
   __builtin_amdgcn_sched_barrier(0);
 
   const int G = gridDim.x, MR = M * r, P = sa.P, NMR = P * MR, r16 = sa.r16;
   // B rows and T1 have rows of r16 floats, zero past r
-  const uint32_t o_x = kTabBytes;
-  const uint32_t o_lb = o_x + (uint32_t)KL * kFragLine;
+  const uint32_t o_x = kTabBytes;  // one K-line of X fragments per wave
+  const uint32_t o_lb = o_x + (uint32_t)kLW * kFragLine;
   const uint32_t o_red = o_lb + (uint32_t)(16 * R * (r > 0 ? r16 : 1)) * 4;
   const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
-  const uint32_t o_flag = o_t1 + 64 * 4;  // set when a T1 slice never arrived
+  const uint32_t o_flag = o_t1 + kT1Floats * 4;  // set when a T1 slice never arrived
   const uint32_t o_ep = o_flag + 4;       // epoch + 1 (0: not yet known)
   const uint32_t o_tp = o_flag + 16;      // T1 slice partials
 
@@ -429,26 +439,34 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     // zero padding of lbs, t1s and the slice partials
     const v4u z4 = {0u, 0u, 0u, 0u};
     for (int i = tid; i < 4 * R * r16; i += kThreads) *LDS_AT(lds_u4, o_lb + (uint32_t)i * 16) = z4;
-    if (tid < 16) *LDS_AT(lds_u4, o_t1 + (uint32_t)tid * 16) = z4;
-    for (int i = tid; i < MR * PP / 4; i += kThreads) *LDS_AT(lds_u4, o_tp + (uint32_t)i * 16) = z4;
+    if (tid < kT1Floats / 4) *LDS_AT(lds_u4, o_t1 + (uint32_t)tid * 16) = z4;
+    if (kT1In)
+      for (int i = tid; i < MR * PP / 4; i += kThreads)
+        *LDS_AT(lds_u4, o_tp + (uint32_t)i * 16) = z4;
   }
   lds_barrier();  // B1: the table is in LDS
   __builtin_amdgcn_sched_barrier(0);
   // A producer's T1 slice goes out right behind its first code line (the
   // slice is computed when the second line is due).
-  const bool producer = r > 0 && wave == 0 && c < P;
-  T1Slice<XBF16, M, t1_units(R)> t1s;
-  if (producer) t1s.load(x, a, K, r, c, P, sa.lps, lane);
+  const bool producer = kT1In && r > 0 && wave == 0 && c < P;
+  T1Slice<XBF16, kT1In ? M : 1, t1_units(R)> t1s;
+  if (kT1In && producer) t1s.load(x, a, K, r, c, P, sa.lps, lane);
   __builtin_amdgcn_sched_barrier(0);
   // The epilogue's operands: LoRA B rows of the workgroup's tiles (16 R r
   // <= 2 R * 512 floats) and the tagged T1 partials.
   float lbv[2 * R];
   uint64_t tpv[kT1Loads];  // tagged partials tid + 512 q
+  float t1v = 0.0f;        // batches of 4 and 8: T1 element tid (m, j)
+  int t1e = -1;            // its place in LDS (m r16 + j), -1: none
   // T1 element to of this lane, (m, j) = (to / r, to % r), at m r16 + j
   int t1slot = 0;
   if (r > 0) {
     const int m = div_small(to, sa.inv_r);
     t1slot = m * r16 + (to - m * r);
+  }
+  if (!kT1In && r > 0 && tid < M * r) {
+    const int m = div_small(tid, sa.inv_r);
+    t1e = m * r16 + (tid - m * r);
   }
   // element offsets into B (N r < 2^31) and into lbs (-1: none), computed once
   int lbi[2 * R], lbo[2 * R];
@@ -469,13 +487,21 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   auto issue_tail = [&]() {
 #pragma unroll
     for (int q = 0; q < 2 * R; ++q) lbv[q] = lbp[lbi[q]];
+    if (kT1In) {
 #pragma unroll
-    for (int q = 0; q < kT1Loads; ++q) {
-      const int i = tid + 512 * q;
-      tpv[q] = ld_dev64(t1w + (i < NMR ? i : (NMR > 0 ? NMR - 1 : 0)));
+      for (int q = 0; q < kT1Loads; ++q) {
+        const int i = tid + 512 * q;
+        tpv[q] = ld_dev64(t1w + (i < NMR ? i : (NMR > 0 ? NMR - 1 : 0)));
+      }
+    } else {
+      // rows past mact read row mact - 1's (their outputs are not stored)
+      const int mr = sa.mact * (r > 0 ? r : 1);
+      const float *tp = r > 0 ? sa.t1ext : lbp;
+      t1v = tp[tid < mr ? tid : mr - 1];
     }
   };
   auto publish = [&]() {
+    if (!kT1In) return;
     if (r > 0 && wave == 0) {
       // The epoch is in (it came back with line 0): hand it to the other
       // waves, then add this workgroup's share to the counters (after its
@@ -492,12 +518,13 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       }
     }
     if (producer) {
-      float pm[M];
+      constexpr int MT = kT1In ? M : 1;
+      float pm[MT];
       t1s.reduce(pm);
       const int j = lane / t1s.lpj;
       if (t1s.sub == 0 && j < r) {
 #pragma unroll
-        for (int m = 0; m < M; ++m)
+        for (int m = 0; m < MT; ++m)
           st_dev64(t1w + (c * M + m) * r + j, ((ev >> 4) + 1) << 32 | __float_as_uint(pm[m]));
       }
     }
@@ -512,10 +539,10 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- the weight stream ----------------------------------------------
-  // Fragments of the wave's K-line kk (a padded line repeats the last one).
-  auto xfrag = [&](int kk) {
-    return o_x + (uint32_t)(kl0 + (kk < nkl ? kk : nkl - 1)) * kFragLine;
-  };
+  // The wave's fragment slot holds one K-line at a time: line kk's
+  // fragments are written after every read of line kk - 1's (a wave's LDS
+  // operations complete in order).
+  auto xfrag = [&](int) { return o_x + (uint32_t)wave * kFragLine; };
   const uint32_t xunit = (uint32_t)(us * 2 + up) * M2 * 4 * FragOf<M>::kUnit;
   {
     const uint32_t lo8 = (uint32_t)(lane & 31) * 8u;
@@ -527,15 +554,18 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     // of step i + D are requested before step i's MFMAs.  A line's X
     // fragments are written and its code bytes regrouped when its first
     // step is fetched (a wave's LDS operations complete in order).
-    constexpr int D = R == 1 ? 4 : 2;
+    // (the X of wider batches takes the registers of a deeper pipeline)
+    constexpr int D = R == 1 && M <= 2 ? 4 : 2;
     constexpr int NS = KLW * 8;
-    uint32_t sw[2][R][8];
+    // one line's regrouped code dwords: a line's are dead once its last
+    // step is fetched, before the next line's are regrouped
+    uint32_t sw[R][8];
     StepOps<R> ops[D + 1];
     write_frags<XBF16, M>(xv[0], xfrag(0) + xunit, ug);
 #pragma unroll
-    for (int t = 0; t < R; ++t) regroup(L[0][t], sw[0][t]);
+    for (int t = 0; t < R; ++t) regroup(L[0][t], sw[t]);
 #pragma unroll
-    for (int f = 0; f < D; ++f) fetch_step<M, R>(ops[f], sw[0], f, xfrag(0), xo, lo8);
+    for (int f = 0; f < D; ++f) fetch_step<M, R>(ops[f], sw, f, xfrag(0), xo, lo8);
     floatx4 d[R];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
@@ -551,9 +581,9 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
         if (fs == 0) {
           write_frags<XBF16, M>(xv[fk], xfrag(fk) + xunit, ug);
 #pragma unroll
-          for (int t = 0; t < R; ++t) regroup(L[fk][t], sw[fk & 1][t]);
+          for (int t = 0; t < R; ++t) regroup(L[fk][t], sw[t]);
         }
-        fetch_step<M, R>(ops[f % (D + 1)], sw[fk & 1], fs, xfrag(fk), xo, lo8);
+        fetch_step<M, R>(ops[f % (D + 1)], sw, fs, xfrag(fk), xo, lo8);
       }
       if ((s & 1) == 0) {
 #pragma unroll
@@ -579,9 +609,9 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
             sc = (float)(int8_t)((L[kk][t].sf.x >> (8 * j)) & 255u) *
                  (amax * (1.0f / 127.0f) * valid);
           }
-          // only D rows < 2M (lane group 0) carry output
+          // only D rows < 2M carry output
 #pragma unroll
-          for (int v = 0; v < M2; ++v) acc[t][v] = fmaf(sc, d[t][v], acc[t][v]);
+          for (int v = 0; v < (M2 < 4 ? M2 : 4); ++v) acc[t][v] = fmaf(sc, d[t][v], acc[t][v]);
           // here, not sunk past the loop into the lanes that store it
           asm volatile("" : "+v"(acc[t]));
         }
@@ -590,14 +620,31 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       // would wait for that line's bytes.
       __builtin_amdgcn_sched_barrier(0);
     }
-    // Lanes 0..15 hold D rows 0..3 of column nl: y_m = D[m] + D[M+m].
-    if (g == 0) {
+    // Lane (nl, g) holds D rows 4g..4g+3 of column nl: y_m = D[m] + D[M+m].
+    if constexpr (M <= 2) {
+      if (g == 0) {
 #pragma unroll
-      for (int t = 0; t < R; ++t)
+        for (int t = 0; t < R; ++t)
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-          *LDS_AT(lds_f, o_red + (uint32_t)(((wave * R + t) * M + m) * 16 + nl) * 4) =
-              acc[t][m] + acc[t][M + m];
+          for (int m = 0; m < M; ++m)
+            *LDS_AT(lds_f, o_red + (uint32_t)(((wave * R + t) * M + m) * 16 + nl) * 4) =
+                acc[t][m] + acc[t][M + m];
+      }
+    } else {
+      // the lo rows M + 4g + v sit M / 4 lane groups further
+      const int src = lane + 16 * (M / 4);
+#pragma unroll
+      for (int t = 0; t < R; ++t) {
+        float lo[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) lo[v] = __shfl(acc[t][v], src < 64 ? src : lane);
+        if (g < M / 4) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            *LDS_AT(lds_f, o_red + (uint32_t)(((wave * R + t) * M + 4 * g + v) * 16 + nl) * 4) =
+                acc[t][v] + lo[v];
+        }
+      }
     }
   }
   if (r > 0) {
@@ -605,7 +652,8 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     for (int q = 0; q < 2 * R; ++q)
       if (lbo[q] >= 0) *LDS_AT(lds_f, o_lb + (uint32_t)lbo[q] * 4) = lbv[q];
   }
-  if (r > 0) {
+  if (!kT1In && t1e >= 0) *LDS_AT(lds_f, o_t1 + (uint32_t)t1e * 4) = t1v;
+  if (kT1In && r > 0) {
     // Tagged partials: a word whose tag is not this launch's is re-read a
     // bounded number of times; the values go to LDS.
     // this launch's tag, from wave 0 (written right after B1; a wave gets
@@ -627,14 +675,14 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
         }
         stale |= (uint32_t)(v >> 32) != want;
         // stored transposed, [output][slice], so a lane reads a run of slices
-        const int cc = i / MR, o = i - cc * MR;
+        const int cc = div_small(i, sa.inv_mr), o = i - cc * MR;
         *LDS_AT(lds_f, o_tp + (uint32_t)(o * PP + cc) * 4) = __uint_as_float((uint32_t)v);
       }
     }
     if (stale) *LDS_AT(lds_f, o_flag) = 1.0f;
   }
   lds_barrier();  // B2: partial sums, B rows and T1 slice partials are in LDS
-  if (r > 0 && wave == 0) {
+  if constexpr (kT1In) if (r > 0 && wave == 0) {
     // T1[o] = the sum of its P slices: lane (o, q) adds slices [32 q, 32 q +
     // 32) in a fixed tree, then lanes q = 0..NQ-1 of an output add in q order.
     float v[kT1Words];
@@ -689,7 +737,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
     }
   }
   // T1 is in LDS: the output lanes are wave 0's alone, or a barrier (B3)
-  if (r > 0) {
+  if (kT1In && r > 0) {
     if (R * M * 16 <= 64)
       wave_lds_fence();
     else
@@ -727,7 +775,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
       }
       sum = fmaf(s_lora, (l[0] + l[1]) + (l[2] + l[3]), sum);
     }
-    if (n < N) y[(int64_t)m * N + n] = sum;
+    if (n < N && m < sa.mact) y[(int64_t)m * N + n] = sum;
   }
 }
 
@@ -753,22 +801,34 @@ int cu_count() {
   return g_cus[dev];
 }
 
-// (R, KLW) pairs that are compiled.
+// (R, KLW) pairs that are compiled, for batches of 1-2 and of 4-8 rows.
 #define QH_STREAM_SHAPES(F) \
   F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(1, 8) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2) F(4, 1) F(4, 2)
+#define QH_STREAM_SHAPES_WIDE(F) \
+  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(2, 1) F(2, 2) F(3, 1) F(3, 2)
 
-bool shape_compiled(int R, int KLW) {
+bool shape_compiled(int R, int KLW, int Mt) {
 #define QH_SHAPE_EQ(rr, kk) if (R == rr && KLW == kk) return true;
-  QH_STREAM_SHAPES(QH_SHAPE_EQ)
+  if (Mt <= 2) {
+    QH_STREAM_SHAPES(QH_SHAPE_EQ)
+  } else {
+    QH_STREAM_SHAPES_WIDE(QH_SHAPE_EQ)
+  }
 #undef QH_SHAPE_EQ
   return false;
 }
 
-StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
+// Template rows of a launch of mact rows (the wider templates take the
+// rows in chunks of 8, the last one padded).
+int stream_rows(int64_t M, int64_t mact) { return M <= 2 ? (int)M : (mact <= 4 ? 4 : 8); }
+
+// Plan of one launch of mact rows (<= 8) with template rows Mt.
+StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r) {
   StreamPlan p;
   const int cus = cu_count();
   const int64_t r16 = (r + 15) & ~(int64_t)15;
-  if (cus <= 0 || M < 1 || M > 2 || r < 0 || r > 64 || M * r16 > 64) return p;
+  const bool t1in = Mt <= 2;
+  if (cus <= 0 || mact < 1 || mact > Mt || r < 0 || r > 64 || (t1in && Mt * r16 > 64)) return p;
   if (w.bs != 64 || w.cols % kLine != 0 || w.cols >= (int64_t)1 << 24) return p;
   if ((((uintptr_t)w.codes) & 15) != 0) return p;
   if (w.kind == 0 ? (((uintptr_t)w.scales) & 15) != 0 : (((uintptr_t)w.scale_codes) & 3) != 0)
@@ -777,10 +837,11 @@ StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
   if (KL < kLW) return p;
   const int64_t R = (T + cus - 1) / cus;
   const int64_t KLW = (KL + kLW - 1) / kLW;
-  if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW)) return p;
+  if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW, Mt)) return p;
   const int64_t G = (T + R - 1) / R;
-  const int64_t P = t1_slices((int)G, (int)(M * r));
-  if (r > 0) {
+  const int64_t M = Mt;
+  const int64_t P = t1in ? t1_slices((int)G, (int)(M * r)) : 0;
+  if (t1in && r > 0) {
     // T1 slices: every producer lane covers at most kT1Units float4 units.
     const int64_t lpj = (int64_t)1 << (63 - __builtin_clzll(64 / r));
     const int64_t units = (w.cols / 4 + P - 1) / P;
@@ -790,18 +851,21 @@ StreamPlan stream_plan(const DevQW &w, int64_t M, int64_t r) {
       return p;
   }
   // T1 slice partials: the summing wave reads kT1Words * 64 floats at most
-  const size_t t1_floats = r > 0 ? (size_t)kT1Words * (64 / (M * r)) * (M * r) + 4 : 0;
-  const size_t lds = kTabBytes + (size_t)KL * 16 * 2 * M * 4 * (M == 1 ? 16 : 8) +
+  const size_t t1_floats = t1in && r > 0 ? (size_t)kT1Words * (64 / (M * r)) * (M * r) + 4 : 0;
+  const size_t frag_line = (size_t)16 * 2 * M * 4 * (M == 1 ? 16 : 8);
+  const size_t lds = kTabBytes + (size_t)kLW * frag_line +
                      (size_t)16 * R * (r > 0 ? r16 : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
-                     64 * 4 + 16 + t1_floats * 4;
+                     (size_t)(t1in ? 64 : 64 * M) * 4 + 16 + t1_floats * 4;
   if (lds > kLdsLimit) return p;
   p.sa.P = (int)P;
-  p.sa.LPO = r > 0 ? (int)(64 / (M * r)) : 1;
+  p.sa.LPO = t1in && r > 0 ? (int)(64 / (M * r)) : 1;
   p.sa.NQ = (int)((P + kT1Words - 1) / kT1Words);
   p.sa.r16 = (int)r16;
   p.sa.lps = r > 0 ? 63 - __builtin_clzll((unsigned long long)(64 / r)) : 0;
   p.sa.inv_r = r > 0 ? 1.0f / (float)r : 1.0f;
-  p.sa.inv_mr = r > 0 ? 1.0f / (float)(M * r) : 1.0f;
+  p.sa.inv_mr = t1in && r > 0 ? 1.0f / (float)(M * r) : 1.0f;
+  p.sa.mact = mact;
+  p.sa.t1ext = nullptr;
   p.R = (int)R;
   p.KLW = (int)KLW;
   p.G = (int)G;
@@ -834,31 +898,77 @@ hipError_t dispatch_shape(const DevQW &w, const void *x, const float *a, int r, 
 #define QH_SHAPE_CASE(rr, kk) \
   if (p.R == rr && p.KLW == kk) \
     return run_stream<XBF16, KIND, M, rr, kk>(w, x, a, r, lb, s, t1w, epochs, t1_out, y, p, st);
-  QH_STREAM_SHAPES(QH_SHAPE_CASE)
+  if constexpr (M <= 2) {
+    QH_STREAM_SHAPES(QH_SHAPE_CASE)
+  } else {
+    QH_STREAM_SHAPES_WIDE(QH_SHAPE_CASE)
+  }
 #undef QH_SHAPE_CASE
   return hipErrorInvalidValue;
 }
 
+template <int M>
+hipError_t dispatch_rows(int x_bf16, const DevQW &w, const void *x, const float *a, int r,
+                         const float *lb, float s, uint64_t *t1w, uint64_t *epochs,
+                         float *t1_out, float *y, const StreamPlan &p, hipStream_t st) {
+#define QH_ARGS w, x, a, r, lb, s, t1w, epochs, t1_out, y, p, st
+  if (x_bf16) return w.kind == 0 ? dispatch_shape<1, 0, M>(QH_ARGS) : dispatch_shape<1, 1, M>(QH_ARGS);
+  return w.kind == 0 ? dispatch_shape<0, 0, M>(QH_ARGS) : dispatch_shape<0, 1, M>(QH_ARGS);
+#undef QH_ARGS
+}
+
 }  // namespace
 
-bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r) { return stream_plan(w, M, r).ok; }
+bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r) {
+  if (M < 1 || M > kStreamMaxRows) return false;
+  if (M <= 2) return stream_plan(w, (int)M, (int)M, r).ok;
+  // every chunk of 8 rows (the last one possibly narrower) must fit
+  for (int64_t m0 = 0; m0 < M; m0 += 8) {
+    const int mact = (int)std::min<int64_t>(8, M - m0);
+    if (!stream_plan(w, stream_rows(M, mact), mact, r).ok) return false;
+  }
+  return true;
+}
 
-hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M,
+int64_t decode_stream_chunk(int64_t M) { return M <= 2 ? M : 8; }
+
+namespace {
+float *stream_t1(float *t1_out, unsigned *tickets) {
+  return t1_out ? t1_out : (float *)(tickets + kTicketWords + kStreamT1Words);
+}
+}  // namespace
+
+hipError_t launch_decode_stream_t1(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                                   const float *a, int64_t r, float *t1_out, unsigned *tickets,
+                                   hipStream_t st) {
+  if (M <= 2 || r == 0) return hipSuccess;  // batches of 1-2 compute T1 in the GEMV launch
+  return launch_lora_t1(x, x_bf16, M, w.cols, a, r, stream_t1(t1_out, tickets), st);
+}
+
+hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M, int64_t m0,
                                 const float *a, int64_t r, const float *lb, float s, float *y,
                                 float *t1_out, unsigned *tickets, hipStream_t st) {
-  const StreamPlan p = stream_plan(w, M, r);
-  if (!p.ok) return hipErrorInvalidValue;
+  if (!decode_stream_ok(w, M, r) || m0 < 0 || m0 >= M || m0 % decode_stream_chunk(M) != 0)
+    return hipErrorInvalidValue;
   uint64_t *epochs = (uint64_t *)(tickets + kStreamEpochWord);
   uint64_t *t1w = (uint64_t *)(tickets + kTicketWords);
   const int ri = (int)r;
-#define QH_ARGS w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st
-  if (M == 1) {
-    if (x_bf16) return w.kind == 0 ? dispatch_shape<1, 0, 1>(QH_ARGS) : dispatch_shape<1, 1, 1>(QH_ARGS);
-    return w.kind == 0 ? dispatch_shape<0, 0, 1>(QH_ARGS) : dispatch_shape<0, 1, 1>(QH_ARGS);
+  if (M <= 2) {
+    const StreamPlan p = stream_plan(w, (int)M, (int)M, r);
+    if (M == 1) return dispatch_rows<1>(x_bf16, w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st);
+    return dispatch_rows<2>(x_bf16, w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st);
   }
-  if (x_bf16) return w.kind == 0 ? dispatch_shape<1, 0, 2>(QH_ARGS) : dispatch_shape<1, 1, 2>(QH_ARGS);
-  return w.kind == 0 ? dispatch_shape<0, 0, 2>(QH_ARGS) : dispatch_shape<0, 1, 2>(QH_ARGS);
-#undef QH_ARGS
+  // Rows [m0, m0 + 8) of a wider batch, T1 from launch_decode_stream_t1.
+  const int64_t N = w.rows, K = w.cols;
+  const int mact = (int)std::min<int64_t>(8, M - m0);
+  const int Mt = stream_rows(M, mact);
+  StreamPlan p = stream_plan(w, Mt, mact, r);
+  p.sa.t1ext = r > 0 ? stream_t1(t1_out, tickets) + m0 * r : nullptr;
+  const void *xm = x_bf16 ? (const void *)((const uint16_t *)x + m0 * K)
+                          : (const void *)((const float *)x + m0 * K);
+  float *ym = y + m0 * N;
+  if (Mt == 4) return dispatch_rows<4>(x_bf16, w, xm, a, ri, lb, s, t1w, epochs, nullptr, ym, p, st);
+  return dispatch_rows<8>(x_bf16, w, xm, a, ri, lb, s, t1w, epochs, nullptr, ym, p, st);
 }
 
 }  // namespace qh

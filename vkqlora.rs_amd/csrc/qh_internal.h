@@ -130,16 +130,27 @@ hipError_t launch_decode_small(const DevQW &w, const void *x, int x_bf16, int64_
                                const float *lb, int64_t r, float s, float *y, float *t1_out,
                                void *scratch, unsigned *tickets, hipStream_t st);
 // ---- k_dstream.hip ----
-// Decode GEMV for batches of 1 and 2 rows in one launch per layer (at most
-// one workgroup per CU), T1 = X A^T included.  It keeps 16 launch counters
+// Decode GEMV in one launch per layer (at most one workgroup per CU) for
+// batches of 1 and 2 rows, T1 = X A^T included; batches of 3 to 16 rows run
+// k_lora_t1 first, then one launch per 8 rows.  It keeps 16 launch counters
 // (uint64) at tickets[kStreamEpochWord..] and tagged T1 partials in the
-// kStreamT1Words words after the kTicketWords counter words; both must be
-// zero before the first launch, and calls sharing them must be
-// stream-ordered.
+// kStreamT1Words words after the kTicketWords counter words (both zero
+// before the first launch), then kStreamT1ExtWords words for T1 of the wider
+// batches; calls sharing them must be stream-ordered.
 constexpr int kStreamEpochWord = 32;
 constexpr int kStreamT1Words = 128 * 64 * 2;
+constexpr int kStreamT1ExtWords = 16 * 64;
+constexpr int kStreamMaxRows = 16;
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r);
-hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M,
+// Rows per launch (M for batches of 1-2, else 8).
+int64_t decode_stream_chunk(int64_t M);
+// Batches of 3-16 rows: T1 = X A^T into t1_out (or the tickets' T1 words),
+// before the row launches; nothing for 1-2 rows.
+hipError_t launch_decode_stream_t1(const DevQW &w, const void *x, int x_bf16, int64_t M,
+                                   const float *a, int64_t r, float *t1_out, unsigned *tickets,
+                                   hipStream_t st);
+// The launch for rows [m0, m0 + decode_stream_chunk(M)).
+hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M, int64_t m0,
                                 const float *a, int64_t r, const float *lb, float s, float *y,
                                 float *t1_out, unsigned *tickets, hipStream_t st);
 // Tuning knobs of the decode GEMV: codebook table (0 = 16-entry nibble

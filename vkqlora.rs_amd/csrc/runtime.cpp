@@ -390,10 +390,15 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
 
   if (decode && g_decode_path == 0 && qh::decode_stream_ok(W, M, r)) {
     const int xb = xe == qh::E_BF16;
-    timed(ctx, "decode_stream", s, [&] {
-      return qh::launch_decode_stream(W, x, xb, M, lora ? l->a : nullptr, r,
-                                      lora ? l->b : nullptr, sc, y, t1_out, ctx->tickets, s);
-    });
+    if (M > 2 && lora)
+      timed(ctx, "decode_stream_t1", s, [&] {
+        return qh::launch_decode_stream_t1(W, x, xb, M, l->a, r, t1_out, ctx->tickets, s);
+      });
+    for (int64_t m0 = 0; m0 < M; m0 += qh::decode_stream_chunk(M))
+      timed(ctx, "decode_stream", s, [&] {
+        return qh::launch_decode_stream(W, x, xb, M, m0, lora ? l->a : nullptr, r,
+                                        lora ? l->b : nullptr, sc, y, t1_out, ctx->tickets, s);
+      });
     return;
   }
 
@@ -617,9 +622,9 @@ qh_status qh_ctx_create(qh_ctx **out) {
     snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
   if ((e = hipSetDevice(c->device)) != hipSuccess ||
       (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
-      (e = hipMalloc((void **)&c->tickets, (qh::kTicketWords + qh::kStreamT1Words) * 4)) !=
+      (e = hipMalloc((void **)&c->tickets, (qh::kTicketWords + qh::kStreamT1Words + qh::kStreamT1ExtWords) * 4)) !=
           hipSuccess ||
-      (e = hipMemset(c->tickets, 0, (qh::kTicketWords + qh::kStreamT1Words) * 4)) !=
+      (e = hipMemset(c->tickets, 0, (qh::kTicketWords + qh::kStreamT1Words + qh::kStreamT1ExtWords) * 4)) !=
           hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
     if (c->tickets) (void)hipFree(c->tickets);
