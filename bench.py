@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-extra", action="store_true",
+                    help="skip configurations 1, 4, 5 and C3's 14336x4096 layer")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload")
     ap.add_argument("--probe", action="store_true",
@@ -324,6 +326,173 @@ def prefill_bench(args, ctx, torch, dev, QD, act_dtype):
 
 
 # ---------------------------------------------------------------------------
+def _timed_ms(torch, fn, reps):
+    """Mean wall time of fn() on the current stream, between GPU events."""
+    fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _layer(torch, dev, QD, ctx, g, N, K, M, r, alpha, act=None):
+    act = act or torch.float32
+    w = torch.randn(N, K, device=dev, generator=g) * 0.02
+    W = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+    del w
+    a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) / math.sqrt(K)
+    b = torch.randn(N, r, device=dev, generator=g) * 0.01
+    t = dict(N=N, K=K, M=M, r=r, W=W, qw=W.struct(), a=a, b=b,
+             lora=QD.lora_struct(a, b, r, alpha),
+             x=torch.randn(M, K, device=dev, generator=g).to(act),
+             dy=torch.randn(M, N, device=dev, generator=g).to(act),
+             y=torch.empty(M, N, device=dev), t1=torch.empty(M, r, device=dev),
+             gx=torch.empty(M, K, device=dev), ga=torch.empty(r, K, device=dev),
+             gb=torch.empty(N, r, device=dev))
+    return t
+
+
+def _fwd_bwd(QD, ctx, L):
+    QD.forward(None, L["lora"], L["x"], L["M"], L["y"], t1=L["t1"], ctx=ctx, qw=L["qw"])
+    QD.backward(None, L["lora"], L["x"], L["dy"], L["M"], L["gx"], L["ga"], L["gb"],
+                t1=L["t1"], ctx=ctx, qw=L["qw"])
+
+
+def _fwd_bwd_flops(L):
+    M, N, K, r = L["M"], L["N"], L["K"], L["r"]
+    return 4 * M * N * K + 6 * M * r * (K + N)
+
+
+def _adam_step_ms(torch, ctx, tensors, reps=3, max_resident_pages=None):
+    """Device 8-bit Adam step over `tensors` (list of (param, grad) CUDA
+    tensors); the first step creates the state and is not timed."""
+    import ctypes as C
+    import qlora_hip as QH
+    opt = QH.Adam8bit(lr=1e-3, max_resident_pages=max_resident_pages, ctx=ctx)
+    cnt = len(tensors)
+    pp = (C.c_void_p * cnt)(*[p.data_ptr() for p, _ in tensors])
+    gp = (C.c_void_p * cnt)(*[g_.data_ptr() for _, g_ in tensors])
+    ll = (C.c_size_t * cnt)(*[p.numel() for p, _ in tensors])
+    st = QH._lib.AdamStats()
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step():
+        QH._lib.check(ctx.lib.qh_adam8bit_step_dev(opt.h, pp, gp, ll, cnt, C.byref(st), stream))
+    ms = _timed_ms(torch, step, reps)
+    n = sum(p.numel() for p, _ in tensors)
+    blocks = sum(-(-p.numel() // 256) for p, _ in tensors)
+    nbytes = 16 * n + 16 * blocks
+    return dict(ms=ms, elements=n, tensors=cnt, bytes=nbytes, gbs=nbytes / (ms * 1e6),
+                frac_hbm=nbytes / (ms * 1e6) / HBM_PEAK_GBS)
+
+
+def extra_bench(args, ctx, torch, dev, QD):
+    """Configurations 1, 4 and 5 and C3's second layer, each at its own
+    shapes (3, 4 and 2): GPU time per call, rate,
+    fraction of the matching peak."""
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(0x9ABC)
+    # C1: one 576x576 layer, 64 tokens, r=8 (launch-bound)
+    L = _layer(torch, dev, QD, ctx, g, 576, 576, 64, 8, 16.0)
+    ms = _timed_ms(torch, lambda: _fwd_bwd(QD, ctx, L), 20)
+    f = _fwd_bwd_flops(L)
+    out["C1"] = dict(workload="fwd+bwd 576x576 NF4, 64 tokens, r=8", ms=ms, flops=f,
+                     tflops=f / (ms * 1e9), frac_fp32_peak=f / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS,
+                     bound="launch")
+    if not args.no_cpu_baseline:
+        out["C1"]["cpu_baseline"] = cpu_baseline_c1()
+    del L
+    # C3, second layer: 14336x4096, 4096 tokens, r=64, fp32 X
+    L = _layer(torch, dev, QD, ctx, g, 14336, 4096, 4096, 64, 16.0)
+    ms = _timed_ms(torch, lambda: _fwd_bwd(QD, ctx, L), 3)
+    f = _fwd_bwd_flops(L)
+    out["C3_14336x4096"] = dict(workload="fwd+bwd 14336x4096 NF4, 4096 tokens, r=64, fp32 X",
+                                ms=ms, flops=f, tflops=f / (ms * 1e9),
+                                frac_fp32_peak=f / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS)
+    del L
+    torch.cuda.empty_cache()
+    # C4: a SmolLM-135M block's seven projections, 2048 tokens, r=8, then
+    # one Adam step over the 14 adapter tensors (max_resident_pages=4)
+    projs = [(576, 576), (192, 576), (192, 576), (576, 576), (1536, 576), (1536, 576),
+             (576, 1536)]
+    Ls = [_layer(torch, dev, QD, ctx, g, N, K, 2048, 8, 16.0) for N, K in projs]
+
+    def c4_fb():
+        for L in Ls:
+            _fwd_bwd(QD, ctx, L)
+    ms = _timed_ms(torch, c4_fb, 5)
+    f = sum(_fwd_bwd_flops(L) for L in Ls)
+    tens = []
+    for L in Ls:
+        tens += [(L["a"].clone(), L["ga"]), (L["b"].clone(), L["gb"])]
+    ad = _adam_step_ms(torch, ctx, tens, reps=5, max_resident_pages=4)
+    out["C4"] = dict(workload=("fwd+bwd of q/k/v/o/gate/up/down (SmolLM-135M shapes, "
+                               "2048 tokens, r=8), then one 8-bit Adam step over the "
+                               "14 adapter tensors"),
+                     fwd_bwd_ms=ms, flops=f, tflops=f / (ms * 1e9),
+                     frac_fp32_peak=f / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS, adam=ad,
+                     step_ms=ms + ad["ms"])
+    del Ls, tens
+    torch.cuda.empty_cache()
+    # C5: 70B-class layers: quantize throughput (bit-exact path), fwd+bwd
+    # at 2048 tokens, r=64, then Adam over all four adapter tensors
+    c5 = dict(workload=("28672x8192 and 8192x28672: quantize_nf4 from fp32, fwd+bwd at "
+                        "2048 tokens r=64, 8-bit Adam over the 4 adapter tensors"))
+    qs, fbs, tens = [], [], []
+    for N, K in ((28672, 8192), (8192, 28672)):
+        w = torch.randn(N, K, device=dev, generator=g) * 0.02
+        n = N * K
+        qms = _timed_ms(torch, lambda: QD.DeviceWeight.quantize(w, 64, True, ctx=ctx), 3)
+        qb = n * (4 + 0.5 + 1 / 64) + 4 * -(-n // 16384)
+        qs.append(dict(shape=f"{N}x{K}", ms=qms, bytes=qb, gbs=qb / (qms * 1e6),
+                       frac_hbm=qb / (qms * 1e6) / HBM_PEAK_GBS))
+        del w
+        torch.cuda.empty_cache()
+        L = _layer(torch, dev, QD, ctx, g, N, K, 2048, 64, 16.0)
+        ms = _timed_ms(torch, lambda: _fwd_bwd(QD, ctx, L), 3)
+        f = _fwd_bwd_flops(L)
+        fbs.append(dict(shape=f"{N}x{K}", ms=ms, flops=f, tflops=f / (ms * 1e9),
+                        frac_fp32_peak=f / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS))
+        tens += [(L["a"].clone(), L["ga"].clone()), (L["b"].clone(), L["gb"].clone())]
+        del L
+        torch.cuda.empty_cache()
+    c5.update(quantize=qs, fwd_bwd=fbs, adam=_adam_step_ms(torch, ctx, tens, reps=5))
+    out["C5"] = c5
+    return out
+
+
+def cpu_baseline_c1():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    N = K = 576
+    r, alpha, M = 8, 16.0, 64
+    rng = O.Rng(0x1234_5678_9ABC_DEF0 ^ 0)
+    q = O.quantize(rng.normal(N * K, 0.02))
+    a = rng.uniform(r * K, -1 / 24, 1 / 24)
+    b = rng.normal(N * r, 0.01)
+    x = rng.normal(M * K)
+    dy = rng.normal(M * N)
+    t0, steps = time.perf_counter(), 0
+    while True:
+        wd = O.dequantize(q)
+        O.qlora_forward(wd, N, K, a, b, r, alpha, x, M)
+        wd = O.dequantize(q)  # qlora.rs:133: the backward dequantizes again
+        O.qlora_backward(wd, N, K, a, b, r, alpha, x, dy, M)
+        steps += 1
+        if time.perf_counter() - t0 > 2.0 or steps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / steps
+    flops = 4 * M * N * K + 6 * M * r * (K + N)
+    return dict(value=flops / (dt * 1e12), unit="TFLOP/s", ms=dt * 1e3, cores=1, kind="port",
+                sample=f"{steps} full fwd+bwd calls (single thread), {dt * 1e3:.1f} ms each",
+                nproc=os.cpu_count())
+
+
 def cpu_baseline_decode(seconds):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
@@ -417,6 +586,10 @@ def main():
             prefill[p["act_dtype"]] = p
             print(f"# prefill {p['act_dtype']}: {p['tflops']:.1f} TFLOP/s",
                   file=sys.stderr, flush=True)
+    extra = {}
+    if not args.skip_extra:
+        extra = extra_bench(args, ctx, torch, dev, QD)
+        print(f"# extra configs done: {sorted(extra)}", file=sys.stderr, flush=True)
     cpu_dec = cpu_pre = None
     if not args.no_cpu_baseline:
         cpu_dec = cpu_baseline_decode(args.cpu_seconds)
@@ -464,6 +637,7 @@ def main():
         "decode_batches": {str(b): {k: v for k, v in r_.items()} for b, r_ in dec.items()},
         "decode_host_path": dec_cfg["host_path"],
         "prefill": prefill,
+        "configs": extra,
     }
     print(json.dumps(line))
 
