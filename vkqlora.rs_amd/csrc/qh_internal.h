@@ -157,6 +157,9 @@ hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64
 // table, 1 = 256-entry byte-pair table) and the workgroup count the K split
 // aims for.
 void set_decode_table(int t);
+// Tuning knob of the tile engine: 128x128 tiles when the output holds at
+// least this many of them (else 64x64).
+void set_gemm_t128_min(int t);
 void set_decode_split_target(int t);
 
 // ---- k_elem.hip ----

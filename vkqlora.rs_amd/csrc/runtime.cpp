@@ -617,6 +617,7 @@ qh_status qh_ctx_create(qh_ctx **out) {
   if (const char *t = getenv("QH_DECODE_TABLE")) qh::set_decode_table(atoi(t));
   if (const char *t = getenv("QH_DECODE_SPLIT_TARGET")) qh::set_decode_split_target(atoi(t));
   if (const char *t = getenv("QH_DECODE_PATH")) g_decode_path = atoi(t);
+  if (const char *t = getenv("QH_GEMM_T128_MIN")) qh::set_gemm_t128_min(atoi(t));
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, c->device) == hipSuccess)
     snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
