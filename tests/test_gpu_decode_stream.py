@@ -11,7 +11,9 @@ repeatability across calls of two shapes in turn (the epoch counters must
 give every launch new tags).  Batches of 3 to 16 rows take T1 from a
 kernel launched just before and run one launch per 8 rows: their tests
 cover chunking, ragged rows, ranks 0-64, both scale stores and repeatability
-next to batch-1 calls.  Every call checks from the context's kernel timing
+next to batch-1 calls.  The path a workgroup takes when published T1
+slices never arrive (it recomputes them) is forced from the host and must
+give the same bits.  Every call checks from the context's kernel timing
 that k_dstream ran.
 """
 import numpy as np
@@ -244,3 +246,35 @@ def test_stream_wide_repeatable(ctx, QD):
             else:
                 assert np.array_equal(got[0], ref[M][0]) and np.array_equal(got[1], ref[M][1])
     _say("wide repeatable")
+
+
+@pytest.mark.parametrize("N,K,M,r", [(11008, 4096, 1, 16), (4096, 11008, 1, 16),
+                                     (4096, 4096, 2, 8), (4096, 4096, 1, 5)])
+def test_stream_t1_fallback_same_bits(ctx, QD, N, K, M, r):
+    # A workgroup whose published T1 slices never arrive computes every
+    # slice itself with the producers' instructions and sums them in the
+    # same order: forced from the host, y and T1 must equal the normal
+    # path's bit for bit.
+    import os
+    g = O.Rng(SEED ^ (500 + N + K + M + r))
+    dev = torch.device("cuda:0")
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+    b = g.normal(N * r, 0.01)
+    x = torch.from_numpy(g.normal(M * K)).to(dev)
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r, 16.0)
+    _say(f"t1 fallback N={N} K={K} M={M} r={r}")
+    y0, t10, rep = _forward(QD, ctx, W, lora, x, M, N, r)
+    assert "decode_stream" in rep, rep
+    os.environ["QH_STREAM_T1_FALLBACK"] = "1"
+    try:
+        y1, t11, rep = _forward(QD, ctx, W, lora, x, M, N, r)
+    finally:
+        del os.environ["QH_STREAM_T1_FALLBACK"]
+    assert "decode_stream" in rep, rep
+    assert np.array_equal(y0.cpu().numpy(), y1.cpu().numpy())
+    assert np.array_equal(t10.cpu().numpy(), t11.cpu().numpy())
+    wd = O.dequantize(O.quantize(w))
+    yo = O.qlora_forward(wd, N, K, a, b, r, 16.0, x.cpu().numpy().ravel(), M)
+    assert nerr(y1.cpu().numpy().ravel(), yo, K, x.cpu().numpy().ravel(), wd) < TOL_F32
