@@ -34,8 +34,10 @@ COMMON = [
 
 # Per-file flags: the decode stream kernel's step loop (8 steps per K-line,
 # up to 48 steps) must unroll fully, past the default pragma size limit, so
-# that its per-line register arrays stay in registers.
-EXTRA = {"k_dstream.hip": ["-mllvm", "-pragma-unroll-threshold=100000"]}
+# that its per-line register arrays stay in registers; its leading scalar
+# arguments are preloaded into SGPRs.
+EXTRA = {"k_dstream.hip": ["-mllvm", "-pragma-unroll-threshold=100000",
+                           "-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def _compile(src: str) -> str:

@@ -320,9 +320,16 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 // K-line) | lbs (16 R r16 floats) | red (kLW R 16 M floats) | t1s (64
 // floats, M r16 used) | flag, epoch | T1 slice partials (M r x 32 LPO
 // floats, zero past slice P).
+// The weight's pointers, X and the shape lead the arguments: the first 16
+// argument dwords arrive preloaded in SGPRs (no kernel-argument load before
+// the first code line goes out).
 template <int XBF16, int KIND, int M, int R, int KLW>
-__global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__restrict__ x,
-                                                      const float *__restrict__ a, int r,
+__global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict__ codes,
+                                                      const void *__restrict__ scales,
+                                                      const float *__restrict__ absmax,
+                                                      const void *__restrict__ x, int64_t N,
+                                                      int64_t K, const float *__restrict__ a,
+                                                      int r,
                                                       const float *__restrict__ lb,
                                                       float s_lora, uint64_t *__restrict__ t1w,
                                                       uint64_t *__restrict__ epochs,
@@ -338,7 +345,14 @@ __global__ __launch_bounds__(kThreads) void k_dstream(DevQW w, const void *__res
   constexpr uint32_t kFragLine = FragOf<M>::kLine;  // bytes of X fragments per K-line
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar line indices
-  const int64_t N = w.rows, K = w.cols, KB = K >> 6;
+  DevQW w{};  // the view load_line reads
+  w.rows = N;
+  w.cols = K;
+  w.codes = codes;
+  w.scales = (const float *)scales;
+  w.scale_codes = (const uint8_t *)scales;
+  w.absmax = absmax;
+  const int64_t KB = K >> 6;
   const int KL = (int)(K / kLine), c = blockIdx.x;
   const int64_t n0 = (int64_t)c * R * 16;
   const int kl0 = KL * wave / kLW, nkl = KL * (wave + 1) / kLW - kl0;
@@ -893,8 +907,9 @@ hipError_t run_stream(const DevQW &w, const void *x, const float *a, int r, cons
     if (e != hipSuccess) return e;
     attr = true;
   }
-  return qh_launch(k, dim3((unsigned)p.G), dim3(kThreads), p.lds, st, w, x, a, r, lb, s, t1w,
-                   epochs, t1_out, y, p.sa);
+  const void *sc = KIND == 0 ? (const void *)w.scales : (const void *)w.scale_codes;
+  return qh_launch(k, dim3((unsigned)p.G), dim3(kThreads), p.lds, st, w.codes, sc, w.absmax, x,
+                   w.rows, w.cols, a, r, lb, s, t1w, epochs, t1_out, y, p.sa);
 }
 
 template <int XBF16, int KIND, int M>
