@@ -55,7 +55,6 @@ constexpr int kThreads = kLW * 64;
 constexpr int kCopies = 32;               // codebook table copies
 constexpr uint32_t kTabBytes = 256u * kCopies * 8u;  // 64 KiB at LDS offset 0
 constexpr int kMaxLines = 8;   // code lines a wave holds in registers
-constexpr int kT1Words = 32;  // slices per lane of the summing wave
 constexpr int kT1Loads = 4;   // tagged T1 partials read per thread (P * M * r <= 2048)
 constexpr int kLinesAhead = 3; // K-lines of loads a wave keeps in flight
 constexpr int kMaxSlices = 128;  // T1 slices (producing workgroups)
@@ -74,19 +73,6 @@ typedef __attribute__((address_space(3))) float lds_f;
 // LDS is addressed by byte offset: the kernel declares no __shared__ object,
 // so dynamic LDS starts at 0 and the table needs no base register.
 #define LDS_AT(T, off) ((T *)(uintptr_t)(off))
-
-// Sum of a lane's kT1Words slice partials in a fixed tree order (the
-// padding past the last slice is zero, so it adds exactly nothing).
-__device__ __forceinline__ float sum_slices(const float (&v)[kT1Words]) {
-  float h[kT1Words / 2];
-#pragma unroll
-  for (int k = 0; k < kT1Words / 2; ++k) h[k] = v[2 * k] + v[2 * k + 1];
-#pragma unroll
-  for (int w = kT1Words / 4; w >= 1; w /= 2)
-#pragma unroll
-    for (int k = 0; k < w; ++k) h[k] = h[2 * k] + h[2 * k + 1];
-  return h[0];
-}
 
 // LDS visibility between lanes of one wave (its LDS operations complete in
 // order; this keeps the compiler from moving them across).
@@ -183,11 +169,10 @@ __device__ __forceinline__ void mfma_step(const StepOps<R> &o, floatx4 (&d)[R]) 
 // Launch constants of the T1 epilogue, computed on the host.
 struct StreamArgs {
   int P;       // T1 slices (producing workgroups)
-  int LPO;     // lanes per T1 output in the summing wave: 64 / (M r)
-  int NQ;      // of those, lanes that hold slices: ceil(P / kT1Words) <= 4
+  int mrl;     // log2 of MRp, the power of two >= M r (<= 64)
   int r16;     // r rounded up to a multiple of 16
   int lps;     // log2 of the lanes per A row in a slice
-  float inv_r, inv_mr;  // 1 / r, 1 / (M r) (1 when r = 0)
+  float inv_r;  // 1 / r (1 when r = 0)
   int mact;    // rows of X in this launch (<= M; the rest repeat the last)
   const float *t1ext;  // batches of 4 and 8: T1 (mact x r), computed before
   int t1_fallback;     // set by tests: every workgroup computes all T1 slices
@@ -200,15 +185,15 @@ __device__ __forceinline__ int div_small(int v, float inv) {
   return (int)(((float)v + 0.5f) * inv);
 }
 
-// Number of T1 slices (producing workgroups) of a launch of G workgroups:
-// one wave sums the P * M * r tagged partials, lane (o, q) for output
-// o = l % MR and q = l / MR < 64 / MR taking slices [32 q, 32 q + 32).
-__host__ __device__ constexpr int t1_slices(int G, int MR) {
-  return MR <= 0 || MR > 64
+// Number of T1 slices (producing workgroups) of a launch of G workgroups
+// for MRp (the power of two >= M r): thread t reads the tagged partials of
+// output t % MRp for slices t / MRp + (kThreads / MRp) q, q < kT1Loads.
+__host__ __device__ constexpr int t1_slices(int G, int MRp) {
+  return MRp <= 0 || MRp > 64
              ? 1
-             : (G < kMaxSlices ? G : kMaxSlices) < kT1Loads * kThreads / MR
+             : (G < kMaxSlices ? G : kMaxSlices) < kT1Loads * kThreads / MRp
                    ? (G < kMaxSlices ? G : kMaxSlices)
-                   : kT1Loads * kThreads / MR;
+                   : kT1Loads * kThreads / MRp;
 }
 
 // T1 slice c of P: float4 units [U c / P, U (c+1) / P) of K.  Lane l covers
@@ -306,8 +291,9 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 // T1 = X A^T in P slices (t1_slices): wave 0 of workgroup c < P computes
 // slice c near the start and stores it as (tag, value) words, tag =
 // epoch + 1, with no wait; every workgroup reads all P x M x r words with
-// its last code lines (a few per thread), re-reads a word whose tag is
-// stale, and wave 0 sums the slices in order.
+// its last code lines (at most kT1Loads per thread, all of one output),
+// re-reads a word whose tag is stale, and sums them in one fixed order
+// (per thread, then across the lanes of an output, then across waves).
 // The epoch numbers launches: 16 counters (epochs[s]), each advanced by
 // exactly 16 per launch (+1 by every workgroup c with c % 16 == s, the rest
 // by workgroup s % G, each right after its own read of its counter), so
@@ -318,8 +304,8 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 // current).
 // Dynamic LDS (byte offsets): [0, 64K) table | X fragments (KL M KiB, by
 // K-line) | lbs (16 R r16 floats) | red (kLW R 16 M floats) | t1s (64
-// floats, M r16 used) | flag, epoch | T1 slice partials (M r x 32 LPO
-// floats, zero past slice P).
+// floats, M r16 used) | flag, epoch | recomputed T1 slices (P MRp floats) |
+// per-wave T1 partial sums (kLW MRp floats).
 // The weight's pointers, X and the shape lead the arguments: the first 16
 // argument dwords arrive preloaded in SGPRs (no kernel-argument load before
 // the first code line goes out).
@@ -406,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   if (kT1In && r > 0 && wave == 0) ev = ld_dev64(epochs + (c & 15));
   __builtin_amdgcn_sched_barrier(0);
 
-  const int G = gridDim.x, MR = M * r, P = sa.P, NMR = P * MR, r16 = sa.r16;
+  const int G = gridDim.x, MR = M * r, P = sa.P, r16 = sa.r16;
   // B rows and T1 have rows of r16 floats, zero past r
   const uint32_t o_x = kTabBytes;  // one K-line of X fragments per wave
   const uint32_t o_lb = o_x + (uint32_t)kLW * kFragLine;
@@ -414,7 +400,9 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
   const uint32_t o_flag = o_t1 + kT1Floats * 4;  // set when a T1 slice never arrived
   const uint32_t o_ep = o_flag + 4;       // epoch + 1 (0: not yet known)
-  const uint32_t o_tp = o_flag + 16;      // T1 slice partials
+  const uint32_t o_tp = o_flag + 16;      // recomputed T1 slices [cc][o]
+  const int mrl = sa.mrl, MRp = 1 << mrl;
+  const uint32_t o_wp = o_tp + (uint32_t)(P * MRp) * 4;  // per-wave T1 partials
 
   // ---- the codebook table, from constants: no memory round trip --------
   // Built before most loads are issued: a wave issuing more loads than the
@@ -440,12 +428,9 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
       *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
     }
   }
-  // Wave 0 produces slice c (c < P) and sums all slices.
-  const int LPO = sa.LPO;                 // lanes per T1 output
-  const int PP = kT1Words * LPO;          // slice stride of the partials
-  const int NQ = sa.NQ;                   // lanes per output with slices (<= 4)
-  const int tq = div_small(lane, sa.inv_mr), to = lane - tq * (MR > 0 ? MR : 1);
-  const bool t1lane = tq < LPO;           // lanes past LPO*MR idle
+  // Wave 0 of workgroup c < P produces slice c.  Thread t reads the tagged
+  // partials of output so = t % MRp, slices sslot + (kThreads / MRp) q.
+  const int so = tid & (MRp - 1), sslot = tid >> mrl;
   if (tid == 0) {
     *LDS_AT(lds_f, o_flag) = 0.0f;
     *LDS_AT(lds_f, o_ep) = 0.0f;
@@ -455,9 +440,6 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
     const v4u z4 = {0u, 0u, 0u, 0u};
     for (int i = tid; i < 4 * R * r16; i += kThreads) *LDS_AT(lds_u4, o_lb + (uint32_t)i * 16) = z4;
     if (tid < kT1Floats / 4) *LDS_AT(lds_u4, o_t1 + (uint32_t)tid * 16) = z4;
-    if (kT1In)
-      for (int i = tid; i < MR * PP / 4; i += kThreads)
-        *LDS_AT(lds_u4, o_tp + (uint32_t)i * 16) = z4;
   }
   lds_barrier();  // B1: the table is in LDS
   __builtin_amdgcn_sched_barrier(0);
@@ -470,14 +452,20 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   // The epilogue's operands: LoRA B rows of the workgroup's tiles (16 R r
   // <= 2 R * 512 floats) and the tagged T1 partials.
   float lbv[2 * R];
-  uint64_t tpv[kT1Loads];  // tagged partials tid + 512 q
+  uint64_t tpv[kT1Loads];  // tagged partials (slice sslot + (kThreads / MRp) q, output so)
+  int tpi[kT1Loads];       // their word indices (cc MR + so), -1: none
+#pragma unroll
+  for (int q = 0; q < kT1Loads; ++q) {
+    const int cc = sslot + (kThreads >> mrl) * q;
+    tpi[q] = so < MR && cc < P ? cc * MR + so : -1;
+  }
   float t1v = 0.0f;        // batches of 4 and 8: T1 element tid (m, j)
   int t1e = -1;            // its place in LDS (m r16 + j), -1: none
-  // T1 element to of this lane, (m, j) = (to / r, to % r), at m r16 + j
+  // T1 element o = lane of wave 0, (m, j) = (o / r, o % r), at m r16 + j
   int t1slot = 0;
   if (r > 0) {
-    const int m = div_small(to, sa.inv_r);
-    t1slot = m * r16 + (to - m * r);
+    const int m = div_small(lane, sa.inv_r);
+    t1slot = m * r16 + (lane - m * r);
   }
   if (!kT1In && r > 0 && tid < M * r) {
     const int m = div_small(tid, sa.inv_r);
@@ -504,10 +492,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
     for (int q = 0; q < 2 * R; ++q) lbv[q] = lbp[lbi[q]];
     if (kT1In) {
 #pragma unroll
-      for (int q = 0; q < kT1Loads; ++q) {
-        const int i = tid + 512 * q;
-        tpv[q] = ld_dev64(t1w + (i < NMR ? i : (NMR > 0 ? NMR - 1 : 0)));
-      }
+      for (int q = 0; q < kT1Loads; ++q) tpv[q] = ld_dev64(t1w + (tpi[q] >= 0 ? tpi[q] : 0));
     } else {
       // rows past mact read row mact - 1's (their outputs are not stored)
       const int mr = sa.mact * (r > 0 ? r : 1);
@@ -552,6 +537,18 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   // line 0, which the wave waits for next anyway).
   publish();
   __builtin_amdgcn_sched_barrier(0);
+
+  // T1's fixed summation order, shared by the published and the recomputed
+  // slices: a thread adds its slices in q order, the lanes of one output
+  // add by xor butterfly (bits log2 MRp .. 5), and after the barrier wave 0
+  // adds the 8 wave partials in a fixed tree.
+  auto t1_reduce = [&](const float (&v)[kT1Loads]) {
+    float p = v[0];
+#pragma unroll
+    for (int q = 1; q < kT1Loads; ++q) p += v[q];
+    for (int off = 32; off >= MRp; off >>= 1) p += __shfl_xor(p, off);
+    if (lane < MRp) *LDS_AT(lds_f, o_wp + (uint32_t)(wave * MRp + lane) * 4) = p;
+  };
 
   // ---- the weight stream ----------------------------------------------
   // The wave's fragment slot holds one K-line at a time: line kk's
@@ -680,76 +677,60 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
     }
     bool stale = want == 0 || sa.t1_fallback != 0;
     const int polls = sa.t1_fallback ? 0 : kTagPolls;
+    float tv[kT1Loads];
 #pragma unroll
     for (int q = 0; q < kT1Loads; ++q) {
-      const int i = tid + 512 * q;
-      if (i < NMR) {
+      tv[q] = 0.0f;
+      if (tpi[q] >= 0) {
         uint64_t v = tpv[q];
         for (int it = 0; it < polls && (uint32_t)(v >> 32) != want; ++it) {
           __builtin_amdgcn_s_sleep(4);
-          v = ld_dev64(t1w + i);
+          v = ld_dev64(t1w + tpi[q]);
         }
         stale |= (uint32_t)(v >> 32) != want;
-        // stored transposed, [output][slice], so a lane reads a run of slices
-        const int cc = div_small(i, sa.inv_mr), o = i - cc * MR;
-        *LDS_AT(lds_f, o_tp + (uint32_t)(o * PP + cc) * 4) = __uint_as_float((uint32_t)v);
+        tv[q] = __uint_as_float((uint32_t)v);
       }
     }
+    t1_reduce(tv);
     if (stale) *LDS_AT(lds_f, o_flag) = 1.0f;
   }
   lds_barrier();  // B2: partial sums, B rows and T1 slice partials are in LDS
-  if constexpr (kT1In) if (r > 0 && wave == 0) {
-    // T1[o] = the sum of its P slices: lane (o, q) adds slices [32 q, 32 q +
-    // 32) in a fixed tree, then lanes q = 0..NQ-1 of an output add in q order.
-    float v[kT1Words];
-    if (*LDS_AT(const lds_f, o_flag) == 0.0f) {
-      const uint32_t a0 = o_tp + (uint32_t)(to * PP + kT1Words * (t1lane ? tq : 0)) * 4;
-#pragma unroll
-      for (int k = 0; k < kT1Words; k += 4) {
-        const v4u q4 = *LDS_AT(const lds_u4, a0 + (uint32_t)k * 4);
-        v[k] = __uint_as_float(q4.x);
-        v[k + 1] = __uint_as_float(q4.y);
-        v[k + 2] = __uint_as_float(q4.z);
-        v[k + 3] = __uint_as_float(q4.w);
-      }
-    } else {
+  if constexpr (kT1In) if (r > 0) {
+    if (*LDS_AT(const lds_f, o_flag) != 0.0f) {
       // Some slice never arrived (its workgroup not resident): wave 0
-      // computes every slice with the producers' code, into the same places.
+      // computes every slice with the producers' instructions, then every
+      // thread sums its slices again in the same order.
+      if (wave == 0) {
+        for (int cc = 0; cc < P; ++cc) {
+          T1Slice<XBF16, M, t1_units(R)> f;
+          f.load(x, a, K, r, cc, P, sa.lps, lane);
+          float pm[M];
+          f.reduce(pm);
+          const int j = lane / f.lpj;
+          if (f.sub == 0 && j < r) {
 #pragma unroll
-      for (int k = 0; k < kT1Words; ++k) v[k] = 0.0f;
-      for (int cc = 0; cc < P; ++cc) {
-        T1Slice<XBF16, M, t1_units(R)> f;
-        f.load(x, a, K, r, cc, P, sa.lps, lane);
-        float pm[M];
-        f.reduce(pm);
-        // the slice's (m, j) value sits in lane j * lpj: hand it to lane (o, q)
-        const int m = div_small(to, sa.inv_r), j = to - m * r;
-        float u = 0.0f;
-#pragma unroll
-        for (int mm = 0; mm < M; ++mm) {
-          const float vm = __shfl(pm[mm], j * f.lpj);
-          u = mm == m ? vm : u;
+            for (int m = 0; m < M; ++m)
+              *LDS_AT(lds_f, o_tp + (uint32_t)(cc * MRp + m * r + j) * 4) = pm[m];
+          }
         }
-        const int k = cc - kT1Words * tq;
-#pragma unroll
-        for (int kk = 0; kk < kT1Words; ++kk)
-          if (t1lane && kk == k) v[kk] = u;
       }
-    }
-    const float t = sum_slices(v);
-    float u[3];
+      lds_barrier();
+      float tv[kT1Loads];
 #pragma unroll
-    for (int q = 1; q < 4; ++q) {
-      const int src = to + q * MR;
-      u[q - 1] = __shfl(t, src < 64 ? src : lane);
+      for (int q = 0; q < kT1Loads; ++q) {
+        const int cc = sslot + (kThreads >> mrl) * q;
+        tv[q] = tpi[q] >= 0 ? *LDS_AT(const lds_f, o_tp + (uint32_t)(cc * MRp + so) * 4) : 0.0f;
+      }
+      t1_reduce(tv);
+      lds_barrier();
     }
-    float tot = t;
+    if (wave == 0 && lane < MR) {
+      float wv[kLW];
 #pragma unroll
-    for (int q = 1; q < 4; ++q)
-      if (q < NQ) tot += u[q - 1];
-    if (tq == 0 && t1lane) {
+      for (int w8 = 0; w8 < kLW; ++w8) wv[w8] = *LDS_AT(const lds_f, o_wp + (uint32_t)(w8 * MRp + lane) * 4);
+      const float tot = ((wv[0] + wv[1]) + (wv[2] + wv[3])) + ((wv[4] + wv[5]) + (wv[6] + wv[7]));
       *LDS_AT(lds_f, o_t1 + (uint32_t)t1slot * 4) = tot;
-      if (t1_out && c == 0) t1_out[to] = tot;
+      if (t1_out && c == 0) t1_out[lane] = tot;
     }
   }
   // T1 is in LDS: the output lanes are wave 0's alone, or a barrier (B3)
@@ -856,30 +837,28 @@ StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r) {
   if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW, Mt)) return p;
   const int64_t G = (T + R - 1) / R;
   const int64_t M = Mt;
-  const int64_t P = t1in ? t1_slices((int)G, (int)(M * r)) : 0;
+  int64_t MRp = 1;
+  while (MRp < M * r) MRp *= 2;
+  const int64_t P = t1in ? t1_slices((int)G, (int)MRp) : 0;
   if (t1in && r > 0) {
     // T1 slices: every producer lane covers at most kT1Units float4 units.
     const int64_t lpj = (int64_t)1 << (63 - __builtin_clzll(64 / r));
     const int64_t units = (w.cols / 4 + P - 1) / P;
     if (w.cols / 4 < P || (units + lpj - 1) / lpj > t1_units((int)R)) return p;
-    if ((P + 64 / (M * r) - 1) / (64 / (M * r)) > kT1Words ||
-        P * M * r > (int64_t)kT1Loads * kThreads || P * M * r * 4 > (int64_t)kTabBytes)
-      return p;
+    if (MRp > 64 || P * MRp > (int64_t)kT1Loads * kThreads) return p;
   }
-  // T1 slice partials: the summing wave reads kT1Words * 64 floats at most
-  const size_t t1_floats = t1in && r > 0 ? (size_t)kT1Words * (64 / (M * r)) * (M * r) + 4 : 0;
+  // recomputed slices (P MRp floats) and per-wave partials (kLW MRp floats)
+  const size_t t1_floats = t1in && r > 0 ? (size_t)(P + kLW) * MRp : 0;
   const size_t frag_line = (size_t)16 * 2 * M * 4 * (M == 1 ? 16 : 8);
   const size_t lds = kTabBytes + (size_t)kLW * frag_line +
                      (size_t)16 * R * (r > 0 ? r16 : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
                      (size_t)(t1in ? 64 : 64 * M) * 4 + 16 + t1_floats * 4;
   if (lds > kLdsLimit) return p;
   p.sa.P = (int)P;
-  p.sa.LPO = t1in && r > 0 ? (int)(64 / (M * r)) : 1;
-  p.sa.NQ = (int)((P + kT1Words - 1) / kT1Words);
+  p.sa.mrl = 63 - __builtin_clzll((unsigned long long)MRp);
   p.sa.r16 = (int)r16;
   p.sa.lps = r > 0 ? 63 - __builtin_clzll((unsigned long long)(64 / r)) : 0;
   p.sa.inv_r = r > 0 ? 1.0f / (float)r : 1.0f;
-  p.sa.inv_mr = t1in && r > 0 ? 1.0f / (float)(M * r) : 1.0f;
   p.sa.mact = mact;
   p.sa.t1ext = nullptr;
   // Tests force the path a workgroup takes when published T1 slices never
