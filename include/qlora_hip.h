@@ -203,7 +203,9 @@ QH_API qh_status qh_adam8bit_get_state(qh_adam8bit *opt, size_t idx,
                                        uint64_t *step);
 
 /* ---- device-resident hot path (async on `stream`) ----------------------- */
-/* All pointers are device pointers; `w` describes device buffers. */
+/* All pointers are device pointers; `w` describes device buffers.  Calls on
+ * one context share its scratch, launch counters and T1 exchange words: keep
+ * them ordered on one stream (or use one context per stream). */
 QH_API qh_status qh_quantize_nf4_dev(qh_ctx *ctx, const float *d_w,
                                      size_t rows, size_t cols,
                                      size_t block_size, int double_quant,
