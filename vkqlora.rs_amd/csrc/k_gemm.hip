@@ -214,6 +214,7 @@ struct Stage<R, ROWK, E_NF4> {
     const int row = threadIdx.x / TPR, kq = (threadIdx.x % TPR) * EPT;
     const int64_t gr = r0 + row;
     valid = gr < w.rows;
+    raw = word_t{};
     if (valid) {
       const int64_t e = gr * w.cols + k0 + kq;
       raw = *(const word_t *)(w.codes + (e >> 1));
@@ -224,11 +225,15 @@ struct Stage<R, ROWK, E_NF4> {
                                         int kind) const {
     const int row = threadIdx.x / TPR, kq = (threadIdx.x % TPR) * EPT;
     const float s = valid ? decode_scale(kind, sc) : 0.0f;
+    // every codebook read first, then the stores: interleaved, each read
+    // would wait for the store before it (the compiler cannot tell the
+    // codebook from the tile)
+    // (out-of-range rows: code word 0 and scale 0, so no branch per read)
+    float v[EPT];
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      float v = valid ? lut[nib(raw, e)] * s : 0.0f;
-      S[(kq + e) * (R + PAD) + row] = v;
-    }
+    for (int e = 0; e < EPT; ++e) v[e] = lut[nib(raw, e)] * s;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) S[(kq + e) * (R + PAD) + row] = v[e];
   }
 };
 
@@ -247,6 +252,7 @@ struct Stage<R, KROW, E_NF4> {
     const int kr = threadIdx.x / 8, cq = (threadIdx.x % 8) * EPT;
     const int64_t gn = k0 + kr, gc = r0 + cq;
     valid = gn < w.rows && gc < w.cols;
+    raw = word_t{};
     if (valid) {
       const int64_t e = gn * w.cols + gc;
       raw = *(const word_t *)(w.codes + (e >> 1));
@@ -257,15 +263,13 @@ struct Stage<R, KROW, E_NF4> {
                                         int kind) const {
     const int kr = threadIdx.x / 8, cq = (threadIdx.x % 8) * EPT;
     const float s = valid ? decode_scale(kind, sc) : 0.0f;
+    // every codebook read first, then the stores (as above)
+    float v[EPT];
 #pragma unroll
-    for (int e4 = 0; e4 < EPT; e4 += 4) {
-      float4 f;
-      f.x = valid ? lut[nib(raw, e4 + 0)] * s : 0.0f;
-      f.y = valid ? lut[nib(raw, e4 + 1)] * s : 0.0f;
-      f.z = valid ? lut[nib(raw, e4 + 2)] * s : 0.0f;
-      f.w = valid ? lut[nib(raw, e4 + 3)] * s : 0.0f;
-      *(float4 *)&S[kr * (R + PAD) + cq + e4] = f;
-    }
+    for (int e = 0; e < EPT; ++e) v[e] = lut[nib(raw, e)] * s;
+#pragma unroll
+    for (int e4 = 0; e4 < EPT; e4 += 4)
+      *(float4 *)&S[kr * (R + PAD) + cq + e4] = make_float4(v[e4], v[e4 + 1], v[e4 + 2], v[e4 + 3]);
   }
 };
 
