@@ -4,6 +4,10 @@ allocator and stream provider here; all compute is the library's kernels).
 ``DeviceWeight`` keeps a packed NF4 weight in HBM (codes, i8 scale codes,
 fp32 absmax); ``forward`` / ``backward`` call the ``*_dev`` entry points on
 torch's current stream without synchronising.
+
+Import torch before the library is first loaded: torch's wheel bundles its
+own ``libamdhip64.so.7`` (same soname as the one the library links), the
+first one loaded serves the process, and torch finds no GPU on the other.
 """
 from __future__ import annotations
 
