@@ -233,6 +233,65 @@ QH_API qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w,
                                        float *d_grad_x, float *d_grad_a,
                                        float *d_grad_b, void *stream);
 
+/* ---- the glue of a decoder block around its projections ----------------
+ * qlora-model/src/llama.rs calls these between the QLoRA projections of
+ * `block_forward` / `block_backward` (llama.rs:417-602).  All fp32,
+ * row-major.  The host-slice forms validate lengths (QH_ERR_SHAPE_MISMATCH)
+ * and block; the `_dev` forms enqueue on `stream` and trust their sizes. */
+
+/* rmsnorm_in_place (llama.rs:730-739): y = x / sqrt(mean(x^2) + eps) * w for
+ * each of `rows` rows of h; y may alias x. */
+QH_API qh_status qh_rmsnorm(qh_ctx *ctx, const float *x, size_t x_len,
+                            const float *w, size_t h, float eps, float *y);
+QH_API qh_status qh_rmsnorm_dev(qh_ctx *ctx, const float *d_x, const float *d_w,
+                                size_t rows, size_t h, float eps, float *d_y,
+                                void *stream);
+/* rmsnorm_backward (llama.rs:605-631): dx (rows x h) and, unless dw is NULL,
+ * dw (h).  block_backward discards dw (llama.rs:560, 599); pass NULL to skip
+ * it.  dx may alias dy only when dw is NULL (the dw pass reads dy after dx
+ * is written; the device form rejects that aliasing). */
+QH_API qh_status qh_rmsnorm_backward(qh_ctx *ctx, const float *x, size_t x_len,
+                                     const float *w, size_t h, const float *dy,
+                                     size_t dy_len, float eps, float *dx,
+                                     float *dw);
+QH_API qh_status qh_rmsnorm_backward_dev(qh_ctx *ctx, const float *d_x,
+                                         const float *d_w, const float *d_dy,
+                                         size_t rows, size_t h, float eps,
+                                         float *d_dx, float *d_dw,
+                                         void *stream);
+/* MLP activation (llama.rs:452-456, 516-518): act = silu(gate) * up over n
+ * elements; act may alias gate or up. */
+QH_API qh_status qh_swiglu(qh_ctx *ctx, const float *gate, size_t gate_len,
+                           const float *up, size_t up_len, float *act);
+QH_API qh_status qh_swiglu_dev(qh_ctx *ctx, const float *d_gate,
+                               const float *d_up, size_t n, float *d_act,
+                               void *stream);
+/* Its backward (llama.rs:546-551, 520-529): dg = d_act * up * silu'(gate),
+ * du = d_act * silu(gate); dg may alias gate, du may alias up. */
+QH_API qh_status qh_swiglu_backward(qh_ctx *ctx, const float *gate,
+                                    const float *up, const float *d_act,
+                                    size_t n, float *dg, float *du);
+QH_API qh_status qh_swiglu_backward_dev(qh_ctx *ctx, const float *d_gate,
+                                        const float *d_up, const float *d_act,
+                                        size_t n, float *d_dg, float *d_du,
+                                        void *stream);
+/* softmax_cross_entropy (llama.rs:487-514): *loss = mean over seq rows of
+ * -log softmax(logits)[target]; dlogits = (softmax - onehot) / seq, row-major
+ * (seq x vocab), may alias logits.  The host form rejects a target >= vocab
+ * (the reference panics on it); the device form gives a NaN loss for one and
+ * leaves out its one-hot term. */
+QH_API qh_status qh_softmax_cross_entropy(qh_ctx *ctx, const float *logits,
+                                          size_t logits_len,
+                                          const uint32_t *targets, size_t seq,
+                                          size_t vocab, float *loss,
+                                          float *dlogits);
+QH_API qh_status qh_softmax_cross_entropy_dev(qh_ctx *ctx,
+                                              const float *d_logits,
+                                              const uint32_t *d_targets,
+                                              size_t seq, size_t vocab,
+                                              float *d_loss, float *d_dlogits,
+                                              void *stream);
+
 #ifdef __cplusplus
 }
 #endif

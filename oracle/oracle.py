@@ -76,6 +76,20 @@ def lib():
         L.or_adam_get_state.restype = C.c_int
         L.or_adam_get_state.argtypes = [C.c_void_p, C.c_size_t, _u8p, _f32p, _u8p,
                                         _f32p, C.POINTER(C.c_uint64)]
+        L.or_rmsnorm.argtypes = [_f32p, _f32p, C.c_size_t, C.c_size_t, C.c_float,
+                                 _f32p]
+        L.or_rmsnorm_backward.argtypes = [_f32p, _f32p, _f32p, C.c_size_t,
+                                          C.c_size_t, C.c_float, _f32p, _f32p]
+        L.or_silu.restype = C.c_float
+        L.or_silu.argtypes = [C.c_float]
+        L.or_silu_prime.restype = C.c_float
+        L.or_silu_prime.argtypes = [C.c_float]
+        L.or_swiglu.argtypes = [_f32p, _f32p, C.c_size_t, _f32p]
+        L.or_swiglu_backward.argtypes = [_f32p, _f32p, _f32p, C.c_size_t, _f32p,
+                                         _f32p]
+        L.or_softmax_cross_entropy.restype = C.c_float
+        L.or_softmax_cross_entropy.argtypes = [_f32p, C.POINTER(C.c_uint32),
+                                               C.c_size_t, C.c_size_t, _f32p]
         _lib = L
     return _lib
 
@@ -290,3 +304,62 @@ def dequant_block_i8(codes, absmax):
     out = np.empty(codes.size, np.float32)
     lib().or_dequant_block_i8(_bp(codes), absmax, codes.size, _fp(out))
     return out
+
+
+# ---- qlora-model/src/llama.rs: the glue around the projections -------------
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rmsnorm(x, w, rows, h, eps):
+    """llama.rs:730-739"""
+    x, w = _f32(x), _f32(w)
+    y = np.empty(rows * h, np.float32)
+    lib().or_rmsnorm(_fp(x), _fp(w), rows, h, eps, _fp(y))
+    return y
+
+
+def rmsnorm_backward(x, w, dy, rows, h, eps):
+    """llama.rs:605-631 -> (dx, dw)"""
+    x, w, dy = _f32(x), _f32(w), _f32(dy)
+    dx = np.empty(rows * h, np.float32)
+    dw = np.empty(h, np.float32)
+    lib().or_rmsnorm_backward(_fp(x), _fp(w), _fp(dy), rows, h, eps, _fp(dx), _fp(dw))
+    return dx, dw
+
+
+def silu(x: float) -> float:
+    return float(lib().or_silu(x))
+
+
+def silu_prime(x: float) -> float:
+    return float(lib().or_silu_prime(x))
+
+
+def swiglu(gate, up):
+    """llama.rs:452-456"""
+    gate, up = _f32(gate), _f32(up)
+    act = np.empty(gate.size, np.float32)
+    lib().or_swiglu(_fp(gate), _fp(up), gate.size, _fp(act))
+    return act
+
+
+def swiglu_backward(gate, up, d_act):
+    """llama.rs:546-551 -> (d_gate, d_up)"""
+    gate, up, d_act = _f32(gate), _f32(up), _f32(d_act)
+    dg = np.empty(gate.size, np.float32)
+    du = np.empty(gate.size, np.float32)
+    lib().or_swiglu_backward(_fp(gate), _fp(up), _fp(d_act), gate.size, _fp(dg), _fp(du))
+    return dg, du
+
+
+def softmax_cross_entropy(logits, targets, seq, vocab):
+    """llama.rs:487-514 -> (loss, dlogits)"""
+    logits = _f32(logits)
+    targets = np.ascontiguousarray(targets, dtype=np.uint32)
+    assert targets.size == seq and logits.size == seq * vocab
+    assert seq == 0 or int(targets.max()) < vocab
+    d = np.empty(seq * vocab, np.float32)
+    loss = lib().or_softmax_cross_entropy(
+        _fp(logits), targets.ctypes.data_as(C.POINTER(C.c_uint32)), seq, vocab, _fp(d))
+    return float(loss), d

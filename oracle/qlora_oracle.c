@@ -422,3 +422,90 @@ int or_adam_get_state(const or_adam *o, size_t idx, uint8_t *m_codes,
   *step = st->step;
   return 0;
 }
+
+/* ===== qlora-model glue around the projections (qlora-model/src/llama.rs) */
+
+/* llama.rs:730-739.  The row sum is Rust's sequential f32 Sum. */
+void or_rmsnorm(const float *x, const float *w, size_t rows, size_t h,
+                float eps, float *y) {
+  for (size_t t = 0; t < rows; t++) {
+    const float *xr = x + t * h;
+    float *yr = y + t * h;
+    float acc = 0.0f;
+    for (size_t j = 0; j < h; j++) acc += xr[j] * xr[j];
+    float mean_sq = acc / (float)h;
+    float scale = 1.0f / sqrtf(mean_sq + eps);
+    for (size_t j = 0; j < h; j++) yr[j] = xr[j] * scale * w[j];
+  }
+}
+
+/* llama.rs:605-631 */
+void or_rmsnorm_backward(const float *x, const float *w, const float *dy,
+                         size_t rows, size_t h, float eps, float *dx,
+                         float *dw) {
+  for (size_t j = 0; j < h; j++) dw[j] = 0.0f;
+  for (size_t t = 0; t < rows; t++) {
+    const float *xr = x + t * h;
+    const float *dyr = dy + t * h;
+    float acc = 0.0f;
+    for (size_t j = 0; j < h; j++) acc += xr[j] * xr[j];
+    float mean_sq = acc / (float)h;
+    float ss = mean_sq + eps;
+    float r = 1.0f / sqrtf(ss);
+    float ds = 0.0f;
+    for (size_t j = 0; j < h; j++) {
+      ds += dyr[j] * xr[j] * w[j];
+      dw[j] += dyr[j] * xr[j] * r;
+    }
+    ds *= -0.5f * (1.0f / ss) * r;
+    for (size_t j = 0; j < h; j++)
+      dx[t * h + j] = dyr[j] * w[j] * r + 2.0f * xr[j] / (float)h * ds;
+  }
+}
+
+/* llama.rs:516-529 */
+float or_silu(float x) { return x / (1.0f + expf(-x)); }
+
+static float or_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+float or_silu_prime(float x) {
+  float s = or_sigmoid(x);
+  return s * (1.0f + x * (1.0f - s));
+}
+
+/* llama.rs:452-456 */
+void or_swiglu(const float *gate, const float *up, size_t n, float *act) {
+  for (size_t i = 0; i < n; i++) act[i] = or_silu(gate[i]) * up[i];
+}
+
+/* llama.rs:546-551 */
+void or_swiglu_backward(const float *gate, const float *up,
+                        const float *d_act, size_t n, float *dg, float *du) {
+  for (size_t i = 0; i < n; i++) {
+    dg[i] = d_act[i] * up[i] * or_silu_prime(gate[i]);
+    du[i] = d_act[i] * or_silu(gate[i]);
+  }
+}
+
+/* llama.rs:487-514.  f32::max ignores NaN (fmaxf); the row max starts at
+ * -inf. */
+float or_softmax_cross_entropy(const float *logits, const uint32_t *targets,
+                               size_t seq, size_t vocab, float *dlogits) {
+  float loss = 0.0f;
+  for (size_t t = 0; t < seq; t++) {
+    const float *row = logits + t * vocab;
+    float *d = dlogits + t * vocab;
+    float mx = -INFINITY;
+    for (size_t j = 0; j < vocab; j++) mx = fmaxf(mx, row[j]);
+    float sum = 0.0f;
+    for (size_t j = 0; j < vocab; j++) {
+      float e = expf(row[j] - mx);
+      d[j] = e;
+      sum += e;
+    }
+    loss -= (row[targets[t]] - mx - logf(sum)) / (float)seq;
+    for (size_t j = 0; j < vocab; j++) d[j] = d[j] / sum / (float)seq;
+    d[targets[t]] -= 1.0f / (float)seq;
+  }
+  return loss;
+}

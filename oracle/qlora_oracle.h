@@ -89,6 +89,29 @@ int or_adam_get_state(const or_adam *o, size_t idx, uint8_t *m_codes,
                       float *m_scales, uint8_t *v_codes, float *v_scales,
                       uint64_t *step);
 
+/* ---- qlora-model glue around the projections (qlora-model/src/llama.rs) */
+/* rmsnorm_in_place (llama.rs:730-739): y = x * (1/sqrt(mean(x^2)+eps)) * w
+ * per row of h; y may alias x. */
+void or_rmsnorm(const float *x, const float *w, size_t rows, size_t h,
+                float eps, float *y);
+/* rmsnorm_backward (llama.rs:605-631): dx (rows x h) and dw (h). */
+void or_rmsnorm_backward(const float *x, const float *w, const float *dy,
+                         size_t rows, size_t h, float eps, float *dx,
+                         float *dw);
+/* silu / sigmoid / silu_prime (llama.rs:516-529). */
+float or_silu(float x);
+float or_silu_prime(float x);
+/* MLP activation (llama.rs:452-456): act = silu(gate) * up. */
+void or_swiglu(const float *gate, const float *up, size_t n, float *act);
+/* Its backward (llama.rs:546-551): dg = d_act*up*silu'(gate),
+ * du = d_act*silu(gate). */
+void or_swiglu_backward(const float *gate, const float *up,
+                        const float *d_act, size_t n, float *dg, float *du);
+/* softmax_cross_entropy (llama.rs:487-514): mean loss over seq rows and
+ * dlogits (seq x vocab).  Returns the loss. */
+float or_softmax_cross_entropy(const float *logits, const uint32_t *targets,
+                               size_t seq, size_t vocab, float *dlogits);
+
 #ifdef __cplusplus
 }
 #endif

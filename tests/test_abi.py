@@ -165,3 +165,32 @@ def test_python_surface_validation():
     q["codes"] = np.zeros(15, np.uint8)
     with pytest.raises(ValueError, match="codes length"):
         _rebuild(wq, None, None, None)
+
+
+def test_block_glue_validation_messages():
+    L = qlora_hip.load()
+    x = np.ones(12, np.float32).ctypes.data_as(C.c_void_p)
+    # h == 0 has no row (llama.rs:732 chunks of w.len() would panic)
+    assert L.qh_rmsnorm(None, x, 12, x, 0, 1e-5, x) == 1
+    assert _err(L) == "shape mismatch: hidden size (w.len()) is 0"
+    assert L.qh_rmsnorm(None, x, 12, x, 5, 1e-5, x) == 1
+    assert _err(L) == "shape mismatch: x.len() = 12 is not a multiple of the hidden size 5"
+    assert L.qh_rmsnorm_backward(None, x, 12, x, 4, x, 8, 1e-5, x, None) == 1
+    assert _err(L) == "shape mismatch: dy.len() = 8 but x.len() = 12"
+    assert L.qh_rmsnorm_dev(None, x, x, 3, 0, 1e-5, x, None) == 1
+    assert L.qh_rmsnorm_backward_dev(None, x, x, x, 3, 4, 1e-5, x, x, None) == 2
+    assert _err(L) == "invalid config: dx may alias dy only when dw is not requested"
+    assert L.qh_swiglu(None, x, 12, x, 11, x) == 1
+    assert _err(L) == "shape mismatch: gate.len() = 12 but up.len() = 11"
+    # llama.rs:508 indexes row[targets[t]]: a target >= vocab is rejected
+    t = np.array([0, 3], np.uint32)
+    tp = t.ctypes.data_as(C.c_void_p)
+    assert L.qh_softmax_cross_entropy(None, x, 6, tp, 2, 3, None, x) == 1
+    assert _err(L) == "shape mismatch: target 3 at position 1 is out of range for vocab 3"
+    assert L.qh_softmax_cross_entropy(None, x, 5, tp, 2, 3, None, x) == 1
+    assert _err(L) == "shape mismatch: logits.len() = 5 but seq*vocab = 6"
+    assert L.qh_softmax_cross_entropy_dev(None, x, tp, 2, 0, None, x, None) == 1
+    assert _err(L) == "shape mismatch: vocab is 0"
+    # valid arguments reach the context check
+    assert L.qh_swiglu_backward(None, x, x, x, 4, x, x) == 3
+    assert _err(L) == "gpu error: context is NULL"

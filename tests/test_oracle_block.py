@@ -1,0 +1,129 @@
+"""Pins of the oracle's restatement of the glue around the projections in
+qlora-model/src/llama.rs (RMSNorm, SwiGLU, softmax cross-entropy).
+
+Each check is independent of the restated formula: the reference's own
+known answer (llama.rs:846-853), float64 closed forms through numpy/scipy,
+central finite differences of a float64 forward for every backward, and
+invariants (shift invariance, rows of dlogits summing to zero).
+"""
+import numpy as np
+import pytest
+from scipy.special import expit, logsumexp
+
+import oracle as O
+
+
+def test_rmsnorm_known_answer():
+    # llama.rs:846-853
+    y = O.rmsnorm(np.array([1, 2, 3, 4], np.float32), np.ones(4, np.float32), 1, 4, 0.0)
+    rms = np.float32(np.sqrt(np.float32(30.0) / 4))
+    assert abs(y[0] - 1.0 / rms) < 1e-6
+    assert abs(y[3] - 4.0 / rms) < 1e-6
+
+
+def _rms64(x, w, rows, h, eps):
+    x = x.astype(np.float64).reshape(rows, h)
+    return (x / np.sqrt((x * x).mean(axis=1, keepdims=True) + eps) * w.astype(np.float64)).ravel()
+
+
+@pytest.mark.parametrize("rows,h,eps", [(5, 576, 1e-5), (3, 7, 1e-6), (2, 1, 0.5)])
+def test_rmsnorm_closed_form(rows, h, eps):
+    g = O.Rng(11)
+    x = g.normal(rows * h)
+    w = g.uniform(h, 0.5, 1.5)
+    y = O.rmsnorm(x, w, rows, h, eps)
+    ref = _rms64(x, w, rows, h, eps)
+    assert np.max(np.abs(y - ref)) <= 2e-6 * np.max(np.abs(ref))
+    # scale invariance of the normalised part (eps = 0)
+    y1 = O.rmsnorm(x, w, rows, h, 0.0)
+    y2 = O.rmsnorm(x * np.float32(8.0), w, rows, h, 0.0)
+    assert np.max(np.abs(y1 - y2)) <= 1e-6 * np.max(np.abs(y1))
+
+
+def _fd(f, v, eps=1e-4):
+    g = np.zeros_like(v)
+    for i in range(v.size):
+        p, m = v.copy(), v.copy()
+        p[i] += eps
+        m[i] -= eps
+        g[i] = (f(p) - f(m)) / (2 * eps)
+    return g
+
+
+def test_rmsnorm_backward_finite_differences():
+    rows, h, eps = 3, 9, 1e-3
+    g = O.Rng(12)
+    x = g.normal(rows * h)
+    w = g.uniform(h, 0.5, 1.5)
+    dy = g.normal(rows * h)
+    dx, dw = O.rmsnorm_backward(x, w, dy, rows, h, eps)
+    x64, w64, dy64 = x.astype(np.float64), w.astype(np.float64), dy.astype(np.float64)
+    fdx = _fd(lambda v: float(np.dot(dy64, _rms64(v, w64, rows, h, eps))), x64)
+    fdw = _fd(lambda v: float(np.dot(dy64, _rms64(x64, v, rows, h, eps))), w64)
+    assert np.max(np.abs(dx - fdx)) < 1e-4 * max(1.0, np.max(np.abs(fdx)))
+    assert np.max(np.abs(dw - fdw)) < 1e-4 * max(1.0, np.max(np.abs(fdw)))
+
+
+def test_silu_closed_forms():
+    xs = np.array([-30, -5.5, -1, -1e-3, 0, 1e-3, 0.5, 2, 7, 30], np.float32)
+    for x in map(float, xs):
+        ref = x * expit(x)
+        assert abs(O.silu(x) - ref) <= 1e-6 * max(1.0, abs(ref))
+        fd = ((x + 1e-4) * expit(x + 1e-4) - (x - 1e-4) * expit(x - 1e-4)) / 2e-4
+        assert abs(O.silu_prime(x) - fd) < 1e-6
+    assert O.silu(0.0) == 0.0 and O.silu_prime(0.0) == 0.5
+
+
+def test_swiglu_and_backward():
+    g = O.Rng(13)
+    n = 41
+    gate, up, da = g.normal(n, 3.0), g.normal(n), g.normal(n)
+    act = O.swiglu(gate, up)
+    g64, u64 = gate.astype(np.float64), up.astype(np.float64)
+    ref = g64 * expit(g64) * u64
+    assert np.max(np.abs(act - ref)) <= 2e-6 * np.max(np.abs(ref))
+    dg, du = O.swiglu_backward(gate, up, da)
+    d64 = da.astype(np.float64)
+    fdg = _fd(lambda v: float(np.dot(d64, v * expit(v) * u64)), g64)
+    fdu = _fd(lambda v: float(np.dot(d64, g64 * expit(g64) * v)), u64)
+    assert np.max(np.abs(dg - fdg)) < 1e-4
+    assert np.max(np.abs(du - fdu)) < 1e-4
+
+
+def _ce64(logits, targets, seq, vocab):
+    z = logits.astype(np.float64).reshape(seq, vocab)
+    lse = logsumexp(z, axis=1)
+    return float(np.mean(lse - z[np.arange(seq), targets]))
+
+
+@pytest.mark.parametrize("seq,vocab", [(4, 10), (3, 1), (2, 4099)])
+def test_softmax_ce_closed_form(seq, vocab):
+    g = O.Rng(14)
+    logits = g.normal(seq * vocab, 4.0)
+    targets = np.array([(7 * t + 3) % vocab for t in range(seq)], np.uint32)
+    loss, d = O.softmax_cross_entropy(logits, targets, seq, vocab)
+    assert abs(loss - _ce64(logits, targets, seq, vocab)) <= 1e-5 * max(1.0, abs(loss))
+    z = logits.astype(np.float64).reshape(seq, vocab)
+    p = np.exp(z - logsumexp(z, axis=1, keepdims=True))
+    p[np.arange(seq), targets] -= 1.0
+    ref = (p / seq).ravel()
+    # f32 sums over the vocabulary: relative error grows like n * 2^-24
+    assert np.max(np.abs(d - ref)) <= 1e-5 * np.max(np.abs(ref))
+    # rows of dlogits sum to zero; a shift of every logit changes nothing
+    assert np.max(np.abs(d.reshape(seq, vocab).sum(axis=1))) < 1e-5
+    loss2, d2 = O.softmax_cross_entropy(logits + np.float32(3.0), targets, seq, vocab)
+    assert abs(loss2 - loss) < 1e-5 and np.max(np.abs(d2 - d)) < 1e-6
+
+
+def test_softmax_ce_uniform_and_fd():
+    loss, d = O.softmax_cross_entropy(np.zeros(2 * 16, np.float32),
+                                      np.array([0, 15], np.uint32), 2, 16)
+    assert abs(loss - np.log(16)) < 1e-6
+    assert abs(d[0] - (1 / 16 - 1) / 2) < 1e-7 and abs(d[1] - 1 / 32) < 1e-7
+    g = O.Rng(15)
+    seq, vocab = 2, 6
+    logits = g.normal(seq * vocab)
+    tg = np.array([1, 5], np.uint32)
+    _, d = O.softmax_cross_entropy(logits, tg, seq, vocab)
+    fd = _fd(lambda v: _ce64(v, tg, seq, vocab), logits.astype(np.float64))
+    assert np.max(np.abs(d - fd)) < 1e-6

@@ -20,7 +20,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = ["runtime.cpp", "k_quant.hip", "k_gemm.hip", "k_gemv.hip",
-           "k_decode.hip", "k_dstream.hip", "k_adam.hip", "k_elem.hip"]
+           "k_decode.hip", "k_dstream.hip", "k_adam.hip", "k_elem.hip",
+           "k_block.hip"]
 
 COMMON = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",

@@ -1,0 +1,491 @@
+// k_block.hip -- the glue of a decoder block around its projections
+// (qlora-model/src/llama.rs): RMSNorm forward and backward, the SwiGLU
+// activation and its backward, and the softmax cross-entropy of the logits.
+//
+// All of it is HBM-bound streaming: rows are reduced inside one wave (RMSNorm)
+// or one workgroup (cross-entropy, whose rows are vocabulary-long), values are
+// kept in registers between the reduction and the write-back where they fit,
+// and every cross-row sum runs in a fixed order so results repeat bit for bit.
+#include <math.h>
+
+#include "qh_internal.h"
+
+namespace qh {
+namespace {
+
+constexpr int kBlock = 256;    // RMSNorm / SwiGLU workgroups: 4 waves
+constexpr int kCeBlock = 1024; // cross-entropy: 16 waves per row
+
+__device__ __forceinline__ float wave_sum(float v) {
+  // xor butterfly: every lane ends with the same bits (a + b == b + a)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// ---- RMSNorm (llama.rs:730-739) ---------------------------------------------
+// One wave per row: the sum of squares is reduced across the wave, then the
+// row is read again (from cache) and scaled.  y may alias x.
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void k_rmsnorm(const float *x, const float *__restrict__ w,
+                                                    float *y, int64_t rows, int h, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float *xr = x + row * h;
+  float *yr = y + row * h;
+  float acc = 0.0f;
+  if (V4) {
+    const int h4 = h >> 2;
+    for (int c = lane; c < h4; c += 64) {
+      const float4 v = reinterpret_cast<const float4 *>(xr)[c];
+      acc += v.x * v.x;
+      acc += v.y * v.y;
+      acc += v.z * v.z;
+      acc += v.w * v.w;
+    }
+  } else {
+    for (int j = lane; j < h; j += 64) acc += xr[j] * xr[j];
+  }
+  const float mean_sq = wave_sum(acc) / (float)h;
+  const float scale = 1.0f / sqrtf(mean_sq + eps);
+  if (V4) {
+    const int h4 = h >> 2;
+    for (int c = lane; c < h4; c += 64) {
+      const float4 v = reinterpret_cast<const float4 *>(xr)[c];
+      const float4 g = reinterpret_cast<const float4 *>(w)[c];
+      float4 o;
+      o.x = v.x * scale * g.x;
+      o.y = v.y * scale * g.y;
+      o.z = v.z * scale * g.z;
+      o.w = v.w * scale * g.w;
+      reinterpret_cast<float4 *>(yr)[c] = o;
+    }
+  } else {
+    for (int j = lane; j < h; j += 64) yr[j] = xr[j] * scale * w[j];
+  }
+}
+
+// rmsnorm_backward's dx (llama.rs:605-631), one wave per row.  With
+// S = mean(x^2) + eps and r = 1/sqrt(S):
+//   ds = sum(dy x w) * (-0.5 / S * r),  dx = dy w r + 2 x / h * ds.
+// r is kept per row (rstd) when the caller asks for dw.  dx may alias dy
+// when dw is not wanted (k_rmsnorm_dw_part reads dy again).
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_bwd(const float *__restrict__ x,
+                                                        const float *__restrict__ w,
+                                                        const float *dy, float *dx,
+                                                        float *__restrict__ rstd, int64_t rows,
+                                                        int h, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float *xr = x + row * h;
+  const float *gr = dy + row * h;
+  float *dr = dx + row * h;
+  float s1 = 0.0f, s2 = 0.0f;
+  if (V4) {
+    const int h4 = h >> 2;
+    for (int c = lane; c < h4; c += 64) {
+      const float4 v = reinterpret_cast<const float4 *>(xr)[c];
+      const float4 g = reinterpret_cast<const float4 *>(gr)[c];
+      const float4 q = reinterpret_cast<const float4 *>(w)[c];
+      s1 += v.x * v.x;
+      s1 += v.y * v.y;
+      s1 += v.z * v.z;
+      s1 += v.w * v.w;
+      s2 += g.x * v.x * q.x;
+      s2 += g.y * v.y * q.y;
+      s2 += g.z * v.z * q.z;
+      s2 += g.w * v.w * q.w;
+    }
+  } else {
+    for (int j = lane; j < h; j += 64) {
+      s1 += xr[j] * xr[j];
+      s2 += gr[j] * xr[j] * w[j];
+    }
+  }
+  const float ss = wave_sum(s1) / (float)h + eps;
+  const float r = 1.0f / sqrtf(ss);
+  const float ds = wave_sum(s2) * (-0.5f * (1.0f / ss) * r);
+  const float fh = (float)h;
+  if (rstd != nullptr && lane == 0) rstd[row] = r;
+  if (V4) {
+    const int h4 = h >> 2;
+    for (int c = lane; c < h4; c += 64) {
+      const float4 v = reinterpret_cast<const float4 *>(xr)[c];
+      const float4 g = reinterpret_cast<const float4 *>(gr)[c];
+      const float4 q = reinterpret_cast<const float4 *>(w)[c];
+      float4 o;
+      o.x = g.x * q.x * r + 2.0f * v.x / fh * ds;
+      o.y = g.y * q.y * r + 2.0f * v.y / fh * ds;
+      o.z = g.z * q.z * r + 2.0f * v.z / fh * ds;
+      o.w = g.w * q.w * r + 2.0f * v.w / fh * ds;
+      reinterpret_cast<float4 *>(dr)[c] = o;
+    }
+  } else {
+    for (int j = lane; j < h; j += 64) dr[j] = gr[j] * w[j] * r + 2.0f * xr[j] / fh * ds;
+  }
+}
+
+// rmsnorm_backward's dw: dw[j] = sum_t dy[t][j] x[t][j] r[t].  Stage 1: slice
+// z of the rows (blockIdx.y) sums its rows in order for 256 columns per
+// workgroup; stage 2 (k_colsum) adds the slices in order.
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_dw_part(const float *__restrict__ x,
+                                                            const float *__restrict__ dy,
+                                                            const float *__restrict__ rstd,
+                                                            float *__restrict__ part,
+                                                            int64_t rows, int h,
+                                                            int64_t rows_per_slice) {
+  const int j = blockIdx.x * kBlock + threadIdx.x;
+  if (j >= h) return;
+  const int64_t t0 = (int64_t)blockIdx.y * rows_per_slice;
+  const int64_t t1 = t0 + rows_per_slice < rows ? t0 + rows_per_slice : rows;
+  float acc = 0.0f;
+  for (int64_t t = t0; t < t1; ++t) acc += dy[t * h + j] * x[t * h + j] * rstd[t];
+  part[(int64_t)blockIdx.y * h + j] = acc;
+}
+
+__global__ __launch_bounds__(kBlock) void k_colsum(const float *__restrict__ part, int nparts,
+                                                   int h, float *__restrict__ out) {
+  const int j = blockIdx.x * kBlock + threadIdx.x;
+  if (j >= h) return;
+  float acc = 0.0f;
+  for (int z = 0; z < nparts; ++z) acc += part[(int64_t)z * h + j];
+  out[j] = acc;
+}
+
+// ---- SwiGLU (llama.rs:452-456, 516-529, 546-551) ------------------------------
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ float silu_prime(float v) {
+  const float s = 1.0f / (1.0f + expf(-v));
+  return s * (1.0f + v * (1.0f - s));
+}
+
+// act = silu(gate) * up; one float4 per thread, the n % 4 tail by the first
+// threads of the grid.  act may alias gate or up.
+__global__ __launch_bounds__(kBlock) void k_swiglu(const float *gate, const float *up,
+                                                   float *act, int64_t n, int v4) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (v4) {
+    const int64_t n4 = n >> 2;
+    if (i < n4) {
+      const float4 g = reinterpret_cast<const float4 *>(gate)[i];
+      const float4 u = reinterpret_cast<const float4 *>(up)[i];
+      float4 o;
+      o.x = silu(g.x) * u.x;
+      o.y = silu(g.y) * u.y;
+      o.z = silu(g.z) * u.z;
+      o.w = silu(g.w) * u.w;
+      reinterpret_cast<float4 *>(act)[i] = o;
+    }
+    const int64_t k = n4 * 4 + i;
+    if (i < (n & 3)) act[k] = silu(gate[k]) * up[k];
+  } else if (i < n) {
+    act[i] = silu(gate[i]) * up[i];
+  }
+}
+
+// dg = d_act * up * silu'(gate), du = d_act * silu(gate).  dg may alias gate
+// and du may alias up (each element is read before it is written, by the same
+// thread).
+__global__ __launch_bounds__(kBlock) void k_swiglu_bwd(const float *gate, const float *up,
+                                                       const float *d_act, float *dg, float *du,
+                                                       int64_t n, int v4) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (v4) {
+    const int64_t n4 = n >> 2;
+    if (i < n4) {
+      const float4 g = reinterpret_cast<const float4 *>(gate)[i];
+      const float4 u = reinterpret_cast<const float4 *>(up)[i];
+      const float4 d = reinterpret_cast<const float4 *>(d_act)[i];
+      float4 a, b;
+      a.x = d.x * u.x * silu_prime(g.x);
+      a.y = d.y * u.y * silu_prime(g.y);
+      a.z = d.z * u.z * silu_prime(g.z);
+      a.w = d.w * u.w * silu_prime(g.w);
+      b.x = d.x * silu(g.x);
+      b.y = d.y * silu(g.y);
+      b.z = d.z * silu(g.z);
+      b.w = d.w * silu(g.w);
+      reinterpret_cast<float4 *>(dg)[i] = a;
+      reinterpret_cast<float4 *>(du)[i] = b;
+    }
+    const int64_t k = n4 * 4 + i;
+    if (i < (n & 3)) {
+      const float g = gate[k], u = up[k], d = d_act[k];
+      dg[k] = d * u * silu_prime(g);
+      du[k] = d * silu(g);
+    }
+  } else if (i < n) {
+    const float g = gate[i], u = up[i], d = d_act[i];
+    dg[i] = d * u * silu_prime(g);
+    du[i] = d * silu(g);
+  }
+}
+
+// ---- softmax cross-entropy (llama.rs:487-514) ---------------------------------
+// One workgroup of 1024 threads per row.  Each thread holds up to CH float4
+// chunks of the row in registers (chunk c of thread t covers float4 index
+// c * 1024 + t); the rest of the row, if any, is streamed again in each pass.
+// Pass 1: the row max; pass 2: sum of exp(v - max); pass 3: dlogits =
+// exp(v - max) / sum / seq, minus 1/seq at the target.  terms[row] receives
+// (logit[target] - max - ln(sum)) / seq; the loss is -sum(terms) (k_loss).
+// dlogits may alias logits: every read of the row precedes the first
+// barrier after it, and each element is written by the thread that read it.
+template <int CH, bool V4>
+__global__ __launch_bounds__(kCeBlock) void k_softmax_ce(const float *logits,
+                                                         const uint32_t *__restrict__ targets,
+                                                         int64_t vocab, float fseq,
+                                                         float *dlogits,
+                                                         float *__restrict__ terms) {
+  constexpr int E = V4 ? 4 : 1;
+  __shared__ float red[kCeBlock / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const float *lr = logits + row * vocab;
+  float *dr = dlogits + row * vocab;
+  const int64_t nv = V4 ? (vocab >> 2) : vocab;  // vectors of E floats in the row
+  const uint32_t tgt = targets[row];
+  const bool tgt_ok = (int64_t)tgt < vocab;
+  const float xt = (tid == 0 && tgt_ok) ? lr[tgt] : 0.0f;
+
+  auto load = [&](int64_t c, float (&v)[E]) {
+    if (V4) {
+      const float4 q = reinterpret_cast<const float4 *>(lr)[c];
+      v[0] = q.x;
+      v[1] = q.y;
+      v[2] = q.z;
+      v[3] = q.w;
+    } else {
+      v[0] = lr[c];
+    }
+  };
+
+  float cache[CH > 0 ? CH : 1][E];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t q = (int64_t)c * kCeBlock + tid;
+    if (q < nv) {
+      load(q, cache[c]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) mx = fmaxf(mx, cache[c][e]);
+    }
+  }
+  for (int64_t q = (int64_t)CH * kCeBlock + tid; q < nv; q += kCeBlock) {
+    float v[E];
+    load(q, v);
+#pragma unroll
+    for (int e = 0; e < E; ++e) mx = fmaxf(mx, v[e]);
+  }
+  if (V4 && tid < (vocab & 3)) mx = fmaxf(mx, lr[(nv << 2) + tid]);
+  mx = wave_max(mx);
+  if (lane == 0) red[wv] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int k = 1; k < kCeBlock / 64; ++k) mx = fmaxf(mx, red[k]);
+  __syncthreads();
+
+  float sum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t q = (int64_t)c * kCeBlock + tid;
+    if (q < nv) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) sum += expf(cache[c][e] - mx);
+    }
+  }
+  for (int64_t q = (int64_t)CH * kCeBlock + tid; q < nv; q += kCeBlock) {
+    float v[E];
+    load(q, v);
+#pragma unroll
+    for (int e = 0; e < E; ++e) sum += expf(v[e] - mx);
+  }
+  float tail = 0.0f;
+  if (V4 && tid < (vocab & 3)) {
+    tail = lr[(nv << 2) + tid];
+    sum += expf(tail - mx);
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wv] = sum;
+  __syncthreads();
+  // fixed tree over the 16 wave sums: the same bits in every thread
+  float s[kCeBlock / 64];
+#pragma unroll
+  for (int k = 0; k < kCeBlock / 64; ++k) s[k] = red[k];
+#pragma unroll
+  for (int w2 = kCeBlock / 128; w2 > 0; w2 >>= 1) {
+#pragma unroll
+    for (int k = 0; k < w2; ++k) s[k] = s[k] + s[k + w2];
+  }
+  sum = s[0];
+
+  const float inv_seq = 1.0f / fseq;
+  auto grad = [&](float v, int64_t j) {
+    float d = expf(v - mx) / sum / fseq;
+    if (j == (int64_t)tgt) d -= inv_seq;
+    return d;
+  };
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t q = (int64_t)c * kCeBlock + tid;
+    if (q < nv) {
+      if (V4) {
+        float4 o;
+        o.x = grad(cache[c][0], q * 4 + 0);
+        o.y = grad(cache[c][1], q * 4 + 1);
+        o.z = grad(cache[c][2], q * 4 + 2);
+        o.w = grad(cache[c][3], q * 4 + 3);
+        reinterpret_cast<float4 *>(dr)[q] = o;
+      } else {
+        dr[q] = grad(cache[c][0], q);
+      }
+    }
+  }
+  for (int64_t q = (int64_t)CH * kCeBlock + tid; q < nv; q += kCeBlock) {
+    float v[E];
+    load(q, v);
+    if (V4) {
+      float4 o;
+      o.x = grad(v[0], q * 4 + 0);
+      o.y = grad(v[1], q * 4 + 1);
+      o.z = grad(v[2], q * 4 + 2);
+      o.w = grad(v[3], q * 4 + 3);
+      reinterpret_cast<float4 *>(dr)[q] = o;
+    } else {
+      dr[q] = grad(v[0], q);
+    }
+  }
+  if (V4 && tid < (vocab & 3)) dr[(nv << 2) + tid] = grad(tail, (nv << 2) + tid);
+  if (tid == 0) terms[row] = tgt_ok ? (xt - mx - logf(sum)) / fseq : NAN;
+}
+
+// loss = -sum_t terms[t]: thread i adds terms i, i + 1024, ... in order, then
+// a fixed tree over the 1024 partials.
+__global__ __launch_bounds__(kCeBlock) void k_loss(const float *__restrict__ terms,
+                                                   int64_t seq, float *__restrict__ loss) {
+  __shared__ float red[kCeBlock];
+  const int tid = threadIdx.x;
+  float acc = 0.0f;
+  for (int64_t t = tid; t < seq; t += kCeBlock) acc += terms[t];
+  red[tid] = acc;
+  __syncthreads();
+  for (int w2 = kCeBlock / 2; w2 > 0; w2 >>= 1) {
+    if (tid < w2) red[tid] = red[tid] + red[tid + w2];
+    __syncthreads();
+  }
+  if (tid == 0) loss[0] = 0.0f - red[0];
+}
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline unsigned grid_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int64_t rows, int h,
+                          float eps, hipStream_t s) {
+  if (rows == 0 || h == 0) return hipSuccess;
+  const unsigned g = grid_for(rows, kBlock / 64);
+  if (h % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y))
+    return qh_launch(k_rmsnorm<true>, dim3(g), dim3(kBlock), 0, s, x, w, y, rows, h, eps);
+  return qh_launch(k_rmsnorm<false>, dim3(g), dim3(kBlock), 0, s, x, w, y, rows, h, eps);
+}
+
+int rmsnorm_dw_slices(int64_t rows) {
+  // about 64 rows per slice, at most 256 slices
+  int64_t z = (rows + 63) / 64;
+  return (int)(z < 1 ? 1 : (z > 256 ? 256 : z));
+}
+
+// r per row (rounded up to 64 floats), then one partial dw per slice
+size_t rmsnorm_dw_scratch_floats(int64_t rows, int h) {
+  return (size_t)((rows + 63) / 64 * 64) + (size_t)rmsnorm_dw_slices(rows) * (size_t)h;
+}
+
+hipError_t launch_rmsnorm_bwd(const float *x, const float *w, const float *dy, float *dx,
+                              float *dw, float *scratch, int64_t rows, int h, float eps,
+                              hipStream_t s) {
+  if (h == 0) return hipSuccess;
+  float *rstd = dw ? scratch : nullptr;
+  if (rows > 0) {
+    const unsigned g = grid_for(rows, kBlock / 64);
+    hipError_t e;
+    if (h % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx))
+      e = qh_launch(k_rmsnorm_bwd<true>, dim3(g), dim3(kBlock), 0, s, x, w, dy, dx, rstd,
+                    rows, h, eps);
+    else
+      e = qh_launch(k_rmsnorm_bwd<false>, dim3(g), dim3(kBlock), 0, s, x, w, dy, dx, rstd,
+                    rows, h, eps);
+    if (e != hipSuccess || !dw) return e;
+  } else if (!dw) {
+    return hipSuccess;
+  }
+  const int z = rmsnorm_dw_slices(rows);
+  const int64_t per = rows > 0 ? (rows + z - 1) / z : 0;
+  float *part = scratch + ((rows + 63) / 64) * 64;
+  hipError_t e = qh_launch(k_rmsnorm_dw_part, dim3(grid_for(h, kBlock), (unsigned)z),
+                           dim3(kBlock), 0, s, x, dy, (const float *)rstd, part, rows, h, per);
+  if (e != hipSuccess) return e;
+  return qh_launch(k_colsum, dim3(grid_for(h, kBlock)), dim3(kBlock), 0, s,
+                   (const float *)part, z, h, dw);
+}
+
+hipError_t launch_swiglu(const float *gate, const float *up, float *act, int64_t n,
+                         hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const int v4 = aligned16(gate) && aligned16(up) && aligned16(act);
+  const int64_t items = v4 ? ((n >> 2) > (n & 3) ? (n >> 2) : (n & 3)) : n;
+  return qh_launch(k_swiglu, dim3(grid_for(items, kBlock)), dim3(kBlock), 0, s, gate, up, act,
+                   n, v4);
+}
+
+hipError_t launch_swiglu_bwd(const float *gate, const float *up, const float *d_act, float *dg,
+                             float *du, int64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const int v4 = aligned16(gate) && aligned16(up) && aligned16(d_act) && aligned16(dg) &&
+                 aligned16(du);
+  const int64_t items = v4 ? ((n >> 2) > (n & 3) ? (n >> 2) : (n & 3)) : n;
+  return qh_launch(k_swiglu_bwd, dim3(grid_for(items, kBlock)), dim3(kBlock), 0, s, gate, up,
+                   d_act, dg, du, n, v4);
+}
+
+hipError_t launch_softmax_ce(const float *logits, const uint32_t *targets, int64_t seq,
+                             int64_t vocab, float *loss, float *dlogits, float *terms,
+                             hipStream_t s) {
+  if (seq > 0) {
+    const float fseq = (float)seq;
+    const bool v4 = vocab % 4 == 0 && aligned16(logits) && aligned16(dlogits);
+    const int64_t nv = v4 ? vocab / 4 : vocab;
+    const int64_t per = (nv + kCeBlock - 1) / kCeBlock;  // vectors per thread
+    const dim3 g((unsigned)seq), b(kCeBlock);
+    hipError_t e;
+#define QH_CE(CHV)                                                                              \
+  (v4 ? qh_launch(k_softmax_ce<CHV, true>, g, b, 0, s, logits, targets, vocab, fseq, dlogits,  \
+                  terms)                                                                       \
+      : qh_launch(k_softmax_ce<CHV, false>, g, b, 0, s, logits, targets, vocab, fseq, dlogits, \
+                  terms))
+    // 12 float4 per thread (48 values, 108 VGPRs) is the most that stays
+    // out of scratch at 1024 threads; longer rows stream the rest each pass
+    if (per <= 4)
+      e = QH_CE(4);
+    else if (per <= 8)
+      e = QH_CE(8);
+    else
+      e = QH_CE(12);
+#undef QH_CE
+    if (e != hipSuccess) return e;
+  }
+  return qh_launch(k_loss, dim3(1), dim3(kCeBlock), 0, s, (const float *)terms, seq, loss);
+}
+
+}  // namespace qh

@@ -181,4 +181,22 @@ hipError_t launch_adam(const AdamTensor *d_tensors, int ntensors,
                        int64_t total_blocks, int64_t block_size, float lr,
                        float beta1, float beta2, float eps, hipStream_t s);
 
+// Block glue around the projections (k_block.hip).
+hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int64_t rows, int h,
+                          float eps, hipStream_t s);
+int rmsnorm_dw_slices(int64_t rows);
+// scratch of launch_rmsnorm_bwd when dw is wanted (floats)
+size_t rmsnorm_dw_scratch_floats(int64_t rows, int h);
+hipError_t launch_rmsnorm_bwd(const float *x, const float *w, const float *dy, float *dx,
+                              float *dw, float *scratch, int64_t rows, int h, float eps,
+                              hipStream_t s);
+hipError_t launch_swiglu(const float *gate, const float *up, float *act, int64_t n,
+                         hipStream_t s);
+hipError_t launch_swiglu_bwd(const float *gate, const float *up, const float *d_act, float *dg,
+                             float *du, int64_t n, hipStream_t s);
+// terms: seq floats of scratch
+hipError_t launch_softmax_ce(const float *logits, const uint32_t *targets, int64_t seq,
+                             int64_t vocab, float *loss, float *dlogits, float *terms,
+                             hipStream_t s);
+
 }  // namespace qh

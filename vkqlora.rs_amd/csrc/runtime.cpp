@@ -1150,4 +1150,212 @@ qh_status qh_adam8bit_get_state(qh_adam8bit *o, size_t idx, uint8_t *m_codes,
   });
 }
 
+// ---- the glue of a decoder block (qlora-model/src/llama.rs) -------------------
+static qh_status check_rows(size_t len, size_t h, const char *what, size_t *rows) {
+  if (h == 0) return fail(QH_ERR_SHAPE_MISMATCH, "hidden size (w.len()) is 0");
+  if (h > (size_t)INT32_MAX) return fail(QH_ERR_INVALID_CONFIG, "hidden size above 2^31-1");
+  if (len % h != 0)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("%s.len() = %zu is not a multiple of the hidden size %zu", what, len, h));
+  *rows = len / h;
+  return QH_OK;
+}
+
+static qh_status check_dev_rows(size_t rows, size_t h) {
+  size_t n;
+  if (h > (size_t)INT32_MAX) return fail(QH_ERR_INVALID_CONFIG, "hidden size above 2^31-1");
+  if (mul_overflows(rows, h, &n)) return fail(QH_ERR_SHAPE_MISMATCH, "rows*h overflows");
+  if (rows > 0 && h == 0) return fail(QH_ERR_SHAPE_MISMATCH, "hidden size is 0");
+  return QH_OK;
+}
+
+static float *dw_scratch(qh_ctx *ctx, size_t rows, size_t h) {
+  return (float *)ctx->scratch.ensure(qh::rmsnorm_dw_scratch_floats((int64_t)rows, (int)h) * 4);
+}
+
+qh_status qh_rmsnorm(qh_ctx *ctx, const float *x, size_t x_len, const float *w, size_t h,
+                     float eps, float *y) {
+  size_t rows;
+  qh_status st = check_rows(x_len, h, "x", &rows);
+  if (st != QH_OK) return st;
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    float *dx = upload_f32(ctx, 0, x, x_len, s);
+    float *dw = upload_f32(ctx, 1, w, h, s);
+    timed(ctx, "rmsnorm", s, [&] {
+      return qh::launch_rmsnorm(dx, dw, dx, (int64_t)rows, (int)h, eps, s);
+    });
+    download_f32(y, dx, x_len, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_rmsnorm_dev(qh_ctx *ctx, const float *d_x, const float *d_w, size_t rows,
+                         size_t h, float eps, float *d_y, void *stream) {
+  qh_status st = check_dev_rows(rows, h);
+  if (st != QH_OK) return st;
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    timed(ctx, "rmsnorm", s, [&] {
+      return qh::launch_rmsnorm(d_x, d_w, d_y, (int64_t)rows, (int)h, eps, s);
+    });
+    return QH_OK;
+  });
+}
+
+qh_status qh_rmsnorm_backward(qh_ctx *ctx, const float *x, size_t x_len, const float *w,
+                              size_t h, const float *dy, size_t dy_len, float eps, float *dx,
+                              float *dw) {
+  size_t rows;
+  qh_status st = check_rows(x_len, h, "x", &rows);
+  if (st != QH_OK) return st;
+  if (dy_len != x_len)
+    return fail(QH_ERR_SHAPE_MISMATCH, fmt("dy.len() = %zu but x.len() = %zu", dy_len, x_len));
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    float *d_x = upload_f32(ctx, 0, x, x_len, s);
+    float *d_w = upload_f32(ctx, 1, w, h, s);
+    float *d_dy = upload_f32(ctx, 2, dy, dy_len, s);
+    float *d_dw = dw ? alloc_f32(ctx, 3, h) : nullptr;
+    // dx over dy only without dw: the dw stage reads dy after dx is written
+    float *d_dx = dw ? alloc_f32(ctx, 4, x_len) : d_dy;
+    float *scr = dw ? dw_scratch(ctx, rows, h) : nullptr;
+    timed(ctx, "rmsnorm_backward", s, [&] {
+      return qh::launch_rmsnorm_bwd(d_x, d_w, d_dy, d_dx, d_dw, scr, (int64_t)rows, (int)h,
+                                    eps, s);
+    });
+    download_f32(dx, d_dx, x_len, s);
+    if (dw) download_f32(dw, d_dw, h, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_rmsnorm_backward_dev(qh_ctx *ctx, const float *d_x, const float *d_w,
+                                  const float *d_dy, size_t rows, size_t h, float eps,
+                                  float *d_dx, float *d_dw, void *stream) {
+  qh_status st = check_dev_rows(rows, h);
+  if (st != QH_OK) return st;
+  if (d_dw && rows > 0 && d_dx == d_dy)
+    return fail(QH_ERR_INVALID_CONFIG, "dx may alias dy only when dw is not requested");
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    float *scr = d_dw ? dw_scratch(ctx, rows, h) : nullptr;
+    timed(ctx, "rmsnorm_backward", s, [&] {
+      return qh::launch_rmsnorm_bwd(d_x, d_w, d_dy, d_dx, d_dw, scr, (int64_t)rows, (int)h,
+                                    eps, s);
+    });
+    return QH_OK;
+  });
+}
+
+qh_status qh_swiglu(qh_ctx *ctx, const float *gate, size_t gate_len, const float *up,
+                    size_t up_len, float *act) {
+  if (gate_len != up_len)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("gate.len() = %zu but up.len() = %zu", gate_len, up_len));
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    float *d_g = upload_f32(ctx, 0, gate, gate_len, s);
+    float *d_u = upload_f32(ctx, 1, up, up_len, s);
+    timed(ctx, "swiglu", s, [&] { return qh::launch_swiglu(d_g, d_u, d_g, (int64_t)gate_len, s); });
+    download_f32(act, d_g, gate_len, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_swiglu_dev(qh_ctx *ctx, const float *d_gate, const float *d_up, size_t n,
+                        float *d_act, void *stream) {
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    timed(ctx, "swiglu", s, [&] { return qh::launch_swiglu(d_gate, d_up, d_act, (int64_t)n, s); });
+    return QH_OK;
+  });
+}
+
+qh_status qh_swiglu_backward(qh_ctx *ctx, const float *gate, const float *up,
+                             const float *d_act, size_t n, float *dg, float *du) {
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    float *d_g = upload_f32(ctx, 0, gate, n, s);
+    float *d_u = upload_f32(ctx, 1, up, n, s);
+    float *d_a = upload_f32(ctx, 2, d_act, n, s);
+    timed(ctx, "swiglu_backward", s, [&] {
+      return qh::launch_swiglu_bwd(d_g, d_u, d_a, d_g, d_u, (int64_t)n, s);
+    });
+    download_f32(dg, d_g, n, s);
+    download_f32(du, d_u, n, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_swiglu_backward_dev(qh_ctx *ctx, const float *d_gate, const float *d_up,
+                                 const float *d_act, size_t n, float *d_dg, float *d_du,
+                                 void *stream) {
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    timed(ctx, "swiglu_backward", s, [&] {
+      return qh::launch_swiglu_bwd(d_gate, d_up, d_act, d_dg, d_du, (int64_t)n, s);
+    });
+    return QH_OK;
+  });
+}
+
+static qh_status check_ce(size_t seq, size_t vocab) {
+  size_t n;
+  if (mul_overflows(seq, vocab, &n)) return fail(QH_ERR_SHAPE_MISMATCH, "seq*vocab overflows");
+  if (seq > 0 && vocab == 0) return fail(QH_ERR_SHAPE_MISMATCH, "vocab is 0");
+  if (seq > (size_t)INT32_MAX) return fail(QH_ERR_INVALID_CONFIG, "seq above 2^31-1");
+  return QH_OK;
+}
+
+qh_status qh_softmax_cross_entropy(qh_ctx *ctx, const float *logits, size_t logits_len,
+                                   const uint32_t *targets, size_t seq, size_t vocab,
+                                   float *loss, float *dlogits) {
+  qh_status st = check_ce(seq, vocab);
+  if (st != QH_OK) return st;
+  if (logits_len != seq * vocab)
+    return fail(QH_ERR_SHAPE_MISMATCH,
+                fmt("logits.len() = %zu but seq*vocab = %zu", logits_len, seq * vocab));
+  for (size_t t = 0; t < seq; t++)
+    if ((size_t)targets[t] >= vocab)
+      return fail(QH_ERR_SHAPE_MISMATCH,
+                  fmt("target %u at position %zu is out of range for vocab %zu", targets[t], t,
+                      vocab));
+  return guarded(ctx, [&] {
+    hipStream_t s = ctx->stream;
+    float *d_l = upload_f32(ctx, 0, logits, logits_len, s);
+    uint32_t *d_t = (uint32_t *)ctx->stage[1].ensure(seq * 4 + 16);
+    if (seq) check(hipMemcpyAsync(d_t, targets, seq * 4, hipMemcpyHostToDevice, s), "upload");
+    float *d_loss = alloc_f32(ctx, 2, 1);
+    float *terms = (float *)ctx->scratch.ensure(seq * 4 + 16);
+    timed(ctx, "softmax_cross_entropy", s, [&] {
+      return qh::launch_softmax_ce(d_l, d_t, (int64_t)seq, (int64_t)vocab, d_loss, d_l, terms, s);
+    });
+    download_f32(dlogits, d_l, logits_len, s);
+    download_f32(loss, d_loss, 1, s);
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+}
+
+qh_status qh_softmax_cross_entropy_dev(qh_ctx *ctx, const float *d_logits,
+                                       const uint32_t *d_targets, size_t seq, size_t vocab,
+                                       float *d_loss, float *d_dlogits, void *stream) {
+  qh_status st = check_ce(seq, vocab);
+  if (st != QH_OK) return st;
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    float *terms = (float *)ctx->scratch.ensure(seq * 4 + 16);
+    timed(ctx, "softmax_cross_entropy", s, [&] {
+      return qh::launch_softmax_ce(d_logits, d_targets, (int64_t)seq, (int64_t)vocab, d_loss,
+                                   d_dlogits, terms, s);
+    });
+    return QH_OK;
+  });
+}
+
 }  // extern "C"

@@ -36,6 +36,9 @@ EXPORTED = [
     "qh_adam8bit_step_dev", "qh_adam8bit_state_bytes", "qh_adam8bit_get_state",
     "qh_quantize_nf4_dev", "qh_dequantize_dev", "qh_matmul_dev",
     "qh_qlora_forward_dev", "qh_qlora_backward_dev",
+    "qh_rmsnorm", "qh_rmsnorm_dev", "qh_rmsnorm_backward", "qh_rmsnorm_backward_dev",
+    "qh_swiglu", "qh_swiglu_dev", "qh_swiglu_backward", "qh_swiglu_backward_dev",
+    "qh_softmax_cross_entropy", "qh_softmax_cross_entropy_dev",
 ]
 
 
@@ -133,6 +136,17 @@ def load() -> C.CDLL:
                                            vp, i32, sz, vp, vp, vp]
         L.qh_qlora_backward_dev.argtypes = [vp, C.POINTER(QWeight), C.POINTER(Lora),
                                             vp, vp, i32, sz, vp, vp, vp, vp, vp]
+        f32 = C.c_float
+        L.qh_rmsnorm.argtypes = [vp, vp, sz, vp, sz, f32, vp]
+        L.qh_rmsnorm_dev.argtypes = [vp, vp, vp, sz, sz, f32, vp, vp]
+        L.qh_rmsnorm_backward.argtypes = [vp, vp, sz, vp, sz, vp, sz, f32, vp, vp]
+        L.qh_rmsnorm_backward_dev.argtypes = [vp, vp, vp, vp, sz, sz, f32, vp, vp, vp]
+        L.qh_swiglu.argtypes = [vp, vp, sz, vp, sz, vp]
+        L.qh_swiglu_dev.argtypes = [vp, vp, vp, sz, vp, vp]
+        L.qh_swiglu_backward.argtypes = [vp, vp, vp, vp, sz, vp, vp]
+        L.qh_swiglu_backward_dev.argtypes = [vp, vp, vp, vp, sz, vp, vp, vp]
+        L.qh_softmax_cross_entropy.argtypes = [vp, vp, sz, vp, sz, sz, vp, vp]
+        L.qh_softmax_cross_entropy_dev.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         _lib = L
         return L
 

@@ -142,3 +142,78 @@ def backward(w: DeviceWeight, lora, x: torch.Tensor, dy: torch.Tensor, batch: in
     check(ctx.lib.qh_qlora_backward_dev(
         ctx.h, C.byref(s), None if lora is None else C.byref(lora), _p(x), _p(dy),
         _dt(x), batch, _p(t1), _p(gx), _p(ga), _p(gb), C.c_void_p(_stream())))
+
+
+# ---- the glue of a decoder block (qlora-model/src/llama.rs) ------------------
+def _f32c(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise TypeError(f"{what} must be a contiguous float32 tensor")
+    return t
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float,
+            out: Optional[torch.Tensor] = None, ctx=None) -> torch.Tensor:
+    """rmsnorm_in_place (llama.rs:730-739) over the last dimension of x;
+    ``out`` may be ``x`` itself."""
+    ctx = ctx or default_context()
+    _f32c(x, "x"), _f32c(w, "w")
+    h = w.numel()
+    out = torch.empty_like(x) if out is None else _f32c(out, "out")
+    check(ctx.lib.qh_rmsnorm_dev(ctx.h, _p(x), _p(w), x.numel() // max(h, 1), h, eps,
+                                 _p(out), C.c_void_p(_stream())))
+    return out
+
+
+def rmsnorm_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, eps: float,
+                     want_dw: bool = True, ctx=None):
+    """rmsnorm_backward (llama.rs:605-631) -> (dx, dw or None)."""
+    ctx = ctx or default_context()
+    for t, n in ((x, "x"), (w, "w"), (dy, "dy")):
+        _f32c(t, n)
+    h = w.numel()
+    dx = torch.empty_like(x)
+    dw = torch.empty(h, dtype=torch.float32, device=x.device) if want_dw else None
+    check(ctx.lib.qh_rmsnorm_backward_dev(ctx.h, _p(x), _p(w), _p(dy), x.numel() // max(h, 1),
+                                          h, eps, _p(dx), _p(dw), C.c_void_p(_stream())))
+    return dx, dw
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = None,
+           ctx=None) -> torch.Tensor:
+    """act = silu(gate) * up (llama.rs:452-456)."""
+    ctx = ctx or default_context()
+    _f32c(gate, "gate"), _f32c(up, "up")
+    if gate.numel() != up.numel():
+        raise ValueError("gate and up differ in size")
+    out = torch.empty_like(gate) if out is None else _f32c(out, "out")
+    check(ctx.lib.qh_swiglu_dev(ctx.h, _p(gate), _p(up), gate.numel(), _p(out),
+                                C.c_void_p(_stream())))
+    return out
+
+
+def swiglu_backward(gate: torch.Tensor, up: torch.Tensor, d_act: torch.Tensor, ctx=None):
+    """(d_gate, d_up) of act = silu(gate) * up (llama.rs:546-551)."""
+    ctx = ctx or default_context()
+    for t, n in ((gate, "gate"), (up, "up"), (d_act, "d_act")):
+        _f32c(t, n)
+    dg, du = torch.empty_like(gate), torch.empty_like(up)
+    check(ctx.lib.qh_swiglu_backward_dev(ctx.h, _p(gate), _p(up), _p(d_act), gate.numel(),
+                                         _p(dg), _p(du), C.c_void_p(_stream())))
+    return dg, du
+
+
+def softmax_cross_entropy(logits: torch.Tensor, targets: torch.Tensor,
+                          dlogits: Optional[torch.Tensor] = None, ctx=None):
+    """softmax_cross_entropy (llama.rs:487-514) of (seq, vocab) logits and
+    int32 targets -> (loss tensor of one float, dlogits).  ``dlogits`` may be
+    ``logits`` itself."""
+    ctx = ctx or default_context()
+    _f32c(logits, "logits")
+    if targets.dtype != torch.int32 or not targets.is_contiguous():
+        raise TypeError("targets must be a contiguous int32 tensor")
+    seq, vocab = logits.shape
+    d = torch.empty_like(logits) if dlogits is None else _f32c(dlogits, "dlogits")
+    loss = torch.empty(1, dtype=torch.float32, device=logits.device)
+    check(ctx.lib.qh_softmax_cross_entropy_dev(ctx.h, _p(logits), _p(targets), seq, vocab,
+                                               _p(loss), _p(d), C.c_void_p(_stream())))
+    return loss, d
