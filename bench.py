@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-extra", action="store_true",
                     help="skip configurations 1, 4, 5 and C3's 14336x4096 layer")
+    ap.add_argument("--skip-glue", action="store_true",
+                    help="skip the RMSNorm / SwiGLU / cross-entropy measurements")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload")
     ap.add_argument("--probe", action="store_true",
@@ -466,6 +468,94 @@ def extra_bench(args, ctx, torch, dev, QD):
     return out
 
 
+def glue_bench(args, ctx, torch, dev, QD):
+    """The block glue around the projections (llama.rs: RMSNorm, SwiGLU,
+    softmax cross-entropy) at two model scales, 2048 tokens: SmolLM-135M
+    (hidden 576, MLP 1536, vocab 49152; C4's block) and a 70B-class block
+    (hidden 8192, MLP 28672, vocab 128256; C5's layers).  Inputs rotate over
+    enough copies that each call misses the 256 MB MALL; the calls over all
+    copies are captured once as a HIP graph and replayed, so host launch
+    cost stays out (each replay is checked against the eager outputs first).
+    Time per call is between GPU events around the replays; bytes are
+    algorithmic (each input read once, each output written once)."""
+    import ctypes as C
+    g = torch.Generator(device="cuda").manual_seed(0x5151)
+    out = {}
+    T = 2048
+    st = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    L = ctx.lib
+    for name, H, I, V in (("smollm135m", 576, 1536, 49152), ("70b", 8192, 28672, 128256)):
+        res = {}
+
+        def run(op, ws_bytes, make, call, n_out, nbytes, calls=20):
+            copies = max(1, -(-512_000_000 // ws_bytes))
+            sets = [make() for _ in range(copies)]
+
+            def all_calls():
+                for t in sets:
+                    call(*t)
+            all_calls()
+            torch.cuda.synchronize()
+            ref = [[x.clone() for x in t[-n_out:]] for t in sets]
+            gr = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                call(*sets[0])
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(gr):
+                all_calls()
+            for _ in range(2):
+                gr.replay()
+                torch.cuda.synchronize()
+                for t, rr in zip(sets, ref):
+                    for x, y in zip(t[-n_out:], rr):
+                        assert torch.equal(x, y), f"{op}: graph replay differs from eager run"
+            reps = max(2, -(-calls // copies))
+            gr.replay()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / (reps * copies)
+            res[op] = dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e6),
+                           frac_hbm=nbytes / (ms * 1e6) / HBM_PEAK_GBS, copies=copies)
+            del sets, ref, gr
+            torch.cuda.empty_cache()
+
+        w = torch.rand(H, device=dev, generator=g) + 0.5
+        rn = lambda *s: torch.randn(*s, device=dev, generator=g)  # noqa: E731
+        em = lambda *s: torch.empty(*s, device=dev)  # noqa: E731
+        run("rmsnorm", T * H * 8, lambda: (rn(T, H), em(T, H)),
+            lambda x, y: QD.rmsnorm(x, w, 1e-5, out=y, ctx=ctx), 1, T * H * 8 + H * 4)
+        run("rmsnorm_backward_dx", T * H * 12, lambda: (rn(T, H), rn(T, H), em(T, H)),
+            lambda x, dy, dx: QD.check(L.qh_rmsnorm_backward_dev(
+                ctx.h, QD._p(x), QD._p(w), QD._p(dy), T, H, 1e-5, QD._p(dx), None, st())),
+            1, T * H * 12 + H * 4)
+        run("swiglu", T * I * 12, lambda: (rn(T, I), rn(T, I), em(T, I)),
+            lambda a, b, o: QD.swiglu(a, b, out=o, ctx=ctx), 1, T * I * 12)
+        run("swiglu_backward", T * I * 20,
+            lambda: (rn(T, I), rn(T, I), rn(T, I), em(T, I), em(T, I)),
+            lambda a, b, d, dg, du: QD.check(L.qh_swiglu_backward_dev(
+                ctx.h, QD._p(a), QD._p(b), QD._p(d), T * I, QD._p(dg), QD._p(du), st())),
+            2, T * I * 20)
+        tg = torch.randint(0, V, (T,), device=dev, generator=g, dtype=torch.int32)
+        run("softmax_cross_entropy", T * V * 8,
+            lambda: (rn(T, V) * 3, em(1), em(T, V)),
+            lambda lg, loss, d: QD.check(L.qh_softmax_cross_entropy_dev(
+                ctx.h, QD._p(lg), QD._p(tg), T, V, QD._p(loss), QD._p(d), st())),
+            2, T * V * 8 + T * 4 + 4, calls=5)
+        out[name] = dict(tokens=T, hidden=H, mlp=I, vocab=V, ops=res)
+        print(f"# glue {name}: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in res.items()),
+              file=sys.stderr, flush=True)
+    return out
+
+
 def cpu_baseline_c1():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -590,6 +680,9 @@ def main():
     if not args.skip_extra:
         extra = extra_bench(args, ctx, torch, dev, QD)
         print(f"# extra configs done: {sorted(extra)}", file=sys.stderr, flush=True)
+    glue = None
+    if not args.skip_glue:
+        glue = glue_bench(args, ctx, torch, dev, QD)
     cpu_dec = cpu_pre = None
     if not args.no_cpu_baseline:
         cpu_dec = cpu_baseline_decode(args.cpu_seconds)
@@ -638,6 +731,7 @@ def main():
         "decode_host_path": dec_cfg["host_path"],
         "prefill": prefill,
         "configs": extra,
+        "block_glue": glue,
     }
     print(json.dumps(line))
 

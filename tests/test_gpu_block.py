@@ -200,7 +200,10 @@ def test_swiglu_host_slices_in_place(QD, ctx):
     _close(tu, rdu, "in-place du")
 
 
-CE_SHAPES = [(64, 49152), (16, 32000), (4, 128256), (5, 1001), (3, 1), (1, 7), (300, 64)]
+# rows in registers (49152, 32000, ...), rows past the register cache read
+# in a streaming pass (128256; 50001 on the scalar path)
+CE_SHAPES = [(64, 49152), (16, 32000), (4, 128256), (3, 50001), (5, 1001), (3, 1), (1, 7),
+             (300, 64)]
 
 
 @pytest.mark.parametrize("seq,vocab", CE_SHAPES)
@@ -261,3 +264,24 @@ def test_softmax_ce_edges(QD, ctx):
     assert abs(float(row0.sum()) - 1.0 / 2) < 1e-5 and np.all(row0 >= 0)
     _, rd2 = O.softmax_cross_entropy(logits[: 2 * vocab], np.array([0, 1], np.uint32), 2, vocab)
     _close(bd[1], rd2[vocab:], "row with a valid target", TOL_CE_ORACLE)
+
+
+def test_softmax_ce_masked_logits(QD, ctx):
+    """-inf logits (a masked vocabulary), in the register part and in the
+    streamed part of a long row: they get zero probability, like exp(-inf)
+    in llama.rs:500."""
+    seq, vocab = 3, 128256
+    g = O.Rng(21)
+    logits = g.normal(seq * vocab, 2.0).reshape(seq, vocab)
+    logits[0, :60000] = -np.inf        # register part and beyond
+    logits[1, 50000:] = -np.inf        # streamed part only
+    logits[2, ::3] = -np.inf
+    targets = np.array([70000, 7, 1], np.uint32)
+    logits = logits.ravel()
+    rloss, rd = O.softmax_cross_entropy(logits, targets, seq, vocab)
+    loss, d = QD.softmax_cross_entropy(_dev(logits).view(seq, vocab),
+                                       _dev(targets.view(np.int32)), ctx=ctx)
+    torch.cuda.synchronize()
+    _check_loss(loss.item(), rloss, logits, targets, seq, vocab)
+    _close(d, rd, "masked dlogits", TOL_CE_ORACLE)
+    assert torch.count_nonzero(d[0, :60000]).item() == 0

@@ -8,6 +8,8 @@
 // and every cross-row sum runs in a fixed order so results repeat bit for bit.
 #include <math.h>
 
+#include <type_traits>
+
 #include "qh_internal.h"
 
 namespace qh {
@@ -161,6 +163,128 @@ __global__ __launch_bounds__(kBlock) void k_colsum(const float *__restrict__ par
   out[j] = acc;
 }
 
+// Register-resident rows (h % 4 == 0, 16-byte aligned rows): TPR threads
+// share a row and thread t holds its float4 chunks c * TPR + t (c < CH), all
+// loaded before the first use, so a row is read from HBM once and the loads
+// of a wave are all in flight together.  A workgroup holds 256 / TPR rows;
+// rows of several waves reduce their wave sums through LDS in wave order.
+template <int TPR>
+__device__ __forceinline__ float row_sum(float v, float *red) {
+  v = wave_sum(v);
+  if (TPR == 64) return v;
+  constexpr int NW = TPR / 64;
+  const int wv = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wv] = v;
+  __syncthreads();
+  const int w0 = wv / NW * NW;
+  float s = red[w0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) s += red[w0 + k];
+  return s;
+}
+
+template <int TPR, int CH>
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_reg(const float *x, const float *__restrict__ w,
+                                                        float *y, int64_t rows, int h, float eps) {
+  __shared__ float red[kBlock / 64];
+  const int sub = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / TPR) + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const int h4 = h >> 2;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (live ? row : 0) * h);
+  float4 v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = c * TPR + sub;
+    v[c] = (live && q < h4) ? xr[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    acc += v[c].x * v[c].x;
+    acc += v[c].y * v[c].y;
+    acc += v[c].z * v[c].z;
+    acc += v[c].w * v[c].w;
+  }
+  const float mean_sq = row_sum<TPR>(acc, red) / (float)h;
+  const float scale = 1.0f / sqrtf(mean_sq + eps);
+  if (!live) return;
+  float4 *yr = reinterpret_cast<float4 *>(y + row * h);
+  const float4 *wr = reinterpret_cast<const float4 *>(w);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = c * TPR + sub;
+    if (q < h4) {
+      const float4 g = wr[q];
+      float4 o;
+      o.x = v[c].x * scale * g.x;
+      o.y = v[c].y * scale * g.y;
+      o.z = v[c].z * scale * g.z;
+      o.w = v[c].w * scale * g.w;
+      yr[q] = o;
+    }
+  }
+}
+
+template <int TPR, int CH>
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_bwd_reg(const float *__restrict__ x,
+                                                            const float *__restrict__ w,
+                                                            const float *dy, float *dx,
+                                                            float *__restrict__ rstd,
+                                                            int64_t rows, int h, float eps) {
+  __shared__ float red[2][kBlock / 64];
+  const int sub = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * (kBlock / TPR) + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const int h4 = h >> 2;
+  const int64_t off = (live ? row : 0) * h;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + off);
+  const float4 *gr = reinterpret_cast<const float4 *>(dy + off);
+  const float4 *wr = reinterpret_cast<const float4 *>(w);
+  float4 v[CH], g[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = c * TPR + sub;
+    const bool in = live && q < h4;
+    v[c] = in ? xr[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    g[c] = in ? gr[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = c * TPR + sub;
+    const float4 k = q < h4 ? wr[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    s1 += v[c].x * v[c].x;
+    s1 += v[c].y * v[c].y;
+    s1 += v[c].z * v[c].z;
+    s1 += v[c].w * v[c].w;
+    s2 += g[c].x * v[c].x * k.x;
+    s2 += g[c].y * v[c].y * k.y;
+    s2 += g[c].z * v[c].z * k.z;
+    s2 += g[c].w * v[c].w * k.w;
+  }
+  const float ss = row_sum<TPR>(s1, red[0]) / (float)h + eps;
+  const float r = 1.0f / sqrtf(ss);
+  const float ds = row_sum<TPR>(s2, red[1]) * (-0.5f * (1.0f / ss) * r);
+  if (!live) return;
+  if (rstd != nullptr && sub == 0) rstd[row] = r;
+  const float fh = (float)h;
+  float4 *dr = reinterpret_cast<float4 *>(dx + row * h);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = c * TPR + sub;
+    if (q < h4) {
+      const float4 k = wr[q];
+      float4 o;
+      o.x = g[c].x * k.x * r + 2.0f * v[c].x / fh * ds;
+      o.y = g[c].y * k.y * r + 2.0f * v[c].y / fh * ds;
+      o.z = g[c].z * k.z * r + 2.0f * v[c].z / fh * ds;
+      o.w = g[c].w * k.w * r + 2.0f * v[c].w / fh * ds;
+      dr[q] = o;
+    }
+  }
+}
+
 // ---- SwiGLU (llama.rs:452-456, 516-529, 546-551) ------------------------------
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
@@ -234,13 +358,14 @@ __global__ __launch_bounds__(kBlock) void k_swiglu_bwd(const float *gate, const 
 // ---- softmax cross-entropy (llama.rs:487-514) ---------------------------------
 // One workgroup of 1024 threads per row.  Each thread holds up to CH float4
 // chunks of the row in registers (chunk c of thread t covers float4 index
-// c * 1024 + t); the rest of the row, if any, is streamed again in each pass.
-// Pass 1: the row max; pass 2: sum of exp(v - max); pass 3: dlogits =
-// exp(v - max) / sum / seq, minus 1/seq at the target.  terms[row] receives
+// c * 1024 + t).  Pass 1: the row max; pass 2: sum of exp(v - max); pass 3:
+// dlogits = exp(v - max) / sum / seq, minus 1/seq at the target.  A row
+// longer than the cache (STREAM) reads its remainder twice: once for a
+// running max and sum (folded into pass 1) and once to write it.  terms[row] receives
 // (logit[target] - max - ln(sum)) / seq; the loss is -sum(terms) (k_loss).
 // dlogits may alias logits: every read of the row precedes the first
 // barrier after it, and each element is written by the thread that read it.
-template <int CH, bool V4>
+template <int CH, bool V4, bool STREAM>
 __global__ __launch_bounds__(kCeBlock) void k_softmax_ce(const float *logits,
                                                          const uint32_t *__restrict__ targets,
                                                          int64_t vocab, float fseq,
@@ -280,14 +405,36 @@ __global__ __launch_bounds__(kCeBlock) void k_softmax_ce(const float *logits,
       for (int e = 0; e < E; ++e) mx = fmaxf(mx, cache[c][e]);
     }
   }
+  const bool has_tail = V4 && tid < (vocab & 3);
+  const float tail = has_tail ? lr[(nv << 2) + tid] : 0.0f;
+  // STREAM: the part of the row past the register cache (and the tail) in
+  // one online pass: running max m_s and sum s_s of exp(v - m_s)
+  float m_s = -INFINITY, s_s = 0.0f;
+  auto online = [&](float m4, const float *v, int cnt) {
+    if (m4 > m_s) {
+      s_s = s_s * expf(m_s - m4);
+      m_s = m4;
+    }
+    for (int e = 0; e < cnt; ++e) s_s += m_s == -INFINITY ? 0.0f : expf(v[e] - m_s);
+  };
   for (int64_t q = (int64_t)CH * kCeBlock + tid; q < nv; q += kCeBlock) {
     float v[E];
     load(q, v);
+    float m4 = v[0];
 #pragma unroll
-    for (int e = 0; e < E; ++e) mx = fmaxf(mx, v[e]);
+    for (int e = 1; e < E; ++e) m4 = fmaxf(m4, v[e]);
+    if (STREAM)
+      online(m4, v, E);
+    else
+      mx = fmaxf(mx, m4);
   }
-  if (V4 && tid < (vocab & 3)) mx = fmaxf(mx, lr[(nv << 2) + tid]);
-  mx = wave_max(mx);
+  if (has_tail) {
+    if (STREAM)
+      online(tail, &tail, 1);
+    else
+      mx = fmaxf(mx, tail);
+  }
+  mx = wave_max(fmaxf(mx, m_s));
   if (lane == 0) red[wv] = mx;
   __syncthreads();
   mx = red[0];
@@ -295,6 +442,8 @@ __global__ __launch_bounds__(kCeBlock) void k_softmax_ce(const float *logits,
   for (int k = 1; k < kCeBlock / 64; ++k) mx = fmaxf(mx, red[k]);
   __syncthreads();
 
+  // sum of exp(v - max): cached values exactly as the reference forms them,
+  // the streamed part rescaled from its running max
   float sum = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -304,16 +453,16 @@ __global__ __launch_bounds__(kCeBlock) void k_softmax_ce(const float *logits,
       for (int e = 0; e < E; ++e) sum += expf(cache[c][e] - mx);
     }
   }
-  for (int64_t q = (int64_t)CH * kCeBlock + tid; q < nv; q += kCeBlock) {
-    float v[E];
-    load(q, v);
+  if (STREAM) {
+    if (m_s != -INFINITY) sum += s_s * expf(m_s - mx);
+  } else {
+    for (int64_t q = (int64_t)CH * kCeBlock + tid; q < nv; q += kCeBlock) {
+      float v[E];
+      load(q, v);
 #pragma unroll
-    for (int e = 0; e < E; ++e) sum += expf(v[e] - mx);
-  }
-  float tail = 0.0f;
-  if (V4 && tid < (vocab & 3)) {
-    tail = lr[(nv << 2) + tid];
-    sum += expf(tail - mx);
+      for (int e = 0; e < E; ++e) sum += expf(v[e] - mx);
+    }
+    if (has_tail) sum += expf(tail - mx);
   }
   sum = wave_sum(sum);
   if (lane == 0) red[wv] = sum;
@@ -365,7 +514,7 @@ __global__ __launch_bounds__(kCeBlock) void k_softmax_ce(const float *logits,
       dr[q] = grad(v[0], q);
     }
   }
-  if (V4 && tid < (vocab & 3)) dr[(nv << 2) + tid] = grad(tail, (nv << 2) + tid);
+  if (has_tail) dr[(nv << 2) + tid] = grad(tail, (nv << 2) + tid);
   if (tid == 0) terms[row] = tgt_ok ? (xt - mx - logf(sum)) / fseq : NAN;
 }
 
@@ -390,14 +539,66 @@ inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 inline unsigned grid_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
 
+// Register-resident shape for a row of h floats: threads per row and float4
+// chunks per thread (TPR 64 up to h = 1024, 128 up to 2048, 256 up to 8192);
+// 0 when the row does not fit (then the streaming kernels run).
+struct RegShape {
+  int tpr = 0, ch = 0;
+};
+
+RegShape reg_shape(int h) {
+  RegShape r;
+  const int h4 = h / 4;
+  r.tpr = h4 <= 256 ? 64 : (h4 <= 512 ? 128 : (h4 <= 2048 ? 256 : 0));
+  if (!r.tpr) return r;
+  const int ch = (h4 + r.tpr - 1) / r.tpr;
+  r.ch = ch <= 4 ? ch : (ch <= 6 ? 6 : 8);
+  return r;
+}
+
+template <int TPR, int CH>
+hipError_t launch_rms_reg(const float *x, const float *w, float *y, int64_t rows, int h, float eps,
+                          hipStream_t s) {
+  return qh_launch(k_rmsnorm_reg<TPR, CH>, dim3(grid_for(rows, kBlock / TPR)), dim3(kBlock), 0,
+                   s, x, w, y, rows, h, eps);
+}
+
+template <int TPR, int CH>
+hipError_t launch_rms_bwd_reg(const float *x, const float *w, const float *dy, float *dx,
+                              float *rstd, int64_t rows, int h, float eps, hipStream_t s) {
+  return qh_launch(k_rmsnorm_bwd_reg<TPR, CH>, dim3(grid_for(rows, kBlock / TPR)), dim3(kBlock),
+                   0, s, x, w, dy, dx, rstd, rows, h, eps);
+}
+
+// Calls F<TPR, CH> for the register shape, or returns false.
+template <class F>
+bool with_reg_shape(RegShape r, F &&f) {
+#define QH_RS(T, C)                                          \
+  if (r.tpr == T && r.ch == C) {                            \
+    f(std::integral_constant<int, T>(), std::integral_constant<int, C>()); \
+    return true;                                             \
+  }
+  QH_RS(64, 1) QH_RS(64, 2) QH_RS(64, 3) QH_RS(64, 4)
+  QH_RS(128, 3) QH_RS(128, 4)
+  QH_RS(256, 3) QH_RS(256, 4) QH_RS(256, 6) QH_RS(256, 8)
+#undef QH_RS
+  return false;
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int64_t rows, int h,
                           float eps, hipStream_t s) {
   if (rows == 0 || h == 0) return hipSuccess;
   const unsigned g = grid_for(rows, kBlock / 64);
-  if (h % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y))
+  if (h % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y)) {
+    hipError_t e = hipSuccess;
+    if (with_reg_shape(reg_shape(h), [&](auto T, auto C) {
+          e = launch_rms_reg<decltype(T)::value, decltype(C)::value>(x, w, y, rows, h, eps, s);
+        }))
+      return e;
     return qh_launch(k_rmsnorm<true>, dim3(g), dim3(kBlock), 0, s, x, w, y, rows, h, eps);
+  }
   return qh_launch(k_rmsnorm<false>, dim3(g), dim3(kBlock), 0, s, x, w, y, rows, h, eps);
 }
 
@@ -420,7 +621,13 @@ hipError_t launch_rmsnorm_bwd(const float *x, const float *w, const float *dy, f
   if (rows > 0) {
     const unsigned g = grid_for(rows, kBlock / 64);
     hipError_t e;
-    if (h % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx))
+    const bool v4 = h % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
+    if (v4 && with_reg_shape(reg_shape(h), [&](auto T, auto C) {
+          e = launch_rms_bwd_reg<decltype(T)::value, decltype(C)::value>(x, w, dy, dx, rstd, rows,
+                                                                         h, eps, s);
+        }))
+      ;
+    else if (v4)
       e = qh_launch(k_rmsnorm_bwd<true>, dim3(g), dim3(kBlock), 0, s, x, w, dy, dx, rstd,
                     rows, h, eps);
     else
@@ -469,19 +676,21 @@ hipError_t launch_softmax_ce(const float *logits, const uint32_t *targets, int64
     const int64_t per = (nv + kCeBlock - 1) / kCeBlock;  // vectors per thread
     const dim3 g((unsigned)seq), b(kCeBlock);
     hipError_t e;
-#define QH_CE(CHV)                                                                              \
-  (v4 ? qh_launch(k_softmax_ce<CHV, true>, g, b, 0, s, logits, targets, vocab, fseq, dlogits,  \
-                  terms)                                                                       \
-      : qh_launch(k_softmax_ce<CHV, false>, g, b, 0, s, logits, targets, vocab, fseq, dlogits, \
-                  terms))
+#define QH_CE(CHV, ST)                                                                          \
+  (v4 ? qh_launch(k_softmax_ce<CHV, true, ST>, g, b, 0, s, logits, targets, vocab, fseq,       \
+                  dlogits, terms)                                                              \
+      : qh_launch(k_softmax_ce<CHV, false, ST>, g, b, 0, s, logits, targets, vocab, fseq,      \
+                  dlogits, terms))
     // 12 float4 per thread (48 values, 108 VGPRs) is the most that stays
-    // out of scratch at 1024 threads; longer rows stream the rest each pass
+    // out of scratch at 1024 threads; longer rows stream the rest
     if (per <= 4)
-      e = QH_CE(4);
+      e = QH_CE(4, false);
     else if (per <= 8)
-      e = QH_CE(8);
+      e = QH_CE(8, false);
+    else if (per <= 12)
+      e = QH_CE(12, false);
     else
-      e = QH_CE(12);
+      e = QH_CE(12, true);
 #undef QH_CE
     if (e != hipSuccess) return e;
   }
