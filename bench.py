@@ -556,6 +556,60 @@ def glue_bench(args, ctx, torch, dev, QD):
     return out
 
 
+def load_bench(args, ctx, torch, dev, QD):
+    """Weights into HBM from the host, C5's 28672x8192 layer: the packed
+    NF4 file image (pinned host memory, parsed and copied part by part into
+    HBM) against the fp32 path (pinned fp32 weights copied to HBM, then
+    quantized there).  Host-to-device copies bound both; the packed path
+    moves 0.5157 B per weight instead of 4."""
+    import numpy as np
+    import qlora_hip as QH
+    N, K = 28672, 8192
+    g = torch.Generator(device="cuda").manual_seed(0x10AD)
+    w = torch.randn(N, K, device=dev, generator=g) * 0.02
+    W = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+    host = dict(rows=N, cols=K, block_size=64, n=N * K, codes=W.codes.cpu().numpy(),
+                scale_codes=W.scale_codes.cpu().numpy(), absmax=W.absmax.cpu().numpy())
+    img = QH.nf4_file_bytes({"w": host})
+    pinned = torch.empty(len(img), dtype=torch.uint8, pin_memory=True)
+    pinned.numpy()[:] = np.frombuffer(img, np.uint8)
+    w_host = torch.empty(N, K, dtype=torch.float32, pin_memory=True)
+    w_host.copy_(w)
+    del w
+    torch.cuda.empty_cache()
+
+    def packed():
+        return QD.load_nf4(pinned, device=dev, ctx=ctx)["w"]
+
+    def fp32():
+        wd = w_host.to(dev, non_blocking=True)
+        q = QD.DeviceWeight.quantize(wd, 64, True, ctx=ctx)
+        torch.cuda.current_stream().synchronize()
+        return q
+
+    out = {}
+    for name, fn, nbytes in (("packed_file", packed, len(img)), ("fp32_then_quantize", fp32,
+                                                                  N * K * 4)):
+        fn()
+        torch.cuda.synchronize()
+        reps = 5
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            q = fn()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / reps * 1e3
+        out[name] = dict(ms=ms, host_bytes=nbytes, gbs=nbytes / (ms * 1e6))
+        assert torch.equal(q.codes, W.codes) and torch.equal(q.scale_codes, W.scale_codes)
+        del q
+    out["speedup"] = out["fp32_then_quantize"]["ms"] / out["packed_file"]["ms"]
+    out["workload"] = f"{N}x{K} NF4 (block 64, double quant) from host memory into HBM"
+    print(f"# load {N}x{K}: packed {out['packed_file']['ms']:.2f} ms, fp32+quantize "
+          f"{out['fp32_then_quantize']['ms']:.2f} ms", file=sys.stderr, flush=True)
+    del pinned, w_host, W
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline_c1():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -683,6 +737,7 @@ def main():
     glue = None
     if not args.skip_glue:
         glue = glue_bench(args, ctx, torch, dev, QD)
+    load = None if args.skip_extra else load_bench(args, ctx, torch, dev, QD)
     cpu_dec = cpu_pre = None
     if not args.no_cpu_baseline:
         cpu_dec = cpu_baseline_decode(args.cpu_seconds)
@@ -732,6 +787,7 @@ def main():
         "prefill": prefill,
         "configs": extra,
         "block_glue": glue,
+        "weight_load": load,
     }
     print(json.dumps(line))
 

@@ -45,7 +45,9 @@ typedef enum qh_status {
   QH_ERR_SHAPE_MISMATCH = 1, /* QloraError::ShapeMismatch (error.rs:8) */
   QH_ERR_INVALID_CONFIG = 2, /* QloraError::InvalidConfig (error.rs:10) */
   QH_ERR_GPU = 3,            /* QloraError::Gpu (error.rs:12) */
-  QH_NO_DEVICE = 4 /* try_new_blocking() -> Ok(None) (context.rs:50-53) */
+  QH_NO_DEVICE = 4, /* try_new_blocking() -> Ok(None) (context.rs:50-53) */
+  QH_ERR_MALFORMED = 5,  /* qlora-io IoError::Malformed (qlora-io/src/error.rs:8) */
+  QH_ERR_UNSUPPORTED = 6 /* qlora-io IoError::Unsupported (error.rs:10) */
 } qh_status;
 
 /* Scale storage of a quantized weight: `ScaleStore` (quant.rs:84-89). */
@@ -291,6 +293,43 @@ QH_API qh_status qh_softmax_cross_entropy_dev(qh_ctx *ctx,
                                               size_t seq, size_t vocab,
                                               float *d_loss, float *d_dlogits,
                                               void *stream);
+
+/* ---- packed NF4 files -----------------------------------------------------
+ * No counterpart in the reference: its quantized weights leave `quantize`
+ * only as fp32 (QuantizedWeight.scales, qlora-python/src/lib.rs:101) and
+ * qlora-io writes and reads fp32 tensors (npz.rs:46, safetensors.rs:25).  A
+ * safetensors file holding, per weight <name>, "<name>.nf4_codes" (U8),
+ * then "<name>.nf4_scale_codes" (U8, the int8 codes bit-cast) and
+ * "<name>.nf4_absmax" (F32), or "<name>.nf4_scales" (F32), plus
+ * "__metadata__" {"format": "qlora-hip-nf4/1", "<name>": "rows,cols,bs"}.
+ * Readers that convert every tensor to fp32 (qlora-io's read_safetensors)
+ * still parse it.  Malformed files return QH_ERR_MALFORMED, other dtypes
+ * QH_ERR_UNSUPPORTED, part lengths that disagree with the shape
+ * QH_ERR_SHAPE_MISMATCH (the from_raw_parts rule, quant.rs:170-197). */
+/* File size for `count` host-resident weights named names[i]. */
+QH_API qh_status qh_nf4_file_size(const qh_qweight *ws, const char *const *names,
+                                  size_t count, size_t *bytes);
+/* Write the file into buf (buf_len must equal qh_nf4_file_size's bytes). */
+QH_API qh_status qh_nf4_file_write(const qh_qweight *ws, const char *const *names,
+                                   size_t count, uint8_t *buf, size_t buf_len);
+/* Number of weights in a file image. */
+QH_API qh_status qh_nf4_file_count(const uint8_t *buf, size_t len,
+                                   size_t *count);
+/* Weight `index` (file order): its name and a view whose pointers point
+ * into buf (no copy). */
+QH_API qh_status qh_nf4_file_entry(const uint8_t *buf, size_t len,
+                                   size_t index, char *name, size_t name_len,
+                                   qh_qweight *view);
+QH_API qh_status qh_nf4_file_find(const uint8_t *buf, size_t len,
+                                  const char *name, qh_qweight *view);
+/* Copy a host-resident weight (e.g. a view into a file image) into device
+ * buffers of its part sizes, on `stream` (asynchronous for pinned host
+ * memory): the packed form loads straight into HBM, no fp32 and no
+ * quantize on the way. */
+QH_API qh_status qh_weight_upload_dev(qh_ctx *ctx, const qh_qweight *w,
+                                      uint8_t *d_codes, float *d_scales,
+                                      uint8_t *d_scale_codes, float *d_absmax,
+                                      void *stream);
 
 #ifdef __cplusplus
 }

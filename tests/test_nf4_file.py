@@ -1,0 +1,147 @@
+"""The packed NF4 file (safetensors) entry points, on the CPU: bit-exact
+round trips of both scale stores, interchange with the independent
+`safetensors` implementation in both directions, and the error paths
+(malformed images, unsupported dtypes, part lengths that disagree with the
+weight's shape).  No GPU is involved: the format code is host-only.
+"""
+import ctypes as C
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import oracle as O
+import qlora_hip as QH
+from qlora_hip import _lib
+
+safetensors_np = pytest.importorskip("safetensors.numpy")
+
+
+def _q(rows, cols, seed, block_size=64, dq=True):
+    w = O.Rng(seed).normal(rows * cols, 0.02)
+    q = O.quantize(w, block_size, dq)
+    q.update(rows=rows, cols=cols)
+    return q
+
+
+def _same(a, b):
+    assert a["rows"] == b["rows"] and a["cols"] == b["cols"]
+    assert a["block_size"] == b["block_size"]
+    for k in ("codes", "scale_codes", "absmax", "scales"):
+        assert (k in a) == (k in b), k
+        if k in a:
+            assert a[k].dtype == b[k].dtype and np.array_equal(
+                a[k].view(np.uint8), b[k].view(np.uint8)), k
+
+
+def test_round_trip_both_stores():
+    ws = {"layers.0.mlp.down": _q(3, 67, 1),              # odd n, ragged block
+          "q_proj": _q(5, 64, 2, dq=False),                # fp32 scales
+          "big": _q(64, 1040, 3, block_size=32),           # > 256 blocks: 2 absmax
+          'we"ird é name': _q(1, 1, 4)}
+    img = QH.nf4_file_bytes(ws)
+    # the header is padded so the tensor data starts 8-byte aligned
+    assert int.from_bytes(img[:8], "little") % 8 == 0
+    back = QH.load_nf4(img)
+    assert list(back) == list(ws)
+    for k in ws:
+        _same(ws[k], back[k])
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "w.safetensors")
+        assert QH.save_nf4(p, ws) == len(img)
+        for k, q in QH.load_nf4(p).items():
+            _same(ws[k], q)
+
+
+def test_read_by_the_safetensors_library():
+    ws = {"w": _q(3, 67, 5), "s": _q(2, 64, 6, dq=False)}
+    img = QH.nf4_file_bytes(ws)
+    t = safetensors_np.load(img)
+    assert set(t) == {"w.nf4_codes", "w.nf4_scale_codes", "w.nf4_absmax", "s.nf4_codes",
+                      "s.nf4_scales"}
+    assert t["w.nf4_codes"].dtype == np.uint8 and np.array_equal(t["w.nf4_codes"],
+                                                                 ws["w"]["codes"])
+    assert np.array_equal(t["w.nf4_scale_codes"], ws["w"]["scale_codes"])
+    assert np.array_equal(t["w.nf4_absmax"].view(np.uint32), ws["w"]["absmax"].view(np.uint32))
+    assert np.array_equal(t["s.nf4_scales"].view(np.uint32), ws["s"]["scales"].view(np.uint32))
+    from safetensors import safe_open
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "w.safetensors")
+        QH.save_nf4(p, ws)
+        with safe_open(p, "np") as f:
+            md = f.metadata()
+    assert md == {"format": "qlora-hip-nf4/1", "w": "3,67,64", "s": "2,64,64"}
+
+
+def test_written_by_the_safetensors_library():
+    q = _q(7, 100, 7)
+    tensors = {"x.nf4_codes": q["codes"], "x.nf4_scale_codes": q["scale_codes"],
+               "x.nf4_absmax": q["absmax"], "unrelated": np.ones(3, np.float32)}
+    img = safetensors_np.save(tensors, metadata={"x": "7,100,64", "note": "hello"})
+    back = QH.load_nf4(img)
+    assert list(back) == ["x"]
+    _same(q, back["x"])
+
+
+def _find(img, name="w"):
+    L = _lib.load()
+    buf = np.frombuffer(img, np.uint8).copy()
+    v = _lib.QWeight()
+    st = L.qh_nf4_file_find(buf.ctypes.data_as(C.c_void_p), buf.size, name.encode(),
+                            C.byref(v))
+    return st, L.qh_last_error().decode()
+
+
+def test_malformed_and_unsupported():
+    img = QH.nf4_file_bytes({"w": _q(3, 67, 8)})
+    assert _find(b"")[0] == 5
+    assert _find(b"")[1] == "malformed input: file smaller than safetensors header"
+    st, msg = _find(b"\xff" * 8 + img[8:])
+    assert st == 5 and msg == "malformed input: safetensors header length exceeds file"
+    bad = bytearray(img)
+    bad[8] = ord("X")
+    st, msg = _find(bytes(bad))
+    assert st == 5 and msg.startswith("malformed input: safetensors header:")
+    st, msg = _find(img[:-1])  # data cut short: offsets outside the data
+    assert st == 5 and "offsets outside the data" in msg
+    st, msg = _find(img, "nope")
+    assert st == 5 and msg == 'malformed input: no weight "nope" in the file'
+    q = _q(3, 67, 9)
+    f16 = safetensors_np.save({"w.nf4_codes": q["codes"].astype(np.float16),
+                               "w.nf4_scale_codes": q["scale_codes"],
+                               "w.nf4_absmax": q["absmax"]}, metadata={"w": "3,67,64"})
+    st, msg = _find(f16)
+    assert st == 6 and msg == "unsupported: tensor \"w.nf4_codes\" has dtype F16, expected U8"
+    short = safetensors_np.save({"w.nf4_codes": q["codes"][:-1],
+                                 "w.nf4_scale_codes": q["scale_codes"],
+                                 "w.nf4_absmax": q["absmax"]}, metadata={"w": "3,67,64"})
+    st, msg = _find(short)
+    assert st == 1 and msg == ("shape mismatch: w.nf4_codes has 100 elements but the "
+                               "weight's shape needs 101")
+    for md, want in (("3,67", 5), ("3,67,0", 2), ("3;67;64", 5)):
+        img2 = safetensors_np.save({"w.nf4_codes": q["codes"]}, metadata={"w": md})
+        assert _find(img2)[0] == want, md
+
+
+def test_writer_validation():
+    L = _lib.load()
+    q = _q(2, 64, 10)
+    s = QH.qweight_struct(q)
+    arr = (_lib.QWeight * 2)(s, s)
+    names = (C.c_char_p * 2)(b"a", b"a")
+    size = C.c_size_t()
+    assert L.qh_nf4_file_size(arr, names, 2, C.byref(size)) == 1
+    assert L.qh_last_error().decode() == 'shape mismatch: weight name "a" repeats'
+    names = (C.c_char_p * 1)(b"format")
+    assert L.qh_nf4_file_size(arr, names, 1, C.byref(size)) == 2
+    names = (C.c_char_p * 1)(b"ok")
+    assert L.qh_nf4_file_size(arr, names, 1, C.byref(size)) == 0
+    buf = np.empty(size.value - 1, np.uint8)
+    assert L.qh_nf4_file_write(arr, names, 1, buf.ctypes.data_as(C.c_void_p), buf.size) == 1
+    s.codes = None
+    arr = (_lib.QWeight * 1)(s)
+    assert L.qh_nf4_file_size(arr, names, 1, C.byref(size)) == 1
+    # zero weights: a valid (empty) file
+    img = QH.nf4_file_bytes({})
+    assert QH.load_nf4(img) == {}

@@ -19,7 +19,7 @@ OUT = os.path.join(HERE, "qlora_hip", "libqlora_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["runtime.cpp", "k_quant.hip", "k_gemm.hip", "k_gemv.hip",
+SOURCES = ["runtime.cpp", "nf4_file.cpp", "k_quant.hip", "k_gemm.hip", "k_gemv.hip",
            "k_decode.hip", "k_dstream.hip", "k_adam.hip", "k_elem.hip",
            "k_block.hip"]
 

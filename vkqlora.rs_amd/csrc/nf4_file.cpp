@@ -1,0 +1,459 @@
+// nf4_file.cpp -- packed NF4 weights in a safetensors file, so quantized
+// weights go from disk straight into HBM without an fp32 round trip and
+// without quantizing again.
+//
+// Layout (a valid safetensors file; readers that convert to fp32, like
+// qlora-io's read_safetensors, still parse it):
+//   u64 LE header length, JSON header padded with spaces to a multiple of 8,
+//   then the tensors' bytes back to back in header order.
+//   "__metadata__": {"format": "qlora-hip-nf4/1",
+//                    "<name>": "<rows>,<cols>,<block_size>", ...}
+//   "<name>.nf4_codes":       U8  [ceil(n/2)]   two codes per byte, low nibble first
+//   "<name>.nf4_scale_codes": U8  [nb]          int8 double-quant codes, bit-cast
+//   "<name>.nf4_absmax":      F32 [ceil(nb/256)]
+// or, for fp32 block scales,
+//   "<name>.nf4_scales":      F32 [nb]
+// with n = rows * cols and nb = ceil(n / block_size) (quant.rs:93-100).
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "qh_host.h"
+#include "qlora_hip.h"
+
+namespace {
+
+constexpr const char *kFormat = "qlora-hip-nf4/1";
+
+using qh::host_fail;
+
+struct TensorMeta {
+  std::string dtype;
+  std::vector<uint64_t> shape;
+  uint64_t start = 0, end = 0;
+};
+
+struct Header {
+  std::map<std::string, std::string> meta;
+  std::map<std::string, TensorMeta> tensors;
+  std::vector<std::string> order;  // metadata keys in file order
+  const uint8_t *data = nullptr;
+  uint64_t data_len = 0;
+};
+
+// ---- a JSON reader for the safetensors header schema -----------------------
+struct Json {
+  const char *p, *e;
+  std::string err;
+
+  void ws() {
+    while (p < e && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p;
+  }
+  bool eat(char c) {
+    ws();
+    if (p < e && *p == c) {
+      ++p;
+      return true;
+    }
+    return false;
+  }
+  bool fail_(const char *m) {
+    if (err.empty()) err = m;
+    return false;
+  }
+  static void put_utf8(std::string &s, uint32_t cp) {
+    if (cp < 0x80) {
+      s += (char)cp;
+    } else if (cp < 0x800) {
+      s += (char)(0xC0 | (cp >> 6));
+      s += (char)(0x80 | (cp & 0x3F));
+    } else {
+      s += (char)(0xE0 | (cp >> 12));
+      s += (char)(0x80 | ((cp >> 6) & 0x3F));
+      s += (char)(0x80 | (cp & 0x3F));
+    }
+  }
+  bool str(std::string &out) {
+    ws();
+    if (p >= e || *p != '"') return fail_("expected string");
+    ++p;
+    out.clear();
+    while (p < e) {
+      char c = *p++;
+      if (c == '"') return true;
+      if (c != '\\') {
+        out += c;
+        continue;
+      }
+      if (p >= e) break;
+      c = *p++;
+      switch (c) {
+        case '"': out += '"'; break;
+        case '\\': out += '\\'; break;
+        case '/': out += '/'; break;
+        case 'n': out += '\n'; break;
+        case 't': out += '\t'; break;
+        case 'r': out += '\r'; break;
+        case 'b': out += '\b'; break;
+        case 'f': out += '\f'; break;
+        case 'u': {
+          if (e - p < 4) return fail_("bad unicode escape");
+          uint32_t cp = 0;
+          for (int i = 0; i < 4; ++i) {
+            const char h = p[i];
+            cp <<= 4;
+            if (h >= '0' && h <= '9') cp |= (uint32_t)(h - '0');
+            else if (h >= 'a' && h <= 'f') cp |= (uint32_t)(h - 'a' + 10);
+            else if (h >= 'A' && h <= 'F') cp |= (uint32_t)(h - 'A' + 10);
+            else return fail_("bad unicode escape");
+          }
+          p += 4;
+          put_utf8(out, cp);
+          break;
+        }
+        default: return fail_("bad escape");
+      }
+    }
+    return fail_("unterminated string");
+  }
+  bool num(uint64_t &v) {
+    ws();
+    const char *s = p;
+    v = 0;
+    while (p < e && *p >= '0' && *p <= '9') {
+      const uint64_t d = (uint64_t)(*p - '0');
+      if (v > (UINT64_MAX - d) / 10) return fail_("number too large");
+      v = v * 10 + d;
+      ++p;
+    }
+    return p != s ? true : fail_("expected number");
+  }
+  bool nums(std::vector<uint64_t> &out) {
+    out.clear();
+    if (!eat('[')) return fail_("expected [");
+    if (eat(']')) return true;
+    for (;;) {
+      uint64_t v;
+      if (!num(v)) return false;
+      out.push_back(v);
+      if (eat(']')) return true;
+      if (!eat(',')) return fail_("expected , or ]");
+    }
+  }
+};
+
+qh_status malformed(const std::string &m) { return host_fail(QH_ERR_MALFORMED, m); }
+
+qh_status parse(const uint8_t *buf, size_t len, Header *h) {
+  if (!buf || len < 8) return malformed("file smaller than safetensors header");
+  uint64_t hlen = 0;
+  for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | buf[i];
+  if (hlen > len - 8) return malformed("safetensors header length exceeds file");
+  Json j{(const char *)buf + 8, (const char *)buf + 8 + hlen, {}};
+  auto bad = [&]() { return malformed("safetensors header: " + j.err); };
+  if (!j.eat('{')) return j.fail_("expected {"), bad();
+  if (!j.eat('}')) {
+    for (;;) {
+      std::string key;
+      if (!j.str(key) || !j.eat(':')) return j.fail_("expected :"), bad();
+      if (key == "__metadata__") {
+        if (!j.eat('{')) return j.fail_("expected {"), bad();
+        if (!j.eat('}')) {
+          for (;;) {
+            std::string k, v;
+            if (!j.str(k) || !j.eat(':') || !j.str(v)) return j.fail_("bad metadata"), bad();
+            if (!h->meta.count(k)) h->order.push_back(k);
+            h->meta[k] = v;
+            if (j.eat('}')) break;
+            if (!j.eat(',')) return j.fail_("expected , or }"), bad();
+          }
+        }
+      } else {
+        TensorMeta t;
+        bool has_d = false, has_s = false, has_o = false;
+        if (!j.eat('{')) return j.fail_("expected {"), bad();
+        if (!j.eat('}')) {
+          for (;;) {
+            std::string f;
+            if (!j.str(f) || !j.eat(':')) return j.fail_("expected :"), bad();
+            if (f == "dtype") {
+              if (!j.str(t.dtype)) return bad();
+              has_d = true;
+            } else if (f == "shape") {
+              if (!j.nums(t.shape)) return bad();
+              has_s = true;
+            } else if (f == "data_offsets") {
+              std::vector<uint64_t> o;
+              if (!j.nums(o)) return bad();
+              if (o.size() != 2) return j.fail_("data_offsets must have 2 elements"), bad();
+              t.start = o[0];
+              t.end = o[1];
+              has_o = true;
+            } else {
+              return j.fail_("unexpected tensor field"), bad();
+            }
+            if (j.eat('}')) break;
+            if (!j.eat(',')) return j.fail_("expected , or }"), bad();
+          }
+        }
+        if (!has_d || !has_s || !has_o)
+          return j.fail_("tensor entry missing dtype/shape/data_offsets"), bad();
+        h->tensors[key] = t;
+      }
+      if (j.eat('}')) break;
+      if (!j.eat(',')) return j.fail_("expected , or }"), bad();
+    }
+  }
+  j.ws();
+  if (j.p != j.e) return j.fail_("trailing data after header object"), bad();
+  h->data = buf + 8 + hlen;
+  h->data_len = len - 8 - hlen;
+  for (auto &kv : h->tensors) {
+    const TensorMeta &t = kv.second;
+    if (t.end < t.start || t.end > h->data_len)
+      return malformed("tensor \"" + kv.first + "\": offsets outside the data");
+  }
+  return QH_OK;
+}
+
+size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
+
+struct Sizes {
+  size_t n, nb, codes, scales, absmax;  // element counts
+};
+
+bool sizes_of(size_t rows, size_t cols, size_t bs, Sizes *s) {
+  if (bs == 0 || __builtin_mul_overflow(rows, cols, &s->n)) return false;
+  s->nb = div_ceil(s->n, bs);
+  s->codes = div_ceil(s->n, 2);
+  s->scales = s->nb;
+  s->absmax = div_ceil(s->nb, 256);
+  return true;
+}
+
+// One tensor of the file as (pointer, element count), checked against the
+// dtype and the element count the weight's shape implies.
+qh_status tensor_view(const Header &h, const std::string &key, const char *dtype, size_t isz,
+                      size_t want, const void **ptr) {
+  auto it = h.tensors.find(key);
+  if (it == h.tensors.end()) return malformed("missing tensor \"" + key + "\"");
+  const TensorMeta &t = it->second;
+  if (t.dtype != dtype)
+    return host_fail(QH_ERR_UNSUPPORTED,
+                     "tensor \"" + key + "\" has dtype " + t.dtype + ", expected " + dtype);
+  uint64_t numel = 1;
+  for (uint64_t d : t.shape)
+    if (__builtin_mul_overflow(numel, d, &numel)) return malformed("tensor shape overflows");
+  if (t.end - t.start != numel * isz)
+    return malformed("tensor \"" + key + "\": byte range does not match its shape");
+  if (numel != want) {
+    // from_raw_parts (quant.rs:184-197): the part lengths follow from the shape
+    char m[256];
+    snprintf(m, sizeof m, "%s has %llu elements but the weight's shape needs %zu", key.c_str(),
+             (unsigned long long)numel, want);
+    return host_fail(QH_ERR_SHAPE_MISMATCH, m);
+  }
+  *ptr = h.data + t.start;
+  return QH_OK;
+}
+
+qh_status view_of(const Header &h, const std::string &name, qh_qweight *out) {
+  auto it = h.meta.find(name);
+  if (it == h.meta.end()) return malformed("no weight \"" + name + "\" in the file");
+  unsigned long long r, c, b;
+  char tail;
+  if (sscanf(it->second.c_str(), "%llu,%llu,%llu%c", &r, &c, &b, &tail) != 3)
+    return malformed("weight \"" + name + "\": metadata is not rows,cols,block_size");
+  if (b == 0) return host_fail(QH_ERR_INVALID_CONFIG, "block_size must be > 0");
+  Sizes s;
+  if (!sizes_of((size_t)r, (size_t)c, (size_t)b, &s))
+    return host_fail(QH_ERR_INVALID_CONFIG, "rows*cols overflow");
+  qh_qweight w{};
+  w.rows = (size_t)r;
+  w.cols = (size_t)c;
+  w.block_size = (size_t)b;
+  const void *p = nullptr;
+  qh_status st = tensor_view(h, name + ".nf4_codes", "U8", 1, s.codes, &p);
+  if (st != QH_OK) return st;
+  w.codes = (const uint8_t *)p;
+  if (h.tensors.count(name + ".nf4_scales")) {
+    w.scale_kind = QH_SCALES_F32;
+    if ((st = tensor_view(h, name + ".nf4_scales", "F32", 4, s.scales, &p)) != QH_OK) return st;
+    w.scales = (const float *)p;
+  } else {
+    w.scale_kind = QH_SCALES_DQ_INT8;
+    if ((st = tensor_view(h, name + ".nf4_scale_codes", "U8", 1, s.scales, &p)) != QH_OK)
+      return st;
+    w.scale_codes = (const uint8_t *)p;
+    if ((st = tensor_view(h, name + ".nf4_absmax", "F32", 4, s.absmax, &p)) != QH_OK) return st;
+    w.absmax = (const float *)p;
+  }
+  *out = w;
+  return QH_OK;
+}
+
+// Weight names of a parsed header, in metadata order (entries of
+// __metadata__ other than "format" that have a codes tensor).
+std::vector<std::string> weight_names(const Header &h) {
+  std::vector<std::string> out;
+  for (const auto &k : h.order)
+    if (k != "format" && h.tensors.count(k + ".nf4_codes")) out.push_back(k);
+  return out;
+}
+
+void json_str(std::string &o, const std::string &s) {
+  o += '"';
+  for (unsigned char c : s) {
+    if (c == '"' || c == '\\') {
+      o += '\\';
+      o += (char)c;
+    } else if (c < 0x20) {
+      char u[8];
+      snprintf(u, sizeof u, "\\u%04x", c);
+      o += u;
+    } else {
+      o += (char)c;
+    }
+  }
+  o += '"';
+}
+
+struct Part {
+  std::string key;
+  const char *dtype;
+  const void *src;
+  size_t bytes, numel;
+};
+
+// Header text and the list of tensor parts, in file order.
+qh_status layout(const qh_qweight *ws, const char *const *names, size_t count,
+                 std::string *header, std::vector<Part> *parts) {
+  if (count && (!ws || !names)) return host_fail(QH_ERR_SHAPE_MISMATCH, "weights or names NULL");
+  std::map<std::string, int> seen;
+  std::string meta = "\"__metadata__\":{\"format\":";
+  json_str(meta, kFormat);
+  for (size_t i = 0; i < count; ++i) {
+    const qh_qweight &w = ws[i];
+    if (!names[i] || !names[i][0]) return host_fail(QH_ERR_SHAPE_MISMATCH, "empty weight name");
+    const std::string nm = names[i];
+    if (nm == "format" || nm == "__metadata__")
+      return host_fail(QH_ERR_INVALID_CONFIG, "weight name \"" + nm + "\" is reserved");
+    if (seen[nm]++) return host_fail(QH_ERR_SHAPE_MISMATCH, "weight name \"" + nm + "\" repeats");
+    if (w.block_size == 0) return host_fail(QH_ERR_INVALID_CONFIG, "block_size must be > 0");
+    Sizes s;
+    if (!sizes_of(w.rows, w.cols, w.block_size, &s))
+      return host_fail(QH_ERR_INVALID_CONFIG, "rows*cols overflow");
+    if (w.scale_kind != QH_SCALES_F32 && w.scale_kind != QH_SCALES_DQ_INT8)
+      return host_fail(QH_ERR_INVALID_CONFIG, "unknown scale kind");
+    const bool dq = w.scale_kind == QH_SCALES_DQ_INT8;
+    if (!w.codes || (dq ? (!w.scale_codes || !w.absmax) : !w.scales))
+      return host_fail(QH_ERR_SHAPE_MISMATCH, "weight \"" + nm + "\" has a NULL part");
+    meta += ',';
+    json_str(meta, nm);
+    meta += ':';
+    json_str(meta, std::to_string(w.rows) + "," + std::to_string(w.cols) + "," +
+                       std::to_string(w.block_size));
+    parts->push_back({nm + ".nf4_codes", "U8", w.codes, s.codes, s.codes});
+    if (dq) {
+      parts->push_back({nm + ".nf4_scale_codes", "U8", w.scale_codes, s.scales, s.scales});
+      parts->push_back({nm + ".nf4_absmax", "F32", w.absmax, s.absmax * 4, s.absmax});
+    } else {
+      parts->push_back({nm + ".nf4_scales", "F32", w.scales, s.scales * 4, s.scales});
+    }
+  }
+  meta += '}';
+  std::string o = "{" + meta;
+  uint64_t off = 0;
+  for (const Part &p : *parts) {
+    o += ',';
+    json_str(o, p.key);
+    o += ":{\"dtype\":\"";
+    o += p.dtype;
+    o += "\",\"shape\":[" + std::to_string(p.numel) + "],\"data_offsets\":[" +
+         std::to_string(off) + "," + std::to_string(off + p.bytes) + "]}";
+    off += p.bytes;
+  }
+  o += '}';
+  while (o.size() % 8) o += ' ';
+  *header = o;
+  return QH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+qh_status qh_nf4_file_size(const qh_qweight *ws, const char *const *names, size_t count,
+                           size_t *bytes) {
+  std::string hdr;
+  std::vector<Part> parts;
+  qh_status st = layout(ws, names, count, &hdr, &parts);
+  if (st != QH_OK) return st;
+  size_t total = 8 + hdr.size();
+  for (const Part &p : parts) total += p.bytes;
+  if (bytes) *bytes = total;
+  return QH_OK;
+}
+
+qh_status qh_nf4_file_write(const qh_qweight *ws, const char *const *names, size_t count,
+                            uint8_t *buf, size_t buf_len) {
+  std::string hdr;
+  std::vector<Part> parts;
+  qh_status st = layout(ws, names, count, &hdr, &parts);
+  if (st != QH_OK) return st;
+  size_t total = 8 + hdr.size();
+  for (const Part &p : parts) total += p.bytes;
+  if (!buf || buf_len != total)
+    return host_fail(QH_ERR_SHAPE_MISMATCH,
+                     "buf_len = " + std::to_string(buf_len) + " but the file needs " +
+                         std::to_string(total) + " bytes");
+  uint64_t hl = hdr.size();
+  for (int i = 0; i < 8; ++i) buf[i] = (uint8_t)(hl >> (8 * i));
+  memcpy(buf + 8, hdr.data(), hdr.size());
+  uint8_t *d = buf + 8 + hdr.size();
+  for (const Part &p : parts) {
+    if (p.bytes) memcpy(d, p.src, p.bytes);
+    d += p.bytes;
+  }
+  return QH_OK;
+}
+
+qh_status qh_nf4_file_count(const uint8_t *buf, size_t len, size_t *count) {
+  Header h;
+  qh_status st = parse(buf, len, &h);
+  if (st != QH_OK) return st;
+  if (count) *count = weight_names(h).size();
+  return QH_OK;
+}
+
+qh_status qh_nf4_file_entry(const uint8_t *buf, size_t len, size_t index, char *name,
+                            size_t name_len, qh_qweight *view) {
+  Header h;
+  qh_status st = parse(buf, len, &h);
+  if (st != QH_OK) return st;
+  const std::vector<std::string> names = weight_names(h);
+  if (index >= names.size())
+    return host_fail(QH_ERR_SHAPE_MISMATCH, "index " + std::to_string(index) + " but the file has " +
+                                                std::to_string(names.size()) + " weights");
+  if (name) {
+    if (name_len < names[index].size() + 1)
+      return host_fail(QH_ERR_SHAPE_MISMATCH, "name buffer too small");
+    memcpy(name, names[index].c_str(), names[index].size() + 1);
+  }
+  return view ? view_of(h, names[index], view) : QH_OK;
+}
+
+qh_status qh_nf4_file_find(const uint8_t *buf, size_t len, const char *name, qh_qweight *view) {
+  Header h;
+  qh_status st = parse(buf, len, &h);
+  if (st != QH_OK) return st;
+  if (!name) return host_fail(QH_ERR_SHAPE_MISMATCH, "name is NULL");
+  if (!h.tensors.count(std::string(name) + ".nf4_codes"))
+    return malformed("no weight \"" + std::string(name) + "\" in the file");
+  return view_of(h, name, view);
+}
+
+}  // extern "C"

@@ -4,6 +4,7 @@
 // accept/reject rules and messages, staging of host slices, choice of
 // kernel per shape, and the 8-bit Adam state that lives in HBM.
 #include "qlora_hip.h"
+#include "qh_host.h"
 
 #include <cmath>
 #include <cstdarg>
@@ -35,6 +36,9 @@ qh_status fail(qh_status st, const std::string &msg) {
     case QH_ERR_SHAPE_MISMATCH: g_err = "shape mismatch: " + msg; break;
     case QH_ERR_INVALID_CONFIG: g_err = "invalid config: " + msg; break;
     case QH_ERR_GPU: g_err = "gpu error: " + msg; break;
+    // IoError's Display formats (qlora-io/src/error.rs:15-20)
+    case QH_ERR_MALFORMED: g_err = "malformed input: " + msg; break;
+    case QH_ERR_UNSUPPORTED: g_err = "unsupported: " + msg; break;
     default: g_err = msg; break;
   }
   return st;
@@ -1358,4 +1362,35 @@ qh_status qh_softmax_cross_entropy_dev(qh_ctx *ctx, const float *d_logits,
   });
 }
 
+// ---- packed NF4 files: host views into HBM ------------------------------------
+qh_status qh_weight_upload_dev(qh_ctx *ctx, const qh_qweight *w, uint8_t *d_codes,
+                               float *d_scales, uint8_t *d_scale_codes, float *d_absmax,
+                               void *stream) {
+  qh_status st = validate_weight(w);
+  if (st != QH_OK) return st;
+  const bool dq = w->scale_kind == QH_SCALES_DQ_INT8;
+  if (!d_codes || (dq ? (!d_scale_codes || !d_absmax) : !d_scales))
+    return fail(QH_ERR_SHAPE_MISMATCH, "a device buffer for the weight's parts is NULL");
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    const size_t n = w->rows * w->cols, nb = div_ceil(n, w->block_size);
+    if (n) check(hipMemcpyAsync(d_codes, w->codes, div_ceil(n, 2), hipMemcpyHostToDevice, s),
+                 "upload codes");
+    if (dq) {
+      if (nb) check(hipMemcpyAsync(d_scale_codes, w->scale_codes, nb, hipMemcpyHostToDevice, s),
+                    "upload scale codes");
+      if (nb) check(hipMemcpyAsync(d_absmax, w->absmax, div_ceil(nb, 256) * 4,
+                                   hipMemcpyHostToDevice, s), "upload absmax");
+    } else if (nb) {
+      check(hipMemcpyAsync(d_scales, w->scales, nb * 4, hipMemcpyHostToDevice, s),
+            "upload scales");
+    }
+    return QH_OK;
+  });
+}
+
 }  // extern "C"
+
+namespace qh {
+qh_status host_fail(qh_status st, const std::string &msg) { return fail(st, msg); }
+}  // namespace qh

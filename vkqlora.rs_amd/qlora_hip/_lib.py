@@ -18,6 +18,8 @@ QH_ERR_SHAPE_MISMATCH = 1
 QH_ERR_INVALID_CONFIG = 2
 QH_ERR_GPU = 3
 QH_NO_DEVICE = 4
+QH_ERR_MALFORMED = 5
+QH_ERR_UNSUPPORTED = 6
 
 QH_SCALES_F32 = 0
 QH_SCALES_DQ_INT8 = 1
@@ -39,6 +41,8 @@ EXPORTED = [
     "qh_rmsnorm", "qh_rmsnorm_dev", "qh_rmsnorm_backward", "qh_rmsnorm_backward_dev",
     "qh_swiglu", "qh_swiglu_dev", "qh_swiglu_backward", "qh_swiglu_backward_dev",
     "qh_softmax_cross_entropy", "qh_softmax_cross_entropy_dev",
+    "qh_nf4_file_size", "qh_nf4_file_write", "qh_nf4_file_count", "qh_nf4_file_entry",
+    "qh_nf4_file_find", "qh_weight_upload_dev",
 ]
 
 
@@ -147,6 +151,12 @@ def load() -> C.CDLL:
         L.qh_swiglu_backward_dev.argtypes = [vp, vp, vp, vp, sz, vp, vp, vp]
         L.qh_softmax_cross_entropy.argtypes = [vp, vp, sz, vp, sz, sz, vp, vp]
         L.qh_softmax_cross_entropy_dev.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
+        L.qh_nf4_file_size.argtypes = [vp, vp, sz, C.POINTER(sz)]
+        L.qh_nf4_file_write.argtypes = [vp, vp, sz, vp, sz]
+        L.qh_nf4_file_count.argtypes = [vp, sz, C.POINTER(sz)]
+        L.qh_nf4_file_entry.argtypes = [vp, sz, sz, C.c_char_p, sz, C.POINTER(QWeight)]
+        L.qh_nf4_file_find.argtypes = [vp, sz, C.c_char_p, C.POINTER(QWeight)]
+        L.qh_weight_upload_dev.argtypes = [vp, C.POINTER(QWeight), vp, vp, vp, vp, vp]
         _lib = L
         return L
 

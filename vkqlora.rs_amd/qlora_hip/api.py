@@ -332,3 +332,77 @@ class PagedAdam:
 
     def state_bytes(self) -> int:
         return self.opt.state_bytes()
+
+
+# ---- packed NF4 files (safetensors; no fp32 round trip, no re-quantize) ----
+def _qdict(w) -> dict:
+    return w._q if isinstance(w, QuantizedWeight) else w
+
+
+def nf4_file_bytes(weights) -> bytes:
+    """A safetensors image of ``{name: QuantizedWeight or quantize() dict}``
+    holding the packed parts (codes, int8 scale codes + absmax, or fp32
+    scales) and each weight's rows, cols and block size."""
+    L = _lib.load()
+    names = list(weights)
+    qs = [_qdict(weights[n]) for n in names]
+    arr = (QWeight * max(1, len(qs)))()
+    for i, q in enumerate(qs):
+        arr[i] = qweight_struct(q)
+    cn = (C.c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+    size = C.c_size_t()
+    check(L.qh_nf4_file_size(arr, cn, len(names), C.byref(size)))
+    buf = np.empty(size.value, np.uint8)
+    check(L.qh_nf4_file_write(arr, cn, len(names), _ptr(buf), size.value))
+    return buf.tobytes()
+
+
+def save_nf4(path: str, weights) -> int:
+    """Write ``nf4_file_bytes(weights)`` to ``path``; returns its size."""
+    data = nf4_file_bytes(weights)
+    with open(path, "wb") as f:
+        f.write(data)
+    return len(data)
+
+
+def nf4_file_views(buf: np.ndarray):
+    """[(name, qh_qweight view into buf)] of a file image held in ``buf``
+    (a uint8 array the caller keeps alive)."""
+    L = _lib.load()
+    cnt = C.c_size_t()
+    check(L.qh_nf4_file_count(_ptr(buf), buf.size, C.byref(cnt)))
+    out = []
+    for i in range(cnt.value):
+        name = C.create_string_buffer(4096)
+        v = QWeight()
+        check(L.qh_nf4_file_entry(_ptr(buf), buf.size, i, name, 4096, C.byref(v)))
+        out.append((name.value.decode(), v))
+    return out
+
+
+def _copy_part(addr: int, count: int, dtype) -> np.ndarray:
+    nbytes = count * np.dtype(dtype).itemsize
+    raw = (C.c_uint8 * nbytes).from_address(addr) if nbytes else b""
+    return np.frombuffer(bytes(raw), dtype=dtype).copy()
+
+
+def load_nf4(src) -> dict:
+    """``{name: quantize()-style dict}`` from a path or a bytes image; the
+    parts are copied out of the file bit for bit."""
+    if isinstance(src, (bytes, bytearray)):
+        buf = np.frombuffer(bytes(src), np.uint8).copy()
+    else:
+        buf = np.fromfile(src, dtype=np.uint8)
+    out = {}
+    for name, v in nf4_file_views(buf):
+        n = v.rows * v.cols
+        nb = -(-n // v.block_size)
+        q = dict(rows=v.rows, cols=v.cols, block_size=v.block_size, n=n,
+                 codes=_copy_part(v.codes, (n + 1) // 2, np.uint8))
+        if v.scale_kind == QH_SCALES_DQ_INT8:
+            q["scale_codes"] = _copy_part(v.scale_codes, nb, np.uint8)
+            q["absmax"] = _copy_part(v.absmax, -(-nb // 256), np.float32)
+        else:
+            q["scales"] = _copy_part(v.scales, nb, np.float32)
+        out[name] = q
+    return out

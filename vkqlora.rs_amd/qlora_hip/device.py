@@ -73,6 +73,25 @@ class DeviceWeight:
                                           C.c_void_p(_stream())))
         return cls(rows, cols, block_size, codes, scales=sf)
 
+    @classmethod
+    def from_host_view(cls, v: QWeight, device, ctx=None) -> "DeviceWeight":
+        """Copy a host ``qh_qweight`` (e.g. a view into a file image) into
+        HBM with ``qh_weight_upload_dev`` on the current stream."""
+        ctx = ctx or default_context()
+        n = v.rows * v.cols
+        nb = -(-n // v.block_size)
+        codes = torch.empty((n + 1) // 2, dtype=torch.uint8, device=device)
+        if v.scale_kind == QH_SCALES_DQ_INT8:
+            sc = torch.empty(nb, dtype=torch.uint8, device=device)
+            am = torch.empty(-(-nb // 256), dtype=torch.float32, device=device)
+            check(ctx.lib.qh_weight_upload_dev(ctx.h, C.byref(v), _p(codes), None, _p(sc),
+                                               _p(am), C.c_void_p(_stream())))
+            return cls(v.rows, v.cols, v.block_size, codes, scale_codes=sc, absmax=am)
+        sf = torch.empty(nb, dtype=torch.float32, device=device)
+        check(ctx.lib.qh_weight_upload_dev(ctx.h, C.byref(v), _p(codes), _p(sf), None, None,
+                                           C.c_void_p(_stream())))
+        return cls(v.rows, v.cols, v.block_size, codes, scales=sf)
+
     def clone(self) -> "DeviceWeight":
         c = lambda t: None if t is None else t.clone()  # noqa: E731
         return DeviceWeight(self.rows, self.cols, self.block_size, c(self.codes),
@@ -217,3 +236,29 @@ def softmax_cross_entropy(logits: torch.Tensor, targets: torch.Tensor,
     check(ctx.lib.qh_softmax_cross_entropy_dev(ctx.h, _p(logits), _p(targets), seq, vocab,
                                                _p(loss), _p(d), C.c_void_p(_stream())))
     return loss, d
+
+
+# ---- packed NF4 files straight into HBM ---------------------------------------
+def read_file_pinned(path: str) -> torch.Tensor:
+    """The file's bytes in pinned host memory (so uploads are DMA)."""
+    import os
+    n = os.path.getsize(path)
+    buf = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    with open(path, "rb") as f:
+        f.readinto(buf.numpy())
+    return buf
+
+
+def load_nf4(src, device="cuda:0", ctx=None) -> dict:
+    """``{name: DeviceWeight}`` from a packed NF4 file (path, or a host uint8
+    tensor / array holding its image): each weight's parts are copied from the
+    image into HBM as they are stored, with no fp32 and no quantize on the
+    way.  The copies are enqueued on the current stream; the call waits for
+    them before the image can go away."""
+    from .api import nf4_file_views
+    buf = read_file_pinned(src) if isinstance(src, str) else src
+    arr = buf.numpy() if isinstance(buf, torch.Tensor) else buf
+    out = {name: DeviceWeight.from_host_view(v, device, ctx=ctx)
+           for name, v in nf4_file_views(arr)}
+    torch.cuda.current_stream().synchronize()
+    return out
