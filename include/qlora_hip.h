@@ -294,6 +294,42 @@ QH_API qh_status qh_softmax_cross_entropy_dev(qh_ctx *ctx,
                                               float *d_loss, float *d_dlogits,
                                               void *stream);
 
+/* ---- a decoder block's MLP on device ----------------------------------------
+ * The MLP half of `block_forward` / `block_backward` (qlora-model/src/
+ * llama.rs:449-463, 543-565) with its three projections as QLoRA layers
+ * (`Proj::Qlora`, llama.rs:106-140): activations stay in HBM from the norm
+ * to the residual add, all on `stream`.  Device pointers throughout. */
+typedef struct qh_mlp_block {
+  size_t hidden, inter;
+  float eps;                /* LlamaConfig::rms_eps */
+  const float *norm_w;      /* mlp_norm, hidden floats */
+  qh_qweight gate, up;      /* inter x hidden */
+  qh_qweight down;          /* hidden x inter */
+  const qh_lora *gate_lora, *up_lora, *down_lora; /* NULL = no adapter */
+} qh_mlp_block;
+
+/* Activations the forward keeps for the backward (caller-owned device
+ * buffers; the backward consumes gate and up). */
+typedef struct qh_mlp_cache {
+  float *x_mid;             /* seq x hidden: the block's input */
+  float *xn;                /* seq x hidden: rmsnorm(x_mid) */
+  float *gate, *up, *act;   /* seq x inter */
+  float *t1_gate, *t1_up, *t1_down; /* seq x r of each adapter (or NULL) */
+} qh_mlp_cache;
+
+/* x (seq x hidden) <- x + down(silu(gate(xn)) * up(xn)), xn = rmsnorm(x). */
+QH_API qh_status qh_mlp_forward_dev(qh_ctx *ctx, const qh_mlp_block *blk,
+                                    float *d_x, size_t seq,
+                                    const qh_mlp_cache *cache, void *stream);
+/* dx_in = dL/d(block input) from dx_out = dL/d(block output); adapter
+ * gradients in gate, up, down order (d_grad_a[i]: r x in, d_grad_b[i]:
+ * out x r), entries of projections without an adapter are ignored. */
+QH_API qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *blk,
+                                     const qh_mlp_cache *cache,
+                                     const float *d_dx_out, size_t seq,
+                                     float *d_dx_in, float *const *d_grad_a,
+                                     float *const *d_grad_b, void *stream);
+
 /* ---- packed NF4 files -----------------------------------------------------
  * No counterpart in the reference: its quantized weights leave `quantize`
  * only as fp32 (QuantizedWeight.scales, qlora-python/src/lib.rs:101) and

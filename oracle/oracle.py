@@ -363,3 +363,39 @@ def softmax_cross_entropy(logits, targets, seq, vocab):
     loss = lib().or_softmax_cross_entropy(
         _fp(logits), targets.ctypes.data_as(C.POINTER(C.c_uint32)), seq, vocab, _fp(d))
     return float(loss), d
+
+
+def mlp_forward(norm_w, gate, up, down, x, seq, hidden, inter, eps):
+    """The MLP half of block_forward (llama.rs:449-463) with QLoRA
+    projections (llama.rs:106-114).  ``gate``/``up``/``down`` are
+    (w_deq, a, b, r, alpha) with a = b = None for no adapter.  Returns
+    (x_out, cache)."""
+    x = _f32(x)
+    xn = rmsnorm(x, norm_w, seq, hidden, eps)
+
+    def proj(p, inp, out_dim, in_dim):
+        wd, a, b, r, alpha = p
+        return qlora_forward(wd, out_dim, in_dim, a, b, r, alpha, inp, seq)
+    g = proj(gate, xn, inter, hidden)
+    u = proj(up, xn, inter, hidden)
+    act = swiglu(g, u)
+    dn = proj(down, act, hidden, inter)
+    x_out = (x + dn).astype(np.float32)   # x_i += d (llama.rs:460-462)
+    return x_out, dict(x_mid=x, xn=xn, gate=g, up=u, act=act)
+
+
+def mlp_backward(norm_w, gate, up, down, cache, dx_out, seq, hidden, inter, eps):
+    """The MLP branch of block_backward (llama.rs:543-565) -> (dx_in,
+    [(grad_a, grad_b) or None for gate, up, down])."""
+    def proj_bwd(p, inp, dy, out_dim, in_dim):
+        wd, a, b, r, alpha = p
+        gx, ga, gb = qlora_backward(wd, out_dim, in_dim, a, b, r, alpha, inp, dy, seq)
+        return gx, (None if a is None else (ga, gb))
+    dx_out = _f32(dx_out)
+    d_act, gd = proj_bwd(down, cache["act"], dx_out, hidden, inter)
+    dg, du = swiglu_backward(cache["gate"], cache["up"], d_act)
+    dxn_g, gg = proj_bwd(gate, cache["xn"], dg, inter, hidden)
+    dxn_u, gu = proj_bwd(up, cache["xn"], du, inter, hidden)
+    dxn = (dxn_g + dxn_u).astype(np.float32)
+    dx_norm, _ = rmsnorm_backward(cache["x_mid"], norm_w, dxn, seq, hidden, eps)
+    return (dx_norm + dx_out).astype(np.float32), [gg, gu, gd]

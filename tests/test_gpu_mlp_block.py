@@ -1,0 +1,75 @@
+"""GPU parity of the device-resident MLP block (qh_mlp_forward_dev /
+qh_mlp_backward_dev): the MLP half of block_forward / block_backward
+(qlora-model/src/llama.rs:449-463, 543-565) with QLoRA projections, against
+the oracle's composite of the same steps.
+
+Tolerance (fp32, GEMM and row sums in a different order): max |gpu -
+oracle| <= 1e-4 * max |oracle| per output tensor.  The forward is also run
+twice and must repeat bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+TOL = 1e-4
+
+
+def _close(got, ref, what):
+    got = got.detach().cpu().numpy().ravel()
+    ref = np.ravel(ref)
+    scale = float(np.max(np.abs(ref)))
+    err = float(np.max(np.abs(got.astype(np.float64) - ref)))
+    assert err <= TOL * scale, f"{what}: max err {err:.3e} vs scale {scale:.3e}"
+
+
+@pytest.mark.parametrize("seq,adapters", [(64, (True, True, True)), (4, (True, False, True)),
+                                          (130, (False, True, False))])
+def test_mlp_block_parity(ctx, seq, adapters):
+    from qlora_hip import device as QD
+    print(f"mlp block seq={seq} adapters={adapters}", flush=True)
+    h, f, r, alpha, eps = 576, 1536, 8, 16.0, 1e-5
+    dev = torch.device("cuda:0")
+    g = O.Rng(0xB10C + seq)
+    norm = g.uniform(h, 0.5, 1.5)
+    ps, Ws, loras = [], [], []
+    for (out_dim, in_dim), ad in zip(((f, h), (f, h), (h, f)), adapters):
+        w = g.normal(out_dim * in_dim, 0.02)
+        W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(out_dim, in_dim), ctx=ctx)
+        wd = O.dequantize(O.quantize(w))
+        if ad:
+            a = g.uniform(r * in_dim, -1 / np.sqrt(in_dim), 1 / np.sqrt(in_dim))
+            b = g.normal(out_dim * r, 0.01)
+            ps.append([wd, a, b, r, alpha])
+            loras.append((torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r, alpha))
+        else:
+            ps.append([wd, None, None, 0, 0.0])
+            loras.append(None)
+        Ws.append(W)
+    x = g.normal(seq * h)
+    dy = g.normal(seq * h)
+    ref_out, cache = O.mlp_forward(norm, *ps, x, seq, h, f, eps)
+    ref_dx, ref_grads = O.mlp_backward(norm, *ps, cache, dy, seq, h, f, eps)
+
+    blk = QD.MLPBlock(torch.from_numpy(norm).to(dev), *Ws, loras=loras, eps=eps, ctx=ctx)
+    tx = torch.from_numpy(x).to(dev).view(seq, h)
+    c = blk.new_cache(seq)
+    x1 = blk.forward(tx.clone(), c)
+    c2 = blk.new_cache(seq)
+    x2 = blk.forward(tx.clone(), c2)
+    torch.cuda.synchronize()
+    assert torch.equal(x1, x2)
+    _close(x1, ref_out, "x_out")
+    _close(c["act"], cache["act"], "act")
+    dx, grads = blk.backward(c, torch.from_numpy(dy).to(dev).view(seq, h))
+    torch.cuda.synchronize()
+    _close(dx, ref_dx, "dx_in")
+    for name, got, want in zip(("gate", "up", "down"), grads, ref_grads):
+        assert (got is None) == (want is None), name
+        if got is not None:
+            _close(got[0], want[0], f"{name} grad_a")
+            _close(got[1], want[1], f"{name} grad_b")

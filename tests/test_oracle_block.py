@@ -127,3 +127,61 @@ def test_softmax_ce_uniform_and_fd():
     _, d = O.softmax_cross_entropy(logits, tg, seq, vocab)
     fd = _fd(lambda v: _ce64(v, tg, seq, vocab), logits.astype(np.float64))
     assert np.max(np.abs(d - fd)) < 1e-6
+
+
+def _tiny_block(seed, h=8, f=12, r=2, seq=3, adapters=(True, True, True)):
+    g = O.Rng(seed)
+    norm = g.uniform(h, 0.5, 1.5)
+
+    def proj(out_dim, in_dim, ad):
+        q = O.quantize(g.normal(out_dim * in_dim, 0.3))
+        wd = O.dequantize(q)
+        if not ad:
+            return [wd, None, None, 0, 0.0]
+        return [wd, g.uniform(r * in_dim, -0.5, 0.5), g.normal(out_dim * r, 0.5), r, 4.0]
+    ps = [proj(f, h, adapters[0]), proj(f, h, adapters[1]), proj(h, f, adapters[2])]
+    x = g.normal(seq * h)
+    dy = g.normal(seq * h)
+    return norm, ps, x, dy, seq, h, f
+
+
+def test_mlp_block_backward_finite_differences():
+    # the reference's own check of block_backward is a finite-difference
+    # comparison of the adapter gradients (qlora-model/tests/backward.rs:168-195)
+    norm, ps, x, dy, seq, h, f = _tiny_block(31)
+    eps = 1e-5
+
+    def loss(xv=None, which=None, k=None, val=None):
+        pp = [list(p) for p in ps]
+        if which is not None:
+            arr = pp[which[0]][which[1]].copy()
+            arr[k] = val
+            pp[which[0]][which[1]] = arr
+        out, _ = O.mlp_forward(norm, *pp, x if xv is None else xv, seq, h, f, eps)
+        return float(np.dot(out.astype(np.float64), dy.astype(np.float64)))
+
+    _, cache = O.mlp_forward(norm, *ps, x, seq, h, f, eps)
+    dx, grads = O.mlp_backward(norm, *ps, cache, dy, seq, h, f, eps)
+    d = 1e-2
+    for k in range(0, seq * h, 5):
+        xp, xm = x.copy(), x.copy()
+        xp[k] += d
+        xm[k] -= d
+        fd = (loss(xp) - loss(xm)) / (2 * d)
+        assert abs(dx[k] - fd) < 5e-3 * max(1.0, abs(fd)), (k, dx[k], fd)
+    for pi in range(3):
+        for slot in (1, 2):  # A, then B
+            arr = ps[pi][slot]
+            got = grads[pi][slot - 1]
+            for k in range(0, arr.size, 7):
+                fd = (loss(which=(pi, slot), k=k, val=arr[k] + d)
+                      - loss(which=(pi, slot), k=k, val=arr[k] - d)) / (2 * d)
+                assert abs(got[k] - fd) < 5e-3 * max(1.0, abs(fd)), (pi, slot, k, got[k], fd)
+
+
+def test_mlp_block_without_adapters():
+    norm, ps, x, dy, seq, h, f = _tiny_block(32, adapters=(False, True, False))
+    out, cache = O.mlp_forward(norm, *ps, x, seq, h, f, 1e-5)
+    dx, grads = O.mlp_backward(norm, *ps, cache, dy, seq, h, f, 1e-5)
+    assert grads[0] is None and grads[2] is None and grads[1] is not None
+    assert out.shape == x.shape and dx.shape == x.shape

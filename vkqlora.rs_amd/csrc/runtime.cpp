@@ -126,6 +126,7 @@ struct qh_ctx {
   std::mutex mu;
   DevBuf stage[10];  // host-API staging
   DevBuf scratch;    // internal scratch of the fused paths
+  DevBuf block_tmp[2];  // intermediate activations of the MLP block calls
   // Zero-initialised counters of kernels whose last workgroup finishes a
   // reduction; each such kernel leaves its counter at zero again.
   unsigned *tickets = nullptr;
@@ -650,6 +651,7 @@ void qh_ctx_destroy(qh_ctx *ctx) {
   }
   for (auto &b : ctx->stage) b.release();
   ctx->scratch.release();
+  for (auto &b : ctx->block_tmp) b.release();
   if (ctx->tickets) (void)hipFree(ctx->tickets);
   delete ctx;
 }
@@ -1385,6 +1387,113 @@ qh_status qh_weight_upload_dev(qh_ctx *ctx, const qh_qweight *w, uint8_t *d_code
       check(hipMemcpyAsync(d_scales, w->scales, nb * 4, hipMemcpyHostToDevice, s),
             "upload scales");
     }
+    return QH_OK;
+  });
+}
+
+// ---- a decoder block's MLP on device (qlora-model llama.rs) --------------------
+static qh_status validate_mlp(const qh_mlp_block *b) {
+  if (!b) return fail(QH_ERR_SHAPE_MISMATCH, "block descriptor is NULL");
+  const size_t h = b->hidden, f = b->inter;
+  if (h == 0 || f == 0) return fail(QH_ERR_SHAPE_MISMATCH, "hidden and inter must be > 0");
+  if (h > (size_t)INT32_MAX) return fail(QH_ERR_INVALID_CONFIG, "hidden size above 2^31-1");
+  if (!b->norm_w) return fail(QH_ERR_SHAPE_MISMATCH, "norm weight is NULL");
+  qh_status st;
+  const qh_qweight *ws[3] = {&b->gate, &b->up, &b->down};
+  const qh_lora *ls[3] = {b->gate_lora, b->up_lora, b->down_lora};
+  const size_t rows[3] = {f, f, h}, cols[3] = {h, h, f};
+  const char *nm[3] = {"gate", "up", "down"};
+  for (int i = 0; i < 3; ++i) {
+    if ((st = validate_weight(ws[i])) != QH_OK) return st;
+    if (ws[i]->rows != rows[i] || ws[i]->cols != cols[i])
+      return fail(QH_ERR_SHAPE_MISMATCH,
+                  fmt("%s weight is %zu x %zu but the block needs %zu x %zu", nm[i], ws[i]->rows,
+                      ws[i]->cols, rows[i], cols[i]));
+    if ((st = validate_lora(ls[i], cols[i], rows[i])) != QH_OK) return st;
+  }
+  return QH_OK;
+}
+
+static qh_status validate_cache(const qh_mlp_block *b, const qh_mlp_cache *c) {
+  if (!c || !c->x_mid || !c->xn || !c->gate || !c->up || !c->act)
+    return fail(QH_ERR_SHAPE_MISMATCH, "cache buffers must not be NULL");
+  return QH_OK;
+}
+
+qh_status qh_mlp_forward_dev(qh_ctx *ctx, const qh_mlp_block *b, float *d_x, size_t seq,
+                             const qh_mlp_cache *c, void *stream) {
+  qh_status st = validate_mlp(b);
+  if (st != QH_OK) return st;
+  if ((st = validate_cache(b, c)) != QH_OK) return st;
+  return guarded(ctx, [&] {
+    if (seq == 0) return QH_OK;
+    hipStream_t s = pick_stream(ctx, stream);
+    const size_t h = b->hidden, f = b->inter;
+    // llama.rs:449-463: xn = rmsnorm(x); gate, up; act = silu(gate) * up;
+    // x += down(act).  The block input is kept for the backward's norm.
+    check(hipMemcpyAsync(c->x_mid, d_x, seq * h * 4, hipMemcpyDeviceToDevice, s), "copy x");
+    timed(ctx, "rmsnorm", s, [&] {
+      return qh::launch_rmsnorm(d_x, b->norm_w, c->xn, (int64_t)seq, (int)h, b->eps, s);
+    });
+    forward_dev(ctx, make_devqw(b->gate), b->gate_lora, c->xn, QH_F32, seq, c->gate,
+                b->gate_lora ? c->t1_gate : nullptr, s);
+    forward_dev(ctx, make_devqw(b->up), b->up_lora, c->xn, QH_F32, seq, c->up,
+                b->up_lora ? c->t1_up : nullptr, s);
+    timed(ctx, "swiglu", s, [&] {
+      return qh::launch_swiglu(c->gate, c->up, c->act, (int64_t)(seq * f), s);
+    });
+    float *down = (float *)ctx->block_tmp[0].ensure(seq * h * 4);
+    forward_dev(ctx, make_devqw(b->down), b->down_lora, c->act, QH_F32, seq, down,
+                b->down_lora ? c->t1_down : nullptr, s);
+    timed(ctx, "residual_add", s, [&] {
+      return qh::launch_axpy_inplace(d_x, down, (int64_t)(seq * h), s);
+    });
+    return QH_OK;
+  });
+}
+
+qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *b, const qh_mlp_cache *c,
+                              const float *d_dx_out, size_t seq, float *d_dx_in,
+                              float *const *d_grad_a, float *const *d_grad_b, void *stream) {
+  qh_status st = validate_mlp(b);
+  if (st != QH_OK) return st;
+  if ((st = validate_cache(b, c)) != QH_OK) return st;
+  const qh_lora *ls[3] = {b->gate_lora, b->up_lora, b->down_lora};
+  for (int i = 0; i < 3; ++i)
+    if (ls[i] && (!d_grad_a || !d_grad_b || !d_grad_a[i] || !d_grad_b[i]))
+      return fail(QH_ERR_SHAPE_MISMATCH, "an adapter's gradient buffer is NULL");
+  return guarded(ctx, [&] {
+    if (seq == 0) return QH_OK;
+    hipStream_t s = pick_stream(ctx, stream);
+    const size_t h = b->hidden, f = b->inter;
+    // llama.rs:543-565 (MLP branch of block_backward)
+    float *d_act = (float *)ctx->block_tmp[0].ensure(seq * f * 4);
+    backward_dev(ctx, make_devqw(b->down), b->down_lora, c->act, d_dx_out, QH_F32, seq,
+                 b->down_lora ? c->t1_down : nullptr, d_act,
+                 b->down_lora ? d_grad_a[2] : nullptr, b->down_lora ? d_grad_b[2] : nullptr, s);
+    // dg over the cached gate, du over the cached up (the cache is consumed)
+    timed(ctx, "swiglu_backward", s, [&] {
+      return qh::launch_swiglu_bwd(c->gate, c->up, d_act, c->gate, c->up, (int64_t)(seq * f), s);
+    });
+    float *dxn_u = (float *)ctx->block_tmp[1].ensure(seq * h * 4);
+    backward_dev(ctx, make_devqw(b->gate), b->gate_lora, c->xn, c->gate, QH_F32, seq,
+                 b->gate_lora ? c->t1_gate : nullptr, d_dx_in,
+                 b->gate_lora ? d_grad_a[0] : nullptr, b->gate_lora ? d_grad_b[0] : nullptr, s);
+    backward_dev(ctx, make_devqw(b->up), b->up_lora, c->xn, c->up, QH_F32, seq,
+                 b->up_lora ? c->t1_up : nullptr, dxn_u,
+                 b->up_lora ? d_grad_a[1] : nullptr, b->up_lora ? d_grad_b[1] : nullptr, s);
+    timed(ctx, "residual_add", s, [&] {
+      return qh::launch_axpy_inplace(d_dx_in, dxn_u, (int64_t)(seq * h), s);
+    });
+    // dx_mid = rmsnorm_backward(x_mid, w, dxn).dx + dx_out (dw is discarded,
+    // llama.rs:560)
+    timed(ctx, "rmsnorm_backward", s, [&] {
+      return qh::launch_rmsnorm_bwd(c->x_mid, b->norm_w, d_dx_in, d_dx_in, nullptr, nullptr,
+                                    (int64_t)seq, (int)h, b->eps, s);
+    });
+    timed(ctx, "residual_add", s, [&] {
+      return qh::launch_axpy_inplace(d_dx_in, d_dx_out, (int64_t)(seq * h), s);
+    });
     return QH_OK;
   });
 }

@@ -42,7 +42,7 @@ EXPORTED = [
     "qh_swiglu", "qh_swiglu_dev", "qh_swiglu_backward", "qh_swiglu_backward_dev",
     "qh_softmax_cross_entropy", "qh_softmax_cross_entropy_dev",
     "qh_nf4_file_size", "qh_nf4_file_write", "qh_nf4_file_count", "qh_nf4_file_entry",
-    "qh_nf4_file_find", "qh_weight_upload_dev",
+    "qh_nf4_file_find", "qh_weight_upload_dev", "qh_mlp_forward_dev", "qh_mlp_backward_dev",
 ]
 
 
@@ -56,6 +56,20 @@ class QWeight(C.Structure):
 class Lora(C.Structure):
     _fields_ = [("a", C.c_void_p), ("a_len", C.c_size_t), ("b", C.c_void_p),
                 ("b_len", C.c_size_t), ("r", C.c_size_t), ("alpha", C.c_float)]
+
+
+class MlpBlock(C.Structure):
+    """qh_mlp_block (include/qlora_hip.h)."""
+    _fields_ = [("hidden", C.c_size_t), ("inter", C.c_size_t), ("eps", C.c_float),
+                ("norm_w", C.c_void_p), ("gate", QWeight), ("up", QWeight),
+                ("down", QWeight), ("gate_lora", C.POINTER(Lora)),
+                ("up_lora", C.POINTER(Lora)), ("down_lora", C.POINTER(Lora))]
+
+
+class MlpCache(C.Structure):
+    """qh_mlp_cache (include/qlora_hip.h)."""
+    _fields_ = [(n, C.c_void_p) for n in ("x_mid", "xn", "gate", "up", "act", "t1_gate",
+                                          "t1_up", "t1_down")]
 
 
 class AdamConfig(C.Structure):
@@ -157,6 +171,10 @@ def load() -> C.CDLL:
         L.qh_nf4_file_entry.argtypes = [vp, sz, sz, C.c_char_p, sz, C.POINTER(QWeight)]
         L.qh_nf4_file_find.argtypes = [vp, sz, C.c_char_p, C.POINTER(QWeight)]
         L.qh_weight_upload_dev.argtypes = [vp, C.POINTER(QWeight), vp, vp, vp, vp, vp]
+        L.qh_mlp_forward_dev.argtypes = [vp, C.POINTER(MlpBlock), vp, sz,
+                                         C.POINTER(MlpCache), vp]
+        L.qh_mlp_backward_dev.argtypes = [vp, C.POINTER(MlpBlock), C.POINTER(MlpCache), vp,
+                                          sz, vp, vp, vp, vp]
         _lib = L
         return L
 

@@ -16,7 +16,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import (Lora, QWeight, QH_BF16, QH_F32, QH_SCALES_DQ_INT8,
+from ._lib import (Lora, MlpBlock, MlpCache, QWeight, QH_BF16, QH_F32, QH_SCALES_DQ_INT8,
                    QH_SCALES_F32, check, default_context)
 
 
@@ -262,3 +262,70 @@ def load_nf4(src, device="cuda:0", ctx=None) -> dict:
            for name, v in nf4_file_views(arr)}
     torch.cuda.current_stream().synchronize()
     return out
+
+
+# ---- a decoder block's MLP on device (qh_mlp_forward_dev / _backward_dev) ----
+class MLPBlock:
+    """The MLP half of a decoder block (llama.rs:449-463, 543-565): RMSNorm,
+    gate / up / down QLoRA projections, SwiGLU and the residual add, with
+    every activation in HBM.  ``loras`` holds (a, b, r, alpha) per
+    projection (gate, up, down) or None."""
+
+    def __init__(self, norm_w: torch.Tensor, gate: DeviceWeight, up: DeviceWeight,
+                 down: DeviceWeight, loras=(None, None, None), eps: float = 1e-5, ctx=None):
+        self.ctx = ctx or default_context()
+        self.norm_w, self.w = _f32c(norm_w, "norm_w"), (gate, up, down)
+        self.loras = [None if l is None else lora_struct(*l) for l in loras]
+        self.ranks = [0 if l is None else l[2] for l in loras]
+        self.hidden, self.inter = down.rows, gate.rows
+        b = MlpBlock()
+        b.hidden, b.inter, b.eps = self.hidden, self.inter, eps
+        b.norm_w = norm_w.data_ptr()
+        b.gate, b.up, b.down = gate.struct(), up.struct(), down.struct()
+        b.gate_lora, b.up_lora, b.down_lora = [
+            C.pointer(l) if l is not None else C.POINTER(Lora)() for l in self.loras]
+        self.s = b
+
+    def new_cache(self, seq: int, device="cuda:0") -> dict:
+        e = lambda n: torch.empty(seq, n, device=device)  # noqa: E731
+        c = dict(x_mid=e(self.hidden), xn=e(self.hidden), gate=e(self.inter),
+                 up=e(self.inter), act=e(self.inter))
+        for name, r in zip(("t1_gate", "t1_up", "t1_down"), self.ranks):
+            c[name] = e(r) if r else None
+        return c
+
+    @staticmethod
+    def _cs(c: dict) -> MlpCache:
+        s = MlpCache()
+        for k in ("x_mid", "xn", "gate", "up", "act", "t1_gate", "t1_up", "t1_down"):
+            setattr(s, k, None if c[k] is None else c[k].data_ptr())
+        return s
+
+    def forward(self, x: torch.Tensor, cache: dict) -> torch.Tensor:
+        """x (seq, hidden) is updated in place: x + mlp(rmsnorm(x))."""
+        _f32c(x, "x")
+        cs = self._cs(cache)
+        check(self.ctx.lib.qh_mlp_forward_dev(self.ctx.h, C.byref(self.s), _p(x), x.shape[0],
+                                              C.byref(cs), C.c_void_p(_stream())))
+        return x
+
+    def backward(self, cache: dict, dx_out: torch.Tensor):
+        """-> (dx_in, [(grad_a, grad_b) or None for gate, up, down]); the
+        cache's gate and up buffers are consumed."""
+        _f32c(dx_out, "dx_out")
+        seq = dx_out.shape[0]
+        dx_in = torch.empty_like(dx_out)
+        grads, ga, gb = [], (C.c_void_p * 3)(), (C.c_void_p * 3)()
+        for i, (l, w) in enumerate(zip(self.loras, self.w)):
+            if l is None:
+                grads.append(None)
+                continue
+            a = torch.empty(l.r * w.cols, device=dx_out.device)
+            b = torch.empty(w.rows * l.r, device=dx_out.device)
+            ga[i], gb[i] = a.data_ptr(), b.data_ptr()
+            grads.append((a, b))
+        cs = self._cs(cache)
+        check(self.ctx.lib.qh_mlp_backward_dev(self.ctx.h, C.byref(self.s), C.byref(cs),
+                                               _p(dx_out), seq, _p(dx_in), ga, gb,
+                                               C.c_void_p(_stream())))
+        return dx_in, grads
