@@ -556,6 +556,45 @@ def glue_bench(args, ctx, torch, dev, QD):
     return out
 
 
+def mlp_block_bench(args, ctx, torch, dev, QD):
+    """The device-resident MLP block (qh_mlp_forward_dev + _backward_dev:
+    RMSNorm, gate/up/down QLoRA projections, SwiGLU, residual add) fwd+bwd
+    at 2048 tokens, SmolLM-135M shapes (r=8) and 70B-class shapes (r=64).
+    Flops are the three projections' fwd+bwd (4MNK + 6Mr(K+N) each); the
+    glue's bytes are left out of the rate."""
+    g = torch.Generator(device="cuda").manual_seed(0x3141)
+    out = {}
+    T = 2048
+    for name, H, F, r, reps in (("smollm135m", 576, 1536, 8, 10), ("70b", 8192, 28672, 64, 3)):
+        Ws, loras, flops = [], [], 0
+        for N, K in ((F, H), (F, H), (H, F)):
+            w = torch.randn(N, K, device=dev, generator=g) * 0.02
+            Ws.append(QD.DeviceWeight.quantize(w, 64, True, ctx=ctx))
+            del w
+            a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) / math.sqrt(K)
+            b = torch.randn(N, r, device=dev, generator=g) * 0.01
+            loras.append((a, b, r, 16.0))
+            flops += 4 * T * N * K + 6 * T * r * (K + N)
+        norm = torch.rand(H, device=dev, generator=g) + 0.5
+        blk = QD.MLPBlock(norm, *Ws, loras=loras, eps=1e-5, ctx=ctx)
+        x = torch.randn(T, H, device=dev, generator=g)
+        dy = torch.randn(T, H, device=dev, generator=g)
+        c = blk.new_cache(T)
+
+        def step():
+            blk.forward(x.clone(), c)
+            blk.backward(c, dy)
+        ms = _timed_ms(torch, step, reps)
+        out[name] = dict(workload=f"MLP block fwd+bwd, hidden {H}, mlp {F}, r={r}, {T} tokens",
+                         ms=ms, flops=flops, tflops=flops / (ms * 1e9),
+                         frac_fp32_peak=flops / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS)
+        print(f"# mlp block {name}: {ms:.2f} ms, {flops / (ms * 1e9):.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
+        del blk, Ws, loras, c, x, dy
+        torch.cuda.empty_cache()
+    return out
+
+
 def load_bench(args, ctx, torch, dev, QD):
     """Weights into HBM from the host, C5's 28672x8192 layer: the packed
     NF4 file image (pinned host memory, parsed and copied part by part into
@@ -738,6 +777,7 @@ def main():
     if not args.skip_glue:
         glue = glue_bench(args, ctx, torch, dev, QD)
     load = None if args.skip_extra else load_bench(args, ctx, torch, dev, QD)
+    mlp = None if args.skip_extra else mlp_block_bench(args, ctx, torch, dev, QD)
     cpu_dec = cpu_pre = None
     if not args.no_cpu_baseline:
         cpu_dec = cpu_baseline_decode(args.cpu_seconds)
@@ -788,6 +828,7 @@ def main():
         "configs": extra,
         "block_glue": glue,
         "weight_load": load,
+        "mlp_block": mlp,
     }
     print(json.dumps(line))
 
