@@ -433,8 +433,7 @@ int g_t128_min = 256;
 // Tile shape by problem size: 128x128 for big outputs, 64x64 otherwise.
 template <int AF, int AE, int BF, int BE, int B2F>
 hipError_t pick(const GemmArgs &g, float *partial, hipStream_t s) {
-  if (g.M >= 128 && g.N >= 128 && (g.M / 128) * (g.N / 128) >= g_t128_min)
-    return run<128, 128, 2, AF, AE, BF, BE, B2F>(g, partial, s);
+  if (gemm_uses_t128(g.M, g.N)) return run<128, 128, 2, AF, AE, BF, BE, B2F>(g, partial, s);
   return run<64, 64, 2, AF, AE, BF, BE, B2F>(g, partial, s);
 }
 
@@ -447,6 +446,10 @@ hipError_t pick_ae(const GemmArgs &g, float *partial, hipStream_t s) {
 }  // namespace
 
 bool nf4_fast_ok(const DevQW &w) { return w.bs == 64 && w.cols % 64 == 0; }
+
+bool gemm_uses_t128(int64_t M, int64_t N) {
+  return M >= 128 && N >= 128 && (M / 128) * (N / 128) >= g_t128_min;
+}
 
 void set_gemm_t128_min(int t) {
   if (t > 0) g_t128_min = t;

@@ -88,6 +88,8 @@ hipError_t launch_dequantize(const DevQW &w, float *out, hipStream_t s);
 // ---- k_gemm.hip ----
 // Runs the tile engine; splits > 1 needs `partial` (splits * M * N floats)
 // and reduces into args.C deterministically.
+// True when the tile engine runs (M x N) on 128x128 tiles (else 64x64).
+bool gemm_uses_t128(int64_t M, int64_t N);
 hipError_t launch_gemm(const GemmArgs &args, float *partial, hipStream_t s);
 // Tile-engine eligibility of a quantized B operand: block_size 64 and
 // whole blocks per row of the reduction form.

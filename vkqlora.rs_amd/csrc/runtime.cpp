@@ -346,14 +346,33 @@ GemmArgs gemm_args(int64_t M, int64_t N, int64_t K, Operand A, Operand B,
 }
 
 // Split-K factor for outputs that cover too few tiles to fill 256 CUs.
+// Split-K of the LoRA-rank GEMMs (one side r <= 64): each workgroup's K loop
+// is a chain of dependent 32-wide steps whose loads the tile engine hides
+// only one step ahead, so a skinny GEMM is paced by load latency.  Split K
+// until about 4 workgroups per CU (1024) run, each keeping >= 4 steps.
 int choose_splits(int64_t M, int64_t N, int64_t K) {
   int64_t tiles = div_ceil(M, 64) * div_ceil(N, 64);
   if (M >= 128 && N >= 128 && (M / 128) * (N / 128) >= 64) return 1;
   if (tiles >= 256) return 1;
-  int64_t sp = 512 / (tiles ? tiles : 1);
+  int64_t sp = 1024 / (tiles ? tiles : 1);
   if (sp > 32) sp = 32;
-  int64_t kmax = K / 256;
+  int64_t kmax = K / 128;
   if (sp > kmax) sp = kmax;
+  return sp < 1 ? 1 : (int)sp;
+}
+
+// Split-K of the base NF4 GEMMs (forward, grad_x) on 64x64 tiles: at C4's
+// shapes (2048 tokens, 576-1536 features) 96-768 tiles leave most CUs with
+// one workgroup that walks 18-48 dependent K steps.  Same target as above,
+// at most 8 splits and 64 MB of partial sums.
+int base_splits(int64_t M, int64_t N, int64_t K) {
+  if (qh::gemm_uses_t128(M, N)) return 1;
+  const int64_t tiles = div_ceil(M, 64) * div_ceil(N, 64);
+  if (tiles >= 1024) return 1;
+  int64_t sp = div_ceil(1024, tiles ? tiles : 1);
+  if (sp > 8) sp = 8;
+  if (sp > K / 128) sp = K / 128;
+  while (sp > 1 && (size_t)(sp * M * N * 4) > ((size_t)64 << 20)) --sp;
   return sp < 1 ? 1 : (int)sp;
 }
 
@@ -445,11 +464,12 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
                     nullptr, r, 1.0f);
     gt1.splits = choose_splits(M, r, K);
   }
+  const int y_splits = base_splits(M, N, K);
   Carve c;
   size_t i_t1 = c.add(lora && !t1_out ? (size_t)M * r * 4 : 0);
   size_t i_w32 = c.add(fast ? 0 : (size_t)W.n * 4);
   size_t i_p1 = c.add(lora ? partial_floats(gt1) * 4 : 0);
-  size_t i_p2 = c.add(0);
+  size_t i_p2 = c.add(y_splits > 1 ? (size_t)y_splits * M * N * 4 : 0);
   auto p = c.bind(ctx->scratch);
   float *t1 = lora ? (t1_out ? t1_out : (float *)p[i_t1]) : nullptr;
 
@@ -473,8 +493,8 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     gm.A2 = op(t1, r, qh::ROWK, qh::E_F32);
     gm.B2 = op(l->b, r, qh::ROWK, qh::E_F32, sc);
   }
-  (void)i_p2;
-  timed(ctx, "forward_gemm", s, [&] { return qh::launch_gemm(gm, nullptr, s); });
+  gm.splits = y_splits;
+  timed(ctx, "forward_gemm", s, [&] { return qh::launch_gemm(gm, (float *)p[i_p2], s); });
 }
 
 // ---- fused backward on device pointers ----------------------------------
@@ -515,6 +535,8 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   size_t i_p2 = c.add(lora ? partial_floats(gds) * 4 : 0);
   size_t i_p3 = c.add(lora ? partial_floats(ggb) * 4 : 0);
   size_t i_p4 = c.add(lora ? partial_floats(gga) * 4 : 0);
+  const int gx_splits = M > 0 ? base_splits(M, K, N) : 1;
+  size_t i_p5 = c.add(gx_splits > 1 ? (size_t)gx_splits * M * K * 4 : 0);
   auto p = c.bind(ctx->scratch);
 
   const float *t1 = nullptr;
@@ -556,7 +578,8 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     gm.A2 = op(ds, r, qh::ROWK, qh::E_F32);
     gm.B2 = op(l->a, K, qh::KROW, qh::E_F32);
   }
-  timed(ctx, "grad_x_gemm", s, [&] { return qh::launch_gemm(gm, nullptr, s); });
+  gm.splits = gx_splits;
+  timed(ctx, "grad_x_gemm", s, [&] { return qh::launch_gemm(gm, (float *)p[i_p5], s); });
 }
 
 // Plain GEMMs (gpu_matmul*): C = A.B, A^T.B, A.B^T.
