@@ -321,7 +321,8 @@ typedef struct qh_mlp_cache {
 QH_API qh_status qh_mlp_forward_dev(qh_ctx *ctx, const qh_mlp_block *blk,
                                     float *d_x, size_t seq,
                                     const qh_mlp_cache *cache, void *stream);
-/* dx_in = dL/d(block input) from dx_out = dL/d(block output); adapter
+/* dx_in = dL/d(block input) from dx_out = dL/d(block output) (separate
+ * buffers: dx_out is read after dx_in is first written); adapter
  * gradients in gate, up, down order (d_grad_a[i]: r x in, d_grad_b[i]:
  * out x r), entries of projections without an adapter are ignored. */
 QH_API qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *blk,

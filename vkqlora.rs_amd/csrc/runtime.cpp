@@ -1481,6 +1481,8 @@ qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *b, const qh_mlp_c
   qh_status st = validate_mlp(b);
   if (st != QH_OK) return st;
   if ((st = validate_cache(b, c)) != QH_OK) return st;
+  if (d_dx_in == d_dx_out && seq > 0)
+    return fail(QH_ERR_INVALID_CONFIG, "dx_in must not alias dx_out (read at the end)");
   const qh_lora *ls[3] = {b->gate_lora, b->up_lora, b->down_lora};
   for (int i = 0; i < 3; ++i)
     if (ls[i] && (!d_grad_a || !d_grad_b || !d_grad_a[i] || !d_grad_b[i]))
