@@ -90,6 +90,24 @@ def test_prefill_shape_parity(ctx, QD, act):
     assert all(v < tol for v in e.values()), e
 
 
+@pytest.mark.parametrize("N,K,r,M,act", [
+    (576, 576, 8, 100, torch.float32),     # C4/C1 class: T1 and Ds on the rank kernel
+    (192, 576, 33, 70, torch.bfloat16),    # r past one 32-column block, bf16 X and dY
+    (576, 1024, 64, 33, torch.float32),    # largest K and r the rank kernel takes
+    (640, 320, 1, 40, torch.bfloat16),     # rank 1
+    (256, 200, 16, 50, torch.float32),     # K not a multiple of 8 (fp32 weight path)
+    (1536, 576, 8, 64, torch.float32),     # Ds over N = 1536: the tile engine again
+])
+def test_rank_gemm_shapes_parity(ctx, QD, N, K, r, M, act):
+    _say(f"rank-gemm shapes N={N} K={K} r={r} M={M} act={act}")
+    d = _setup(QD, ctx, N, K, r, M, SEED ^ (N * 31 + K), act)
+    rows = sorted({0, 1, M // 2, M - 1})
+    e = _run(QD, ctx, d, N, K, r, M, 8.0, rows)
+    tol = TOL_F32 if act == torch.float32 else TOL_BF16
+    _say(e)
+    assert all(v < tol for v in e.values()), e
+
+
 @pytest.mark.parametrize("N,K", [(11008, 4096), (4096, 11008)])
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_decode_shape_forward_parity(ctx, QD, N, K, M):

@@ -1,0 +1,170 @@
+// k_rank.hip -- the LoRA-rank GEMMs whose output is (rows x r), r <= 64:
+//   T1 = X . A^T        (qlora.rs:95, 141; lora.rs:94-102)
+//   Ds = s * dY . B     (qlora.rs:143, 149)
+// out[m][j] = alpha * sum_k P[m][k] * Q(j, k), P (M x K) row-major in fp32
+// or bf16, Q either A (r x K, Q(j,k) = q[j * ldq + k]) or B (K x r,
+// Q(j,k) = q[k * ldq + j]).
+//
+// At training shapes these are skinny (r = 8..64 columns, K = 192..1024):
+// the tile engine's 64x64 tiles waste most of each MFMA and walk K in
+// dependent 32-wide steps, so they ran 10-15 us each at C4's shapes.  Here a
+// workgroup of 8 waves owns 32 rows and every wave one eighth of K, so each
+// wave's chain is short; the eight partial tiles are summed through LDS in
+// wave order (no split-K, no second launch).
+//
+// v_mfma_f32_32x32x2f32 takes, per lane l, one A value A[l % 32][k_l] and one
+// B value B[k_l][l % 32] with k_l one of the step's two reduction indices
+// (lanes 0-31 and 32-63).  The reduction order is free, so chunk t of 8 k
+// values gives lane half g = l / 32 the indices 8t + 4g + e for the chunk's
+// four steps e = 0..3: a lane's four A values are one float4 of its row.
+#include "qh_internal.h"
+
+namespace qh {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kRankWaves = 8;
+constexpr int kRankThreads = kRankWaves * 64;
+constexpr int kRankRows = 32;
+constexpr int kRankUnroll = 4;  // chunks of 8 k loaded before their MFMAs
+
+__device__ __forceinline__ float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
+
+template <int QF, int PE, int NB>
+__global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
+    const void *__restrict__ P, int64_t ldp, const float *__restrict__ Q, int64_t ldq,
+    float *__restrict__ out, int64_t ldo, int64_t M, int64_t K, int r, float alpha) {
+  __shared__ float red[kRankWaves][kRankRows][32 * NB + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int64_t m0 = (int64_t)blockIdx.x * kRankRows;
+  const int64_t row = m0 + l32;
+  const bool row_ok = row < M;
+  // this wave's K range, whole chunks of 8
+  const int64_t chunks = (K + 7) / 8;
+  const int64_t c0 = chunks * wv / kRankWaves, c1 = chunks * (wv + 1) / kRankWaves;
+
+  floatx16 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+
+  auto load_p = [&](int64_t k, float (&p)[4]) {
+    // P[row][k .. k+3], zero past the row's end or K
+    if (PE == E_F32) {
+      const float *pr = (const float *)P + row * ldp;
+      if (row_ok && k + 3 < K && (((uintptr_t)(pr + k)) & 15) == 0) {
+        const float4 v = *(const float4 *)(pr + k);
+        p[0] = v.x; p[1] = v.y; p[2] = v.z; p[3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = (row_ok && k + e < K) ? pr[k + e] : 0.0f;
+      }
+    } else {
+      const uint16_t *pr = (const uint16_t *)P + row * ldp;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[e] = (row_ok && k + e < K) ? bf16f(pr[k + e]) : 0.0f;
+    }
+  };
+  auto load_q = [&](int b, int64_t k, float (&q)[4]) {
+    const int j = b * 32 + l32;
+    const bool j_ok = j < r;
+    if (QF == 0) {
+      const float *qr = Q + (int64_t)j * ldq;
+      if (j_ok && k + 3 < K && (((uintptr_t)(qr + k)) & 15) == 0) {
+        const float4 v = *(const float4 *)(qr + k);
+        q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = (j_ok && k + e < K) ? qr[k + e] : 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = (j_ok && k + e < K) ? Q[(k + e) * ldq + j] : 0.0f;
+    }
+  };
+
+  for (int64_t c = c0; c < c1; c += kRankUnroll) {
+    float p[kRankUnroll][4], q[kRankUnroll][NB][4];
+#pragma unroll
+    for (int u = 0; u < kRankUnroll; ++u) {
+      const int64_t k = (c + u) * 8 + 4 * g;
+      const bool live = c + u < c1;
+      if (live) {
+        load_p(k, p[u]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load_q(b, k, q[u][b]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[u][e] = 0.0f;
+#pragma unroll
+          for (int b = 0; b < NB; ++b) q[u][b][e] = 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRankUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(p[u][e], q[u][b][e], acc[b], 0, 0, 0);
+  }
+
+  // D layout of the 32x32 MFMA: value v of lane l is row 8(v/4) + 4g + v%4,
+  // column l % 32
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      red[wv][8 * (v / 4) + 4 * g + (v % 4)][b * 32 + l32] = acc[b][v];
+  __syncthreads();
+  for (int e = tid; e < kRankRows * 32 * NB; e += kRankThreads) {
+    const int rr = e / (32 * NB), j = e % (32 * NB);
+    const int64_t m = m0 + rr;
+    if (m >= M || j >= r) continue;
+    float s = red[0][rr][j];
+#pragma unroll
+    for (int w = 1; w < kRankWaves; ++w) s += red[w][rr][j];
+    out[m * ldo + j] = alpha * s;
+  }
+}
+
+}  // namespace
+
+// Measured against the split-K tile engine: faster up to K = 1024 (C4's
+// 576-wide T1 and Ds), slower beyond (K = 1536: 20 against 14 us; K = 4096:
+// 72 against 32 us), where each wave's K loop waits on its loads every
+// kRankUnroll chunks and the tile engine's 4+ workgroups per CU hide more.
+bool rank_gemm_ok(int64_t K, int64_t r) { return r >= 1 && r <= 64 && K >= 1 && K <= 1024; }
+
+hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float *Q, int q_kmajor,
+                            int64_t ldq, float *out, int64_t ldo, int64_t M, int64_t K, int64_t r,
+                            float alpha, hipStream_t s) {
+  if (M == 0 || r == 0) return hipSuccess;
+  const dim3 grid((unsigned)((M + kRankRows - 1) / kRankRows)), block(kRankThreads);
+  const int ri = (int)r;
+#define QH_RANK(QF, PE, NB)                                                                    \
+  return qh_launch(k_rank_gemm<QF, PE, NB>, grid, block, 0, s, P, ldp, Q, ldq, out, ldo, M, K, \
+                   ri, alpha)
+  if (r <= 32) {
+    if (q_kmajor) {
+      if (p_bf16) QH_RANK(1, E_BF16, 1);
+      QH_RANK(1, E_F32, 1);
+    }
+    if (p_bf16) QH_RANK(0, E_BF16, 1);
+    QH_RANK(0, E_F32, 1);
+  }
+  if (q_kmajor) {
+    if (p_bf16) QH_RANK(1, E_BF16, 2);
+    QH_RANK(1, E_F32, 2);
+  }
+  if (p_bf16) QH_RANK(0, E_BF16, 2);
+  QH_RANK(0, E_F32, 2);
+#undef QH_RANK
+}
+
+}  // namespace qh

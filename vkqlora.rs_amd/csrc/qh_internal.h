@@ -201,4 +201,12 @@ hipError_t launch_softmax_ce(const float *logits, const uint32_t *targets, int64
                              int64_t vocab, float *loss, float *dlogits, float *terms,
                              hipStream_t s);
 
+// LoRA-rank GEMMs with an (M x r) output, r <= 64, K <= 1024 (k_rank.hip):
+// out[m][j] = alpha * sum_k P[m][k] Q(j, k); P row-major (ldp) in fp32 or
+// bf16; Q(j, k) = q[j * ldq + k] (q_kmajor = 0) or q[k * ldq + j] (1).
+bool rank_gemm_ok(int64_t K, int64_t r);
+hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float *Q, int q_kmajor,
+                            int64_t ldq, float *out, int64_t ldo, int64_t M, int64_t K, int64_t r,
+                            float alpha, hipStream_t s);
+
 }  // namespace qh

@@ -459,10 +459,11 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   }
 
   GemmArgs gt1{}, gm{};
+  const bool t1_rank = lora && qh::rank_gemm_ok(K, r);
   if (lora) {
     gt1 = gemm_args(M, r, K, op(x, K, qh::ROWK, xe), op(l->a, K, qh::ROWK, qh::E_F32),
                     nullptr, r, 1.0f);
-    gt1.splits = choose_splits(M, r, K);
+    gt1.splits = t1_rank ? 1 : choose_splits(M, r, K);
   }
   const int y_splits = base_splits(M, N, K);
   Carve c;
@@ -473,7 +474,11 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   auto p = c.bind(ctx->scratch);
   float *t1 = lora ? (t1_out ? t1_out : (float *)p[i_t1]) : nullptr;
 
-  if (lora) {
+  if (lora && t1_rank) {
+    timed(ctx, "t1_gemm", s, [&] {
+      return qh::launch_rank_gemm(x, xe == qh::E_BF16, K, l->a, 0, K, t1, r, M, K, r, 1.0f, s);
+    });
+  } else if (lora) {
     gt1.C = t1;
     timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(gt1, (float *)p[i_p1], s); });
   }
@@ -510,14 +515,16 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   if (K == 0) return;
 
   GemmArgs gt1{}, gds{}, ggb{}, gga{};
+  const bool t1_rank = lora && qh::rank_gemm_ok(K, r);
+  const bool ds_rank = lora && qh::rank_gemm_ok(N, r);
   if (lora) {
     gt1 = gemm_args(M, r, K, op(x, K, qh::ROWK, ae), op(l->a, K, qh::ROWK, qh::E_F32),
                     nullptr, r, 1.0f);
-    gt1.splits = choose_splits(M, r, K);
+    gt1.splits = t1_rank ? 1 : choose_splits(M, r, K);
     // Ds = s * dY . B   (qlora.rs:143,149)
     gds = gemm_args(M, r, N, op(dy, N, qh::ROWK, ae), op(l->b, r, qh::KROW, qh::E_F32),
                     nullptr, r, sc);
-    gds.splits = choose_splits(M, r, N);
+    gds.splits = ds_rank ? 1 : choose_splits(M, r, N);
     // grad_B = (s * dY)^T . T1  (qlora.rs:147)
     ggb = gemm_args(N, r, M, op(dy, N, qh::KROW, ae), op(nullptr, r, qh::KROW, qh::E_F32),
                     gb, r, sc);
@@ -544,14 +551,27 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   if (lora) {
     if (t1_in) {
       t1 = t1_in;
+    } else if (t1_rank) {
+      float *t1w = (float *)p[i_t1];
+      timed(ctx, "t1_gemm", s, [&] {
+        return qh::launch_rank_gemm(x, ae == qh::E_BF16, K, l->a, 0, K, t1w, r, M, K, r, 1.0f,
+                                    s);
+      });
+      t1 = t1w;
     } else {
       gt1.C = (float *)p[i_t1];
       timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(gt1, (float *)p[i_p1], s); });
       t1 = gt1.C;
     }
     ds = (float *)p[i_ds];
-    gds.C = ds;
-    timed(ctx, "ds_gemm", s, [&] { return qh::launch_gemm(gds, (float *)p[i_p2], s); });
+    if (ds_rank) {
+      timed(ctx, "ds_gemm", s, [&] {
+        return qh::launch_rank_gemm(dy, ae == qh::E_BF16, N, l->b, 1, r, ds, r, M, N, r, sc, s);
+      });
+    } else {
+      gds.C = ds;
+      timed(ctx, "ds_gemm", s, [&] { return qh::launch_gemm(gds, (float *)p[i_p2], s); });
+    }
     if (M > 0) {
       ggb.B.p = t1;
       timed(ctx, "grad_b_gemm", s, [&] { return qh::launch_gemm(ggb, (float *)p[i_p3], s); });
