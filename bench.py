@@ -323,7 +323,7 @@ def prefill_bench(args, ctx, torch, dev, QD, act_dtype):
     ms = e0.elapsed_time(e1) / steps
     rep = ctx.timing_report(reset=True)
     ctx.set_timing(False)
-    flops = 4 * M * N * K + 6 * M * r * (K + N)
+    flops = 4 * M * N * K + 6 * M * r * (K + N)  # fwd 2MNK + 2Mr(K+N), bwd 2MNK + 4Mr(K+N)
     kern = {k: dict(launches=v[0], avg_ms=v[1] / max(v[0], 1)) for k, v in rep.items()}
     fwd_flops = 2 * M * N * K + 2 * M * r * N
     fk = kern.get("forward_gemm")
@@ -754,7 +754,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the hot path shards by tokens, see DESIGN.md); run with --gpus 1",
+              "(the hot path would shard by tokens, one process per GPU); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
     import torch

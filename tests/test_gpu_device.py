@@ -1,5 +1,5 @@
 """GPU parity of the device-resident entry points (``*_dev``) at the
-BASELINE shapes: bf16 activations, the T1 cache handed from forward to
+benchmark configurations' shapes: bf16 activations, the T1 cache handed from forward to
 backward, and full-size size-independent checks.
 
 Outputs are compared with the oracle on sampled rows (every output row is
