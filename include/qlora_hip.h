@@ -294,6 +294,20 @@ QH_API qh_status qh_softmax_cross_entropy_dev(qh_ctx *ctx,
                                               float *d_loss, float *d_dlogits,
                                               void *stream);
 
+/* ---- library-owned device weights ----------------------------------------
+ * A packed weight uploaded once and kept in HBM (the device-resident form a
+ * model stack holds; the reference re-uploads W on every call,
+ * qlora-wgpu/src/kernels.rs:60-75, 268-276).  The view is a qh_qweight of
+ * device pointers for the *_dev entry points; it stays valid until
+ * qh_dweight_destroy, which must come before the context's destroy. */
+typedef struct qh_dweight qh_dweight;
+/* Allocates HBM, copies the host weight (validated like qh_qweight
+ * everywhere else) and waits for the copy. */
+QH_API qh_status qh_weight_upload(qh_ctx *ctx, const qh_qweight *host,
+                                  qh_dweight **out);
+QH_API qh_status qh_dweight_view(const qh_dweight *w, qh_qweight *view);
+QH_API void qh_dweight_destroy(qh_dweight *w);
+
 /* ---- a decoder block's MLP on device ----------------------------------------
  * The MLP half of `block_forward` / `block_backward` (qlora-model/src/
  * llama.rs:449-463, 543-565) with its three projections as QLoRA layers

@@ -194,3 +194,22 @@ def test_block_glue_validation_messages():
     # valid arguments reach the context check
     assert L.qh_swiglu_backward(None, x, x, x, 4, x, x) == 3
     assert _err(L) == "gpu error: context is NULL"
+
+
+def test_weight_upload_validation():
+    L = qlora_hip.load()
+    q = QWeight()
+    q.rows, q.cols, q.block_size, q.scale_kind = 2, 64, 64, 0
+    h = C.c_void_p(123)
+    assert L.qh_weight_upload(None, C.byref(q), None) == 1
+    q.block_size = 0
+    assert L.qh_weight_upload(None, C.byref(q), C.byref(h)) == 2
+    assert h.value is None
+    q.block_size = 64
+    assert L.qh_weight_upload(None, C.byref(q), C.byref(h)) == 1  # NULL parts
+    w = np.zeros(128, np.float32)
+    q.codes = w.ctypes.data
+    q.scales = w.ctypes.data
+    assert L.qh_weight_upload(None, C.byref(q), C.byref(h)) == 3
+    assert L.qh_last_error().decode() == "gpu error: context is NULL"
+    L.qh_dweight_destroy(None)

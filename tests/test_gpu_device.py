@@ -249,3 +249,37 @@ def test_70b_layer_forward_backward_sampled(ctx, QD):
                          r, alpha, xs, len(rows))
     e = nerr(y.cpu().numpy()[rows].ravel(), yo, K, xs, wd)
     assert e < TOL_F32, e
+
+
+def test_library_owned_weight_handle(ctx, QD):
+    """qh_weight_upload keeps a packed weight in HBM; its view drives the
+    device entry points like any device qh_qweight."""
+    import ctypes as C
+    from qlora_hip._lib import QWeight
+    from qlora_hip.api import qweight_struct
+    N, K, r, M = 256, 512, 8, 40
+    g = O.Rng(SEED ^ 0x77)
+    w = g.normal(N * K, 0.02)
+    q = O.quantize(w)
+    q.update(rows=N, cols=K)
+    hs = qweight_struct(q)
+    h = C.c_void_p()
+    QD.check(ctx.lib.qh_weight_upload(ctx.h, C.byref(hs), C.byref(h)))
+    try:
+        v = QWeight()
+        QD.check(ctx.lib.qh_dweight_view(h, C.byref(v)))
+        out = torch.empty(N * K, device="cuda:0")
+        QD.check(ctx.lib.qh_dequantize_dev(ctx.h, C.byref(v), QD._p(out), None))
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), O.dequantize(q).view(np.uint32))
+        a, b = g.uniform(r * K, -0.04, 0.04), g.normal(N * r, 0.01)
+        x = g.normal(M * K)
+        y = torch.empty(M, N, device="cuda:0")
+        lora = QD.lora_struct(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), r, 16.0)
+        QD.forward(None, lora, torch.from_numpy(x).cuda().view(M, K), M, y, ctx=ctx, qw=v)
+        torch.cuda.synchronize()
+        wd = O.dequantize(q)
+        yo = O.qlora_forward(wd, N, K, a, b, r, 16.0, x, M)
+        assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
+    finally:
+        ctx.lib.qh_dweight_destroy(h)

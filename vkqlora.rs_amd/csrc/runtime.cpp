@@ -200,6 +200,12 @@ void drain_timing(qh_ctx *c) {
 
 }  // namespace
 
+struct qh_dweight {
+  qh_ctx *ctx;
+  qh_qweight view;  // device pointers
+  void *codes = nullptr, *scales = nullptr, *absmax = nullptr;
+};
+
 struct ParamStateDev {
   size_t numel = 0, nb = 0;
   uint8_t *m_codes = nullptr, *v_codes = nullptr;
@@ -1541,6 +1547,64 @@ qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *b, const qh_mlp_c
     });
     return QH_OK;
   });
+}
+
+// ---- library-owned device weights ---------------------------------------------
+qh_status qh_weight_upload(qh_ctx *ctx, const qh_qweight *host, qh_dweight **out) {
+  if (!out) return fail(QH_ERR_SHAPE_MISMATCH, "out is NULL");
+  *out = nullptr;
+  qh_status st = validate_weight(host);
+  if (st != QH_OK) return st;
+  const bool dq = host->scale_kind == QH_SCALES_DQ_INT8;
+  const size_t n = host->rows * host->cols, nb = div_ceil(n, host->block_size);
+  if (n && (!host->codes || (dq ? (!host->scale_codes || !host->absmax) : !host->scales)))
+    return fail(QH_ERR_SHAPE_MISMATCH, "a part of the host weight is NULL");
+  qh_dweight *d = new (std::nothrow) qh_dweight();
+  if (!d) return fail(QH_ERR_GPU, "host allocation failed");
+  d->ctx = ctx;
+  st = guarded(ctx, [&] {
+    const size_t cb = div_ceil(n, 2), sb = dq ? nb : nb * 4, ab = dq ? div_ceil(nb, 256) * 4 : 0;
+    check(hipMalloc(&d->codes, cb ? cb : 1), "hipMalloc codes");
+    check(hipMalloc(&d->scales, sb ? sb : 1), "hipMalloc scales");
+    if (dq) check(hipMalloc(&d->absmax, ab ? ab : 4), "hipMalloc absmax");
+    hipStream_t s = ctx->stream;
+    if (cb) check(hipMemcpyAsync(d->codes, host->codes, cb, hipMemcpyHostToDevice, s), "upload");
+    if (sb)
+      check(hipMemcpyAsync(d->scales, dq ? (const void *)host->scale_codes : host->scales, sb,
+                           hipMemcpyHostToDevice, s), "upload");
+    if (ab) check(hipMemcpyAsync(d->absmax, host->absmax, ab, hipMemcpyHostToDevice, s), "upload");
+    check(hipStreamSynchronize(s), "sync");
+    return QH_OK;
+  });
+  if (st != QH_OK) {
+    qh_dweight_destroy(d);
+    return st;
+  }
+  d->view = *host;
+  d->view.codes = (const uint8_t *)d->codes;
+  d->view.scales = dq ? nullptr : (const float *)d->scales;
+  d->view.scale_codes = dq ? (const uint8_t *)d->scales : nullptr;
+  d->view.absmax = dq ? (const float *)d->absmax : nullptr;
+  *out = d;
+  return QH_OK;
+}
+
+qh_status qh_dweight_view(const qh_dweight *w, qh_qweight *view) {
+  if (!w || !view) return fail(QH_ERR_SHAPE_MISMATCH, "weight handle or view is NULL");
+  *view = w->view;
+  return QH_OK;
+}
+
+void qh_dweight_destroy(qh_dweight *w) {
+  if (!w) return;
+  if (w->ctx) {
+    std::lock_guard<std::mutex> lk(w->ctx->mu);
+    (void)hipSetDevice(w->ctx->device);
+    if (w->codes) (void)hipFree(w->codes);
+    if (w->scales) (void)hipFree(w->scales);
+    if (w->absmax) (void)hipFree(w->absmax);
+  }
+  delete w;
 }
 
 }  // extern "C"

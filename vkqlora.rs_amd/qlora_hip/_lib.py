@@ -43,6 +43,7 @@ EXPORTED = [
     "qh_softmax_cross_entropy", "qh_softmax_cross_entropy_dev",
     "qh_nf4_file_size", "qh_nf4_file_write", "qh_nf4_file_count", "qh_nf4_file_entry",
     "qh_nf4_file_find", "qh_weight_upload_dev", "qh_mlp_forward_dev", "qh_mlp_backward_dev",
+    "qh_weight_upload", "qh_dweight_view", "qh_dweight_destroy",
 ]
 
 
@@ -171,6 +172,10 @@ def load() -> C.CDLL:
         L.qh_nf4_file_entry.argtypes = [vp, sz, sz, C.c_char_p, sz, C.POINTER(QWeight)]
         L.qh_nf4_file_find.argtypes = [vp, sz, C.c_char_p, C.POINTER(QWeight)]
         L.qh_weight_upload_dev.argtypes = [vp, C.POINTER(QWeight), vp, vp, vp, vp, vp]
+        L.qh_weight_upload.argtypes = [vp, C.POINTER(QWeight), C.POINTER(vp)]
+        L.qh_dweight_view.argtypes = [vp, C.POINTER(QWeight)]
+        L.qh_dweight_destroy.argtypes = [vp]
+        L.qh_dweight_destroy.restype = None
         L.qh_mlp_forward_dev.argtypes = [vp, C.POINTER(MlpBlock), vp, sz,
                                          C.POINTER(MlpCache), vp]
         L.qh_mlp_backward_dev.argtypes = [vp, C.POINTER(MlpBlock), C.POINTER(MlpCache), vp,
