@@ -93,10 +93,12 @@ def test_prefill_shape_parity(ctx, QD, act):
 @pytest.mark.parametrize("N,K,r,M,act", [
     (576, 576, 8, 100, torch.float32),     # C4/C1 class: T1 and Ds on the rank kernel
     (192, 576, 33, 70, torch.bfloat16),    # r past one 32-column block, bf16 X and dY
-    (576, 1024, 64, 33, torch.float32),    # largest K and r the rank kernel takes
+    (576, 1024, 64, 33, torch.float32),    # r = 64: four 16-column blocks
+    (192, 2048, 64, 37, torch.float32),    # the largest K the rank kernel takes
     (640, 320, 1, 40, torch.bfloat16),     # rank 1
-    (256, 200, 16, 50, torch.float32),     # K not a multiple of 8 (fp32 weight path)
-    (1536, 576, 8, 64, torch.float32),     # Ds over N = 1536: the tile engine again
+    (256, 200, 16, 50, torch.float32),     # K not a multiple of 16 (fp32 weight path)
+    (1536, 576, 8, 64, torch.float32),     # Ds over N = 1536
+    (256, 2560, 16, 40, torch.float32),    # T1 past K = 2048: the tile engine again
 ])
 def test_rank_gemm_shapes_parity(ctx, QD, N, K, r, M, act):
     _say(f"rank-gemm shapes N={N} K={K} r={r} M={M} act={act}")

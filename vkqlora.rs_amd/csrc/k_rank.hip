@@ -5,51 +5,53 @@
 // or bf16, Q either A (r x K, Q(j,k) = q[j * ldq + k]) or B (K x r,
 // Q(j,k) = q[k * ldq + j]).
 //
-// At training shapes these are skinny (r = 8..64 columns, K = 192..1024):
+// At training shapes these are skinny (r = 8..64 columns, K = 192..2048):
 // the tile engine's 64x64 tiles waste most of each MFMA and walk K in
 // dependent 32-wide steps, so they ran 10-15 us each at C4's shapes.  Here a
-// workgroup of 8 waves owns 32 rows and every wave one eighth of K, so each
+// workgroup of 8 waves owns 16 rows and every wave one eighth of K, so each
 // wave's chain is short; the eight partial tiles are summed through LDS in
 // wave order (no split-K, no second launch).
 //
-// v_mfma_f32_32x32x2f32 takes, per lane l, one A value A[l % 32][k_l] and one
-// B value B[k_l][l % 32] with k_l one of the step's two reduction indices
-// (lanes 0-31 and 32-63).  The reduction order is free, so chunk t of 8 k
-// values gives lane half g = l / 32 the indices 8t + 4g + e for the chunk's
-// four steps e = 0..3: a lane's four A values are one float4 of its row.
+// v_mfma_f32_16x16x4f32 takes, per lane l, one A value A[l % 16][k_l] and one
+// B value B[k_l][l % 16] with k_l one of the step's four reduction indices
+// (lane quarters 0-15, 16-31, 32-47, 48-63).  The reduction order is free,
+// so chunk t of 16 k values gives lane quarter g = l / 16 the indices
+// 16t + 4g + e for the chunk's four steps e = 0..3: a lane's four A values
+// are one float4 of its row.
 #include "qh_internal.h"
 
 namespace qh {
 namespace {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kRankWaves = 8;
 constexpr int kRankThreads = kRankWaves * 64;
-constexpr int kRankRows = 32;
-constexpr int kRankUnroll = 4;  // chunks of 8 k loaded before their MFMAs
+constexpr int kRankRows = 16;
+constexpr int kRankUnroll = 4;  // chunks of 16 k loaded before their MFMAs
 
 __device__ __forceinline__ float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
 
+// NB blocks of 16 output columns (r <= 16 * NB)
 template <int QF, int PE, int NB>
 __global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
     const void *__restrict__ P, int64_t ldp, const float *__restrict__ Q, int64_t ldq,
     float *__restrict__ out, int64_t ldo, int64_t M, int64_t K, int r, float alpha) {
-  __shared__ float red[kRankWaves][kRankRows][32 * NB + 1];
+  __shared__ float red[kRankWaves][kRankRows][16 * NB + 1];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int l32 = lane & 31, g = lane >> 5;
+  const int l16 = lane & 15, g = lane >> 4;
   const int64_t m0 = (int64_t)blockIdx.x * kRankRows;
-  const int64_t row = m0 + l32;
+  const int64_t row = m0 + l16;
   const bool row_ok = row < M;
-  // this wave's K range, whole chunks of 8
-  const int64_t chunks = (K + 7) / 8;
+  // this wave's K range, whole chunks of 16
+  const int64_t chunks = (K + 15) / 16;
   const int64_t c0 = chunks * wv / kRankWaves, c1 = chunks * (wv + 1) / kRankWaves;
 
-  floatx16 acc[NB];
+  floatx4 acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[b][v] = 0.0f;
+    for (int v = 0; v < 4; ++v) acc[b][v] = 0.0f;
 
   auto load_p = [&](int64_t k, float (&p)[4]) {
     // P[row][k .. k+3], zero past the row's end or K
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
     }
   };
   auto load_q = [&](int b, int64_t k, float (&q)[4]) {
-    const int j = b * 32 + l32;
+    const int j = b * 16 + l16;
     const bool j_ok = j < r;
     if (QF == 0) {
       const float *qr = Q + (int64_t)j * ldq;
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
     float p[kRankUnroll][4], q[kRankUnroll][NB][4];
 #pragma unroll
     for (int u = 0; u < kRankUnroll; ++u) {
-      const int64_t k = (c + u) * 8 + 4 * g;
+      const int64_t k = (c + u) * 16 + 4 * g;
       const bool live = c + u < c1;
       if (live) {
         load_p(k, p[u]);
@@ -111,19 +113,18 @@ __global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
       for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-          acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(p[u][e], q[u][b][e], acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[u][e], q[u][b][e], acc[b], 0, 0, 0);
   }
 
-  // D layout of the 32x32 MFMA: value v of lane l is row 8(v/4) + 4g + v%4,
-  // column l % 32
+  // D layout of the 16x16x4 MFMA: value v of lane l is row 4(l/16) + v,
+  // column l % 16
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
-      red[wv][8 * (v / 4) + 4 * g + (v % 4)][b * 32 + l32] = acc[b][v];
+    for (int v = 0; v < 4; ++v) red[wv][4 * g + v][b * 16 + l16] = acc[b][v];
   __syncthreads();
-  for (int e = tid; e < kRankRows * 32 * NB; e += kRankThreads) {
-    const int rr = e / (32 * NB), j = e % (32 * NB);
+  for (int e = tid; e < kRankRows * 16 * NB; e += kRankThreads) {
+    const int rr = e / (16 * NB), j = e % (16 * NB);
     const int64_t m = m0 + rr;
     if (m >= M || j >= r) continue;
     float s = red[0][rr][j];
@@ -135,11 +136,11 @@ __global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
 
 }  // namespace
 
-// Measured against the split-K tile engine: faster up to K = 1024 (C4's
-// 576-wide T1 and Ds), slower beyond (K = 1536: 20 against 14 us; K = 4096:
-// 72 against 32 us), where each wave's K loop waits on its loads every
-// kRankUnroll chunks and the tile engine's 4+ workgroups per CU hide more.
-bool rank_gemm_ok(int64_t K, int64_t r) { return r >= 1 && r <= 64 && K >= 1 && K <= 1024; }
+// Measured against the split-K tile engine: faster up to K = 2048 (C4's
+// 576- and 1536-long T1 and Ds: 5-10 against 9-12 us), slower at K = 4096
+// (C3's T1: 52 against 31 us), where a wave's K loop waits on its loads
+// every kRankUnroll chunks and the tile engine's split-K has more waves.
+bool rank_gemm_ok(int64_t K, int64_t r) { return r >= 1 && r <= 64 && K >= 1 && K <= 2048; }
 
 hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float *Q, int q_kmajor,
                             int64_t ldq, float *out, int64_t ldo, int64_t M, int64_t K, int64_t r,
@@ -150,20 +151,21 @@ hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float 
 #define QH_RANK(QF, PE, NB)                                                                    \
   return qh_launch(k_rank_gemm<QF, PE, NB>, grid, block, 0, s, P, ldp, Q, ldq, out, ldo, M, K, \
                    ri, alpha)
+#define QH_RANK_NB(NB)                       \
+  if (q_kmajor) {                            \
+    if (p_bf16) QH_RANK(1, E_BF16, NB);      \
+    QH_RANK(1, E_F32, NB);                   \
+  }                                          \
+  if (p_bf16) QH_RANK(0, E_BF16, NB);        \
+  QH_RANK(0, E_F32, NB);
+  if (r <= 16) {
+    QH_RANK_NB(1)
+  }
   if (r <= 32) {
-    if (q_kmajor) {
-      if (p_bf16) QH_RANK(1, E_BF16, 1);
-      QH_RANK(1, E_F32, 1);
-    }
-    if (p_bf16) QH_RANK(0, E_BF16, 1);
-    QH_RANK(0, E_F32, 1);
+    QH_RANK_NB(2)
   }
-  if (q_kmajor) {
-    if (p_bf16) QH_RANK(1, E_BF16, 2);
-    QH_RANK(1, E_F32, 2);
-  }
-  if (p_bf16) QH_RANK(0, E_BF16, 2);
-  QH_RANK(0, E_F32, 2);
+  QH_RANK_NB(4)
+#undef QH_RANK_NB
 #undef QH_RANK
 }
 

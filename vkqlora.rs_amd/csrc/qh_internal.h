@@ -201,7 +201,7 @@ hipError_t launch_softmax_ce(const float *logits, const uint32_t *targets, int64
                              int64_t vocab, float *loss, float *dlogits, float *terms,
                              hipStream_t s);
 
-// LoRA-rank GEMMs with an (M x r) output, r <= 64, K <= 1024 (k_rank.hip):
+// LoRA-rank GEMMs with an (M x r) output, r <= 64, K <= 2048 (k_rank.hip):
 // out[m][j] = alpha * sum_k P[m][k] Q(j, k); P row-major (ldp) in fp32 or
 // bf16; Q(j, k) = q[j * ldq + k] (q_kmajor = 0) or q[k * ldq + j] (1).
 bool rank_gemm_ok(int64_t K, int64_t r);
