@@ -134,6 +134,76 @@ __global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
   }
 }
 
+// The LoRA-rank GEMMs that reduce over the tokens (qlora.rs:147, 151):
+//   grad_B = s * dY^T . T1   (N x r)      grad_A = Ds^T . X   (r x K)
+// out(c, j) = alpha * sum_m Big[m][c] * Small[m][j], Big (M x C) row-major in
+// fp32 or bf16, Small (M x r) fp32; stored at out[c * ldo + j] (OT = 0) or
+// out[j * ldo + c] (OT = 1).  A workgroup owns 16 columns c and all r, its
+// 8 waves split the tokens; lane quarter g takes tokens 16t + 4g + e, so a
+// lane's four A values are four rows of one column, coalesced across the
+// quarter's 16 lanes.
+template <int OT, int PE, int NB>
+__global__ __launch_bounds__(kRankThreads) void k_rank_tgemm(
+    const void *__restrict__ Big, int64_t ldb, const float *__restrict__ Small, int64_t lds,
+    float *__restrict__ out, int64_t ldo, int64_t M, int64_t C, int r, float alpha) {
+  __shared__ float red[kRankWaves][16][16 * NB + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 16;
+  const int64_t col = c0 + l16;
+  const bool col_ok = col < C;
+  const int64_t chunks = (M + 15) / 16;
+  const int64_t t0 = chunks * wv / kRankWaves, t1 = chunks * (wv + 1) / kRankWaves;
+  floatx4 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[b][v] = 0.0f;
+  for (int64_t t = t0; t < t1; t += kRankUnroll) {
+    float p[kRankUnroll][4], q[kRankUnroll][NB][4];
+#pragma unroll
+    for (int u = 0; u < kRankUnroll; ++u) {
+      const int64_t m = (t + u) * 16 + 4 * g;
+      const bool live = t + u < t1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = live && m + e < M;
+        if (PE == E_F32)
+          p[u][e] = (ok && col_ok) ? ((const float *)Big)[(m + e) * ldb + col] : 0.0f;
+        else
+          p[u][e] = (ok && col_ok) ? bf16f(((const uint16_t *)Big)[(m + e) * ldb + col]) : 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int j = b * 16 + l16;
+          q[u][b][e] = (ok && j < r) ? Small[(m + e) * lds + j] : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRankUnroll; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[u][e], q[u][b][e], acc[b], 0, 0, 0);
+  }
+  // row i of the 16x16 D (a column c of the output), column j
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wv][4 * g + v][b * 16 + l16] = acc[b][v];
+  __syncthreads();
+  for (int e = tid; e < 16 * 16 * NB; e += kRankThreads) {
+    const int ci = e / (16 * NB), j = e % (16 * NB);
+    const int64_t c = c0 + ci;
+    if (c >= C || j >= r) continue;
+    float s = red[0][ci][j];
+#pragma unroll
+    for (int w = 1; w < kRankWaves; ++w) s += red[w][ci][j];
+    out[OT ? (int64_t)j * ldo + c : c * ldo + j] = alpha * s;
+  }
+}
+
 }  // namespace
 
 // Measured against the split-K tile engine: faster up to K = 2048 (C4's
@@ -167,6 +237,40 @@ hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float 
   QH_RANK_NB(4)
 #undef QH_RANK_NB
 #undef QH_RANK
+}
+
+}  // namespace qh
+
+namespace qh {
+
+// Measured against the split-K tile engine at C4's shapes (2048 tokens).
+bool rank_tgemm_ok(int64_t M, int64_t r) { return r >= 1 && r <= 64 && M >= 1 && M <= 2048; }
+
+hipError_t launch_rank_tgemm(const void *Big, int big_bf16, int64_t ldb, const float *Small,
+                             int64_t lds, float *out, int64_t ldo, int out_t, int64_t M,
+                             int64_t C, int64_t r, float alpha, hipStream_t s) {
+  if (C == 0 || r == 0) return hipSuccess;
+  const dim3 grid((unsigned)((C + 15) / 16)), block(kRankThreads);
+  const int ri = (int)r;
+#define QH_RT(OT, PE, NB)                                                                     \
+  return qh_launch(k_rank_tgemm<OT, PE, NB>, grid, block, 0, s, Big, ldb, Small, lds, out, \
+                   ldo, M, C, ri, alpha)
+#define QH_RT_NB(NB)                    \
+  if (out_t) {                          \
+    if (big_bf16) QH_RT(1, E_BF16, NB); \
+    QH_RT(1, E_F32, NB);                \
+  }                                     \
+  if (big_bf16) QH_RT(0, E_BF16, NB);   \
+  QH_RT(0, E_F32, NB);
+  if (r <= 16) {
+    QH_RT_NB(1)
+  }
+  if (r <= 32) {
+    QH_RT_NB(2)
+  }
+  QH_RT_NB(4)
+#undef QH_RT_NB
+#undef QH_RT
 }
 
 }  // namespace qh

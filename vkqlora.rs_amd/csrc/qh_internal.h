@@ -209,4 +209,13 @@ hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float 
                             int64_t ldq, float *out, int64_t ldo, int64_t M, int64_t K, int64_t r,
                             float alpha, hipStream_t s);
 
+// The LoRA-rank GEMMs reducing over M <= 2048 tokens (k_rank.hip):
+// out(c, j) = alpha * sum_m Big[m][c] Small[m][j], Big (M x C, ldb) fp32 or
+// bf16, Small (M x r, lds) fp32; out[c * ldo + j] (out_t = 0) or
+// out[j * ldo + c] (out_t = 1).
+bool rank_tgemm_ok(int64_t M, int64_t r);
+hipError_t launch_rank_tgemm(const void *Big, int big_bf16, int64_t ldb, const float *Small,
+                             int64_t lds, float *out, int64_t ldo, int out_t, int64_t M,
+                             int64_t C, int64_t r, float alpha, hipStream_t s);
+
 }  // namespace qh

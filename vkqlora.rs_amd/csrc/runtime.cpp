@@ -578,7 +578,15 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
       gds.C = ds;
       timed(ctx, "ds_gemm", s, [&] { return qh::launch_gemm(gds, (float *)p[i_p2], s); });
     }
-    if (M > 0) {
+    if (M > 0 && qh::rank_tgemm_ok(M, r)) {
+      // grad_B (N x r) = s dY^T T1, grad_A (r x K) = Ds^T X
+      timed(ctx, "grad_b_gemm", s, [&] {
+        return qh::launch_rank_tgemm(dy, ae == qh::E_BF16, N, t1, r, gb, r, 0, M, N, r, sc, s);
+      });
+      timed(ctx, "grad_a_gemm", s, [&] {
+        return qh::launch_rank_tgemm(x, ae == qh::E_BF16, K, ds, r, ga, K, 1, M, K, r, 1.0f, s);
+      });
+    } else if (M > 0) {
       ggb.B.p = t1;
       timed(ctx, "grad_b_gemm", s, [&] { return qh::launch_gemm(ggb, (float *)p[i_p3], s); });
       gga.A.p = ds;
