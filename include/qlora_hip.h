@@ -112,6 +112,14 @@ QH_API qh_status qh_ctx_synchronize(qh_ctx *ctx);
 QH_API qh_status qh_ctx_set_timing(qh_ctx *ctx, int enable);
 QH_API qh_status qh_ctx_timing_report(qh_ctx *ctx, char *buf, size_t len,
                                       int reset);
+/* Test hooks (no counterpart in the reference): flags that force the rare
+ * paths of the kernels from the host so that tests can check them.
+ * QH_TEST_FORCE_T1_RECOMPUTE: the one-launch decode GEMV takes the path of a
+ * workgroup whose awaited T1 slices never arrive (it computes them itself),
+ * which must give the same bits as the normal path.  Products leave the
+ * flags at 0 (their value after qh_ctx_create). */
+#define QH_TEST_FORCE_T1_RECOMPUTE 1u
+QH_API qh_status qh_ctx_set_test_flags(qh_ctx *ctx, uint32_t flags);
 
 /* ---- layout helpers (quant.rs:93-100, 223-257) ------------------------- */
 QH_API size_t qh_codes_len(size_t rows, size_t cols);

@@ -16,7 +16,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# QH_ORACLE_LIB names another build of the same source (the sanitizer build
+# under tests/sanitize); by default the Makefile's liboracle.so.
+_LIB_PATH = os.environ.get("QH_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 NF4_ZERO_CODE = 7

@@ -1,0 +1,245 @@
+// Host-only harness for the packed NF4 file parser (nf4_file.cpp), built
+// with AddressSanitizer and UndefinedBehaviorSanitizer (see the Makefile
+// beside it).  It feeds the parser every truncation of a valid image, every
+// single-byte corruption of its header from a set of JSON-significant
+// bytes, corrupted header-length fields, a misaligned copy, and hand-made
+// headers with overflowing shapes, inverted or odd offsets, bad escapes and
+// bad metadata.  Every call must return a status (no crash, no sanitizer
+// report), and the cases with a known answer must give it.
+#include <cinttypes>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "qh_host.h"
+#include "qlora_hip.h"
+
+static thread_local std::string g_err;
+
+namespace qh {
+qh_status host_fail(qh_status st, const std::string &msg) {
+  g_err = msg;
+  return st;
+}
+}  // namespace qh
+
+namespace {
+
+int g_failures = 0;
+size_t g_calls = 0;
+
+void expect(bool ok, const char *what) {
+  if (!ok) {
+    fprintf(stderr, "FAILED: %s (last error: %s)\n", what, g_err.c_str());
+    ++g_failures;
+  }
+}
+
+// Runs every reader entry point over an exact-size heap copy of `img`, so
+// that any read past the end is a heap overflow the sanitizer reports.
+qh_status probe(const std::vector<uint8_t> &img, size_t offset = 0) {
+  std::unique_ptr<uint8_t[]> hold(new uint8_t[img.size() + offset + 1]);
+  uint8_t *buf = hold.get() + offset;
+  if (!img.empty()) memcpy(buf, img.data(), img.size());
+  size_t count = 0;
+  qh_status st = qh_nf4_file_count(buf, img.size(), &count);
+  ++g_calls;
+  if (st != QH_OK) return st;
+  qh_status worst = QH_OK;
+  for (size_t i = 0; i < count; ++i) {
+    char name[256];
+    qh_qweight v{};
+    qh_status s2 = qh_nf4_file_entry(buf, img.size(), i, name, sizeof name, &v);
+    ++g_calls;
+    if (s2 == QH_OK) {
+      // touch every byte of every view: a bad view would read out of bounds
+      const size_t n = v.rows * v.cols, nb = (n + v.block_size - 1) / v.block_size;
+      volatile uint32_t sink = 0;
+      for (size_t k = 0; k < (n + 1) / 2; ++k) sink = sink + v.codes[k];
+      if (v.scale_kind == QH_SCALES_F32) {
+        for (size_t k = 0; k < nb; ++k) sink = sink + (uint32_t)v.scales[k];
+      } else {
+        for (size_t k = 0; k < nb; ++k) sink = sink + v.scale_codes[k];
+        for (size_t k = 0; k < (nb + 255) / 256; ++k) sink = sink + (uint32_t)v.absmax[k];
+      }
+      s2 = qh_nf4_file_find(buf, img.size(), name, &v);
+      ++g_calls;
+    }
+    if (s2 != QH_OK) worst = s2;
+  }
+  qh_qweight v{};
+  (void)qh_nf4_file_find(buf, img.size(), "nope", &v);
+  ++g_calls;
+  return worst;
+}
+
+std::vector<uint8_t> image_of(const std::string &header, const std::vector<uint8_t> &data) {
+  std::vector<uint8_t> img(8);
+  const uint64_t hl = header.size();
+  for (int i = 0; i < 8; ++i) img[i] = (uint8_t)(hl >> (8 * i));
+  img.insert(img.end(), header.begin(), header.end());
+  img.insert(img.end(), data.begin(), data.end());
+  return img;
+}
+
+}  // namespace
+
+int main() {
+  // three weights: double-quant with a ragged last block, fp32 scales, and
+  // one with more than 256 blocks (two absmax values)
+  struct W {
+    size_t rows, cols, bs;
+    int dq;
+  } spec[] = {{3, 67, 64, 1}, {5, 64, 64, 0}, {64, 1040, 32, 1}};
+  const char *names[] = {"layers.0.mlp.down", "q_proj", "big"};
+  std::vector<std::vector<uint8_t>> bytes;
+  std::vector<std::vector<float>> floats;
+  qh_qweight ws[3] = {};
+  uint32_t seed = 12345;
+  auto rnd = [&] { return seed = seed * 1664525u + 1013904223u; };
+  for (int i = 0; i < 3; ++i) {
+    const size_t n = spec[i].rows * spec[i].cols, nb = (n + spec[i].bs - 1) / spec[i].bs;
+    bytes.emplace_back((n + 1) / 2);
+    for (auto &b : bytes.back()) b = (uint8_t)rnd();
+    ws[i].rows = spec[i].rows;
+    ws[i].cols = spec[i].cols;
+    ws[i].block_size = spec[i].bs;
+    ws[i].codes = bytes.back().data();
+    if (spec[i].dq) {
+      bytes.emplace_back(nb);
+      for (auto &b : bytes.back()) b = (uint8_t)rnd();
+      floats.emplace_back((nb + 255) / 256, 0.5f);
+      ws[i].scale_kind = QH_SCALES_DQ_INT8;
+      ws[i].scale_codes = bytes.back().data();
+      ws[i].absmax = floats.back().data();
+    } else {
+      floats.emplace_back(nb, 0.25f);
+      ws[i].scale_kind = QH_SCALES_F32;
+      ws[i].scales = floats.back().data();
+    }
+  }
+  size_t total = 0;
+  expect(qh_nf4_file_size(ws, names, 3, &total) == QH_OK, "file size");
+  std::vector<uint8_t> img(total);
+  expect(qh_nf4_file_write(ws, names, 3, img.data(), img.size()) == QH_OK, "file write");
+
+  // the image reads back, and every F32 view is aligned
+  expect(probe(img) == QH_OK, "valid image");
+  for (int i = 0; i < 3; ++i) {
+    qh_qweight v{};
+    expect(qh_nf4_file_find(img.data(), img.size(), names[i], &v) == QH_OK, "find");
+    expect(memcmp(v.codes, ws[i].codes, (v.rows * v.cols + 1) / 2) == 0, "codes round trip");
+    const float *f = v.scale_kind == QH_SCALES_F32 ? v.scales : v.absmax;
+    expect(reinterpret_cast<uintptr_t>(f) % 4 == 0, "F32 view aligned");
+  }
+
+  // every truncation
+  for (size_t len = 0; len < img.size(); ++len) {
+    std::vector<uint8_t> cut(img.begin(), img.begin() + (long)len);
+    expect(probe(cut) != QH_OK || len == img.size(), "truncated image rejected");
+  }
+
+  // every header byte replaced by each JSON-significant byte
+  uint64_t hlen = 0;
+  for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | img[i];
+  const uint8_t subs[] = {'"', '{', '}', '[', ']', ',', ':', '\\', 'u', '0', '9', '-', ' ',
+                          0x00, 0x7f, 0x80, 0xff};
+  for (size_t pos = 8; pos < 8 + hlen; ++pos)
+    for (uint8_t c : subs) {
+      std::vector<uint8_t> bad = img;
+      bad[pos] = c;
+      (void)probe(bad);
+    }
+
+  // corrupted header-length fields
+  const uint64_t lens[] = {0, 1, 7, hlen - 1, hlen + 1, img.size() - 8, img.size() - 7,
+                           (uint64_t)1 << 32, (uint64_t)1 << 63, UINT64_MAX};
+  for (uint64_t L : lens) {
+    std::vector<uint8_t> bad = img;
+    for (int i = 0; i < 8; ++i) bad[i] = (uint8_t)(L >> (8 * i));
+    expect(probe(bad) != QH_OK || L == hlen, "bad header length rejected");
+  }
+
+  // a misaligned copy: the F32 views would be misaligned, so they are refused
+  expect(probe(img, 1) == QH_ERR_MALFORMED, "misaligned image refused");
+  {
+    std::unique_ptr<uint8_t[]> hold(new uint8_t[img.size() + 1]);
+    memcpy(hold.get() + 1, img.data(), img.size());
+    qh_qweight v{};
+    expect(qh_nf4_file_find(hold.get() + 1, img.size(), "q_proj", &v) == QH_ERR_MALFORMED &&
+               g_err == "tensor \"q_proj.nf4_scales\": data is not 4-byte aligned in memory",
+           "alignment message");
+  }
+
+  // hand-made headers
+  const std::vector<uint8_t> data(4096, 0);
+  struct Case {
+    const char *header;
+    qh_status want;
+  } cases[] = {
+      // shape product overflows 64 bits
+      {R"({"__metadata__":{"w":"3,67,64"},"w.nf4_codes":{"dtype":"U8","shape":[4294967296,4294967296,16],"data_offsets":[0,101]}})",
+       QH_ERR_MALFORMED},
+      // an F32 byte count that overflows
+      {R"({"__metadata__":{"w":"2,64,64"},"w.nf4_codes":{"dtype":"U8","shape":[64],"data_offsets":[0,64]},"w.nf4_scales":{"dtype":"F32","shape":[4611686018427387905],"data_offsets":[64,68]}})",
+       QH_ERR_MALFORMED},
+      // end before start
+      {R"({"__metadata__":{"w":"2,64,64"},"w.nf4_codes":{"dtype":"U8","shape":[64],"data_offsets":[64,0]}})",
+       QH_ERR_MALFORMED},
+      // an odd offset for F32 data
+      {R"({"__metadata__":{"w":"2,64,64"},"w.nf4_codes":{"dtype":"U8","shape":[64],"data_offsets":[5,69]},"w.nf4_scales":{"dtype":"F32","shape":[2],"data_offsets":[1,9]}})",
+       QH_ERR_MALFORMED},
+      // rows * cols overflows
+      {R"({"__metadata__":{"w":"18446744073709551615,2,64"},"w.nf4_codes":{"dtype":"U8","shape":[1],"data_offsets":[0,1]}})",
+       QH_ERR_INVALID_CONFIG},
+      // a dimension past 64 bits, a missing dimension, trailing text, a sign
+      {R"({"__metadata__":{"w":"99999999999999999999999,1,1"},"w.nf4_codes":{"dtype":"U8","shape":[1],"data_offsets":[0,1]}})",
+       QH_ERR_MALFORMED},
+      {R"({"__metadata__":{"w":"3,67"},"w.nf4_codes":{"dtype":"U8","shape":[101],"data_offsets":[0,101]}})",
+       QH_ERR_MALFORMED},
+      {R"({"__metadata__":{"w":"3,67,64x"},"w.nf4_codes":{"dtype":"U8","shape":[101],"data_offsets":[0,101]}})",
+       QH_ERR_MALFORMED},
+      {R"({"__metadata__":{"w":"3,-67,64"},"w.nf4_codes":{"dtype":"U8","shape":[101],"data_offsets":[0,101]}})",
+       QH_ERR_MALFORMED},
+      // block size 0
+      {R"({"__metadata__":{"w":"3,67,0"},"w.nf4_codes":{"dtype":"U8","shape":[101],"data_offsets":[0,101]}})",
+       QH_ERR_INVALID_CONFIG},
+      // a number past 64 bits in the tensor entry, a bad escape, a lone
+      // surrogate escape, an unterminated string
+      {R"({"w.nf4_codes":{"dtype":"U8","shape":[184467440737095516160],"data_offsets":[0,1]}})",
+       QH_ERR_MALFORMED},
+      {R"({"w\q":{"dtype":"U8","shape":[1],"data_offsets":[0,1]}})", QH_ERR_MALFORMED},
+      {R"({"__metadata__":{"\ud800":"1,1,1"}})", QH_OK},
+      {R"({"__metadata__":{"w":"1,1,1)", QH_ERR_MALFORMED},
+      // parts that disagree with the shape
+      {R"({"__metadata__":{"w":"3,67,64"},"w.nf4_codes":{"dtype":"U8","shape":[100],"data_offsets":[0,100]},"w.nf4_scale_codes":{"dtype":"U8","shape":[4],"data_offsets":[100,104]},"w.nf4_absmax":{"dtype":"F32","shape":[1],"data_offsets":[104,108]}})",
+       QH_ERR_SHAPE_MISMATCH},
+      // a wrong dtype
+      {R"({"__metadata__":{"w":"2,64,64"},"w.nf4_codes":{"dtype":"F16","shape":[32],"data_offsets":[0,64]}})",
+       QH_ERR_UNSUPPORTED},
+  };
+  int ci = 0;
+  for (const Case &c : cases) {
+    std::string h = c.header;
+    while (h.size() % 8) h += ' ';
+    const qh_status got = probe(image_of(h, data));
+    if (got != c.want) {
+      fprintf(stderr, "case %d: status %d, expected %d (%s)\n", ci, (int)got, (int)c.want,
+              g_err.c_str());
+      ++g_failures;
+    }
+    ++ci;
+  }
+  // deep nesting and a huge header of spaces
+  {
+    std::string h(100000, '[');
+    (void)probe(image_of(h, data));
+    std::string sp = "{" + std::string(1 << 20, ' ') + "}";
+    expect(probe(image_of(sp, {})) == QH_OK, "spaces-only header");
+  }
+  printf("nf4 file fuzz: %zu reader calls, %d failures\n", g_calls, g_failures);
+  return g_failures ? 1 : 0;
+}

@@ -119,6 +119,43 @@ def test_layer_validation_messages():
     assert L.qh_qlora_forward(None, C.byref(w), None, xp, 8, 1, None) == 3
 
 
+def test_device_entry_points_reject_null_buffers():
+    """The *_dev entry points refuse a NULL buffer that the call would read
+    or write, before any launch (no device needed)."""
+    L = qlora_hip.load()
+    codes = np.zeros(16, np.uint8)
+    sc = np.ones(1, np.float32)
+    w = QWeight(rows=4, cols=8, block_size=64, codes=codes.ctypes.data,
+                scale_kind=0, scales=sc.ctypes.data)
+    buf = np.ones(64, np.float32)
+    bp = C.c_void_p(buf.ctypes.data)
+    lora = Lora(a=buf.ctypes.data, a_len=16, b=buf.ctypes.data, b_len=8, r=2, alpha=1)
+    fwd, bwd = L.qh_qlora_forward_dev, L.qh_qlora_backward_dev
+    assert fwd(None, C.byref(w), None, None, 0, 2, bp, None, None) == 1
+    assert _err(L) == "shape mismatch: x is NULL but holds 16 elements"
+    assert fwd(None, C.byref(w), None, bp, 0, 2, None, None, None) == 1
+    assert _err(L) == "shape mismatch: y is NULL but holds 8 elements"
+    # batch 0: nothing is read or written, so NULL buffers are fine
+    assert fwd(None, C.byref(w), None, None, 0, 0, None, None, None) == 3
+    # an adapter needs both gradient buffers
+    assert bwd(None, C.byref(w), C.byref(lora), bp, bp, 0, 2, None, bp, None, bp,
+               None) == 1
+    assert _err(L) == "shape mismatch: grad_a is NULL but holds 16 elements"
+    assert bwd(None, C.byref(w), C.byref(lora), bp, bp, 0, 2, None, bp, bp, None,
+               None) == 1
+    assert _err(L) == "shape mismatch: grad_b is NULL but holds 8 elements"
+    assert bwd(None, C.byref(w), C.byref(lora), bp, bp, 0, 2, None, None, bp, bp,
+               None) == 1
+    assert _err(L) == "shape mismatch: grad_x is NULL but holds 16 elements"
+    assert bwd(None, C.byref(w), None, bp, None, 0, 2, None, bp, None, None, None) == 1
+    assert _err(L) == "shape mismatch: dy is NULL but holds 8 elements"
+    # without an adapter the backward does not read x
+    assert bwd(None, C.byref(w), None, None, bp, 0, 2, None, bp, None, None, None) == 3
+    lora.a = 0
+    assert fwd(None, C.byref(w), C.byref(lora), bp, 0, 2, bp, None, None) == 1
+    assert _err(L) == "shape mismatch: the adapter's A or B is NULL"
+
+
 def test_adam_config_validation():
     L = qlora_hip.load()
     cfg = AdamConfig()

@@ -1,0 +1,166 @@
+"""GPU parity at the full sizes of the benchmark's workloads: every shape
+``bench.py`` reports a rate for is also compared with the oracle here.
+
+* configuration 3: 4096x4096 and 14336x4096 layers, r = 64, 4096 tokens,
+  fp32 and bf16 activations, forward + backward (qlora-core/src/qlora.rs:86-165);
+* configuration 5: 28672x8192 and 8192x28672 layers, r = 64, 2048 tokens,
+  forward + backward, and the 8-bit Adam step over the four adapter tensors
+  (optim.rs:164-248), bit-exact;
+* the device MLP block at 70B-class shapes (hidden 8192, MLP 28672, r = 64,
+  2048 tokens; llama.rs:449-463, 543-565);
+* the backward above 2048 tokens, where grad_A and grad_B leave the
+  token-reduction rank kernel for the split-K tile engine.
+
+Y, dX and the MLP block's outputs are compared on sampled rows (each row is
+an independent reduction, so the oracle on those rows gives exactly those
+rows); T1, grad_A and grad_B in full.  At configuration 5 sizes the oracle's
+weight is the library's dequantization, which the quantize tests pin bit
+for bit against the oracle at the same size.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_layer import run_layer, say, setup_layer
+from parity import SEED, TOL_BF16, TOL_F32
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def QD(ctx):
+    from qlora_hip import device
+    return device
+
+
+def _check(e, tol):
+    say(e)
+    assert all(v < tol for v in e.values()), e
+
+
+@pytest.mark.parametrize("N", [4096, 14336])
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_config3_full_tokens(ctx, QD, N, act):
+    K, r, M, alpha = 4096, 64, 4096, 16.0
+    say(f"config 3 N={N} K={K} M={M} act={act}")
+    d = setup_layer(QD, ctx, N, K, r, M, SEED ^ 3 ^ N, act)
+    rows = [0, 1, 127, 128, 2047, 2048, 4095]
+    e = run_layer(QD, ctx, d, N, K, r, M, alpha, rows)
+    _check(e, TOL_F32 if act == torch.float32 else TOL_BF16)
+
+
+def test_backward_past_rank_kernel_tokens(ctx, QD):
+    # 2100 tokens: grad_A and grad_B take the split-K tile engine
+    N, K, r, M = 1024, 1024, 16, 2100
+    say("backward at 2100 tokens")
+    d = setup_layer(QD, ctx, N, K, r, M, SEED ^ 0x2100)
+    e = run_layer(QD, ctx, d, N, K, r, M, 32.0, [0, 1, 1050, 2047, 2048, 2099])
+    _check(e, TOL_F32)
+
+
+def _device_layer(QD, ctx, N, K, r, M, seed):
+    """Inputs drawn on the GPU (torch's generator) and copied to the host;
+    the oracle's weight is the library's bit-exact dequantization."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn(N, K, device=dev, generator=gen) * 0.02
+    W = QD.DeviceWeight.quantize(w, ctx=ctx)
+    del w
+    a = (torch.rand(r, K, device=dev, generator=gen) * 2 - 1) / np.sqrt(K)
+    b = torch.randn(N, r, device=dev, generator=gen) * 0.01
+    x = torch.randn(M, K, device=dev, generator=gen)
+    dy = torch.randn(M, N, device=dev, generator=gen)
+    h = lambda t: t.cpu().numpy().ravel()  # noqa: E731
+    wd = W.dequantize(ctx=ctx).cpu().numpy()
+    return dict(W=W, ta=a, tb=b, tx=x, tdy=dy, a=h(a), b=h(b), x=h(x), dy=h(dy)), wd
+
+
+@pytest.mark.parametrize("N,K", [(28672, 8192), (8192, 28672)])
+def test_config5_forward_backward(ctx, QD, N, K):
+    r, M, alpha = 64, 2048, 16.0
+    say(f"config 5 N={N} K={K} M={M}")
+    d, wd = _device_layer(QD, ctx, N, K, r, M, 5 + N)
+    e = run_layer(QD, ctx, d, N, K, r, M, alpha, [0, 777, 2047], wd=wd)
+    _check(e, TOL_F32)
+
+
+def _adam_dev(QH, ctx, opt, p_dev, g_dev):
+    import ctypes as C
+    cnt = len(p_dev)
+    pp = (C.c_void_p * cnt)(*[t.data_ptr() for t in p_dev])
+    gp = (C.c_void_p * cnt)(*[t.data_ptr() for t in g_dev])
+    ll = (C.c_size_t * cnt)(*[t.numel() for t in p_dev])
+    st = QH._lib.AdamStats()
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    QH._lib.check(ctx.lib.qh_adam8bit_step_dev(opt.h, pp, gp, ll, cnt, C.byref(st), stream))
+    return st
+
+
+def test_config5_adam_step_bit_exact(ctx):
+    # the four adapter tensors of the two configuration-5 layers (r = 64):
+    # 4 718 592 parameters, default PagedAdam, three steps
+    import qlora_hip as QH
+    r = 64
+    lens = [r * 8192, 28672 * r, r * 28672, 8192 * r]
+    assert sum(lens) == 4718592
+    g = O.Rng(SEED ^ 0xC5)
+    p_np = [g.normal(n, 0.05) for n in lens]
+    p_dev = [torch.from_numpy(p).cuda() for p in p_np]
+    opt = QH.Adam8bit(ctx=ctx)
+    oo = O.Adam8bit()
+    for step in range(3):
+        say(f"config 5 Adam step {step}")
+        gr_np = [g.normal(n, 0.01) for n in lens]
+        st = _adam_dev(QH, ctx, opt, p_dev, [torch.from_numpy(x).cuda() for x in gr_np])
+        pages = oo.step(p_np, gr_np)
+        torch.cuda.synchronize()
+        assert st.pages_streamed == pages == sum(lens) // 256
+        for t, p in zip(p_dev, p_np):
+            assert np.array_equal(t.cpu().numpy().view(np.uint32), p.view(np.uint32))
+    for i, n in enumerate(lens):
+        want, got = oo.state(i, n), opt.state(i, n)
+        for k in ("m_codes", "v_codes"):
+            assert np.array_equal(got[k], want[k]), (i, k)
+        for k in ("m_scales", "v_scales"):
+            assert np.array_equal(got[k].view(np.uint32), want[k].view(np.uint32)), (i, k)
+    assert opt.state_bytes() == oo.state_bytes()
+
+
+def test_mlp_block_70b_sampled_rows(ctx, QD):
+    h, f, r, alpha, eps, seq = 8192, 28672, 64, 16.0, 1e-5, 2048
+    rows = [0, 1234, 2047]
+    say("MLP block at 70B shapes")
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(70)
+    norm = torch.rand(h, device=dev, generator=gen) + 0.5
+    Ws, loras, ps = [], [], []
+    for out_dim, in_dim in ((f, h), (f, h), (h, f)):
+        w = torch.randn(out_dim, in_dim, device=dev, generator=gen) * 0.02
+        W = QD.DeviceWeight.quantize(w, ctx=ctx)
+        del w
+        a = (torch.rand(r, in_dim, device=dev, generator=gen) * 2 - 1) / np.sqrt(in_dim)
+        b = torch.randn(out_dim, r, device=dev, generator=gen) * 0.01
+        Ws.append(W)
+        loras.append((a, b, r, alpha))
+        ps.append([W.dequantize(ctx=ctx).cpu().numpy(), a.cpu().numpy().ravel(),
+                   b.cpu().numpy().ravel(), r, alpha])
+    x = torch.randn(seq, h, device=dev, generator=gen)
+    dy = torch.randn(seq, h, device=dev, generator=gen)
+    blk = QD.MLPBlock(norm, *Ws, loras=loras, eps=eps, ctx=ctx)
+    c = blk.new_cache(seq)
+    x_out = blk.forward(x.clone(), c)
+    dx, _ = blk.backward(c, dy)
+    torch.cuda.synchronize()
+    xs = x.cpu().numpy()[rows].ravel()
+    dys = dy.cpu().numpy()[rows].ravel()
+    nw = norm.cpu().numpy()
+    ref_out, cache = O.mlp_forward(nw, *ps, xs, len(rows), h, f, eps)
+    ref_dx, _ = O.mlp_backward(nw, *ps, cache, dys, len(rows), h, f, eps)
+    for what, got, ref in (("x_out", x_out, ref_out), ("dx_in", dx, ref_dx)):
+        got = got.cpu().numpy()[rows].ravel().astype(np.float64)
+        err = float(np.max(np.abs(got - ref)))
+        scale = float(np.max(np.abs(ref)))
+        say(f"{what}: max err {err:.3e} scale {scale:.3e}")
+        assert err <= 1e-4 * scale, what

@@ -255,7 +255,7 @@ def test_stream_t1_fallback_same_bits(ctx, QD, N, K, M, r):
     # slice itself with the producers' instructions and sums them in the
     # same order: forced from the host, y and T1 must equal the normal
     # path's bit for bit.
-    import os
+    from qlora_hip._lib import QH_TEST_FORCE_T1_RECOMPUTE
     g = O.Rng(SEED ^ (500 + N + K + M + r))
     dev = torch.device("cuda:0")
     w = g.normal(N * K, 0.02)
@@ -267,11 +267,11 @@ def test_stream_t1_fallback_same_bits(ctx, QD, N, K, M, r):
     _say(f"t1 fallback N={N} K={K} M={M} r={r}")
     y0, t10, rep = _forward(QD, ctx, W, lora, x, M, N, r)
     assert "decode_stream" in rep, rep
-    os.environ["QH_STREAM_T1_FALLBACK"] = "1"
+    ctx.set_test_flags(QH_TEST_FORCE_T1_RECOMPUTE)
     try:
         y1, t11, rep = _forward(QD, ctx, W, lora, x, M, N, r)
     finally:
-        del os.environ["QH_STREAM_T1_FALLBACK"]
+        ctx.set_test_flags(0)
     assert "decode_stream" in rep, rep
     assert np.array_equal(y0.cpu().numpy(), y1.cpu().numpy())
     assert np.array_equal(t10.cpu().numpy(), t11.cpu().numpy())

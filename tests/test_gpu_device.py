@@ -10,70 +10,18 @@ import numpy as np
 import pytest
 
 import oracle as O
-from parity import SEED, TOL_BF16, TOL_F32, bf16_round, nerr
+from gpu_layer import run_layer as _run, say as _say, setup_layer as _setup
+from parity import SEED, TOL_BF16, TOL_F32, nerr
 
 pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
 
 
-def _say(*a):
-    print(*a, flush=True)
-
-
 @pytest.fixture(scope="module")
 def QD(ctx):
     from qlora_hip import device
     return device
-
-
-def _setup(QD, ctx, N, K, r, M, seed, act=torch.float32):
-    g = O.Rng(seed)
-    w = g.normal(N * K, 0.02)
-    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
-    b = g.normal(N * r, 0.01)
-    x = g.normal(M * K)
-    dy = g.normal(M * N)
-    if act == torch.bfloat16:
-        x, dy = bf16_round(x), bf16_round(dy)
-    dev = torch.device("cuda:0")
-    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
-    t = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
-    return dict(w=w, a=a, b=b, x=x, dy=dy, W=W, ta=t(a), tb=t(b),
-                tx=t(x).to(act), tdy=t(dy).to(act))
-
-
-def _run(QD, ctx, d, N, K, r, M, alpha, rows):
-    dev = torch.device("cuda:0")
-    lora = QD.lora_struct(d["ta"], d["tb"], r, alpha)
-    y = torch.empty(M, N, device=dev)
-    t1 = torch.empty(M, r, device=dev)
-    gx = torch.empty(M, K, device=dev)
-    ga = torch.empty(r, K, device=dev)
-    gb = torch.empty(N, r, device=dev)
-    QD.forward(d["W"], lora, d["tx"], M, y, t1=t1, ctx=ctx)
-    QD.backward(d["W"], lora, d["tx"], d["tdy"], M, gx, ga, gb, t1=t1, ctx=ctx)
-    torch.cuda.synchronize()
-    q = O.quantize(d["w"])
-    # the device quantization is bit-exact with the oracle's
-    assert np.array_equal(d["W"].codes.cpu().numpy(), q["codes"])
-    assert np.array_equal(d["W"].scale_codes.cpu().numpy(), q["scale_codes"])
-    wd = O.dequantize(q)
-    x, dy = d["x"], d["dy"]
-    xs, dys = x.reshape(M, K)[rows].ravel(), dy.reshape(M, N)[rows].ravel()
-    yo = O.qlora_forward(wd, N, K, d["a"], d["b"], r, alpha, xs, len(rows))
-    gxo, _, _ = O.qlora_backward(wd, N, K, d["a"], d["b"], r, alpha, xs, dys, len(rows))
-    s = np.float32(alpha / r)
-    t1o = O.matmul_trans_b(x, d["a"], M, K, r)
-    ds = O.matmul(dy * s, d["b"], M, N, r)
-    gao = O.matmul_trans_a(ds, x, M, r, K)
-    gbo = O.matmul_trans_a(dy * s, t1o, M, N, r)
-    return dict(
-        y=nerr(y.cpu().numpy()[rows].ravel(), yo, K, x, wd),
-        t1=nerr(t1.cpu().numpy().ravel(), t1o, K, x, d["a"]),
-        gx=nerr(gx.cpu().numpy()[rows].ravel(), gxo, N, dy, wd),
-        ga=nerr(ga.cpu().numpy().ravel(), gao, M, ds, x),
-        gb=nerr(gb.cpu().numpy().ravel(), gbo, M, dy * s, t1o))
 
 
 @pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
@@ -223,36 +171,6 @@ def test_quantize_70b_layer_bit_exact(ctx, QD):
     assert np.array_equal(wd.view(np.uint32), O.dequantize(q).view(np.uint32))
 
 
-def test_70b_layer_forward_backward_sampled(ctx, QD):
-    # config 5's fwd+bwd (28672x8192, r=64, 2048 tokens): sampled rows,
-    # plus the size-independent linearity check y(2x) = 2 y(x)
-    N, K, M, r, alpha = 28672, 8192, 2048, 64, 16.0
-    _say("70b fwd+bwd")
-    gen = torch.Generator(device="cuda").manual_seed(7)
-    dev = torch.device("cuda:0")
-    w = torch.randn(N, K, device=dev, generator=gen) * 0.02
-    W = QD.DeviceWeight.quantize(w, ctx=ctx)
-    del w
-    a = (torch.rand(r, K, device=dev, generator=gen) * 2 - 1) / np.sqrt(K)
-    b = torch.randn(N, r, device=dev, generator=gen) * 0.01
-    x = torch.randn(M, K, device=dev, generator=gen)
-    lora = QD.lora_struct(a, b, r, alpha)
-    y = torch.empty(M, N, device=dev)
-    y2 = torch.empty(M, N, device=dev)
-    QD.forward(W, lora, x, M, y, ctx=ctx)
-    x2 = x * 2
-    QD.forward(W, lora, x2, M, y2, ctx=ctx)
-    torch.cuda.synchronize()
-    assert torch.equal(y2, 2 * y)  # scaling by 2 is exact at every step
-    rows = [0, 777, 2047]
-    wd = W.dequantize(ctx=ctx).cpu().numpy()
-    xs = x.cpu().numpy()[rows].ravel()
-    yo = O.qlora_forward(wd, N, K, a.cpu().numpy().ravel(), b.cpu().numpy().ravel(),
-                         r, alpha, xs, len(rows))
-    e = nerr(y.cpu().numpy()[rows].ravel(), yo, K, xs, wd)
-    assert e < TOL_F32, e
-
-
 def test_library_owned_weight_handle(ctx, QD):
     """qh_weight_upload keeps a packed weight in HBM; its view drives the
     device entry points like any device qh_qweight."""
@@ -285,3 +203,37 @@ def test_library_owned_weight_handle(ctx, QD):
         assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
     finally:
         ctx.lib.qh_dweight_destroy(h)
+
+
+@pytest.mark.parametrize("N,K,M", [(48, 0, 5), (0, 96, 5), (48, 96, 0)])
+def test_empty_reductions(ctx, QD, N, K, M):
+    """A layer with in_dim, out_dim or batch 0 (qlora.rs:86-165): every
+    requested output is written, zeros where the reduction is empty, T1
+    computed when out_dim alone is 0."""
+    r, alpha = 4, 8.0
+    dev = torch.device("cuda:0")
+    g = O.Rng(SEED ^ (N + 3 * K + 7 * M))
+    a, b = g.uniform(r * K, -0.1, 0.1), g.normal(N * r, 0.01)
+    x, dy = g.normal(M * K), g.normal(M * N)
+    if N * K:
+        w = g.normal(N * K, 0.02)
+        W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+        wd = O.dequantize(O.quantize(w))
+    else:
+        W = QD.DeviceWeight(N, K, 64, torch.empty(0, dtype=torch.uint8, device=dev),
+                            scale_codes=torch.empty(0, dtype=torch.uint8, device=dev),
+                            absmax=torch.empty(0, device=dev))
+        wd = np.zeros(0, np.float32)
+    t = lambda v: torch.from_numpy(v).to(dev)  # noqa: E731
+    nan = lambda *s: torch.full(s, float("nan"), device=dev)  # noqa: E731
+    lora = QD.lora_struct(t(a), t(b), r, alpha)
+    y, t1, gx, ga, gb = nan(M, N), nan(M, r), nan(M, K), nan(r, K), nan(N, r)
+    QD.forward(W, lora, t(x), M, y, t1=t1, ctx=ctx)
+    QD.backward(W, lora, t(x), t(dy), M, gx, ga, gb, ctx=ctx)
+    torch.cuda.synchronize()
+    yo = O.qlora_forward(wd, N, K, a, b, r, alpha, x, M)
+    gxo, gao, gbo = O.qlora_backward(wd, N, K, a, b, r, alpha, x, dy, M)
+    t1o = O.matmul_trans_b(x, a, M, K, r)
+    for got, want in ((y, yo), (gx, gxo), (ga, gao), (gb, gbo)):
+        assert np.array_equal(got.cpu().numpy().ravel(), want)
+    assert nerr(t1.cpu().numpy().ravel(), t1o, K, x, a) < TOL_F32

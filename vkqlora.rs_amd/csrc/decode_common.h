@@ -101,9 +101,8 @@ __device__ __forceinline__ float reduce16(float (&v)[16]) {
 
 // Device-coherent (agent scope) stores and loads: they reach the point of
 // coherence shared by all XCDs without writing back or invalidating whole
-// caches.  A producer's stores are complete once its `s_waitcnt` returns,
-// which happens before its ticket increment; a consumer loads only after
-// its own ticket increment returned the final count.
+// caches.  The partials they carry are published by `last_arrival`'s
+// release / acquire pair around the ticket.
 __device__ __forceinline__ void st_dev(float *p, float v) {
   __hip_atomic_store((unsigned *)p, __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -112,16 +111,26 @@ __device__ __forceinline__ float ld_dev(const float *p) {
   return __uint_as_float(
       __hip_atomic_load((unsigned *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
-// Ends a workgroup's partial: waits for its device stores, then takes a
-// ticket; returns true in every thread of the last of `total` workgroups,
-// which also resets the counter for the next launch.
+// Ends a workgroup's partial and takes a ticket; returns true in every
+// thread of the last of `total` workgroups, which also resets the counter
+// for the next launch.  Memory order: every thread's partial stores happen
+// before the workgroup barrier, which happens before thread 0's agent-scope
+// release fence and its ticket increment; the last arrival's increment
+// reads every earlier one, and its acquire fence, followed by the barrier,
+// orders all of them before the loads of the partials.
 __device__ __forceinline__ bool last_arrival(unsigned *counter, unsigned total, int *flag) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned old = atomicAdd(counter, 1u);
-    *flag = old == total - 1;
-    if (old == total - 1) atomicExch(counter, 0u);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const unsigned old =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == total - 1;
+    *flag = last;
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   return *flag != 0;

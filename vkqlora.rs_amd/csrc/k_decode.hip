@@ -183,29 +183,20 @@ struct BlockOps {
   uint4 xh[2], xl[2];         // A-fragments (X hi / lo) per step
 };
 
-template <int XLO, int TAB>
+template <int XLO>
 __device__ __forceinline__ void fetch_block(BlockOps &o, const uint32_t (&sw)[8], int j,
                                             const uint4 *xl, int part, int xo,
-                                            const uint32_t *tab1, const uint2 *tab2) {
+                                            const uint32_t *tab1) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int s = 2 * j + t;
     const uint32_t wd = sw[s];
-    if (TAB == 1) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint2 e = tab2[(wd >> (8 * i)) & 255u];
-        o.h[t][i] = e.x;
-        o.l[t][i] = e.y;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t t0 = tab1[(wd >> (8 * i)) & 15u];
-        const uint32_t t1 = tab1[(wd >> (8 * i + 4)) & 15u];
-        o.h[t][i] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
-        o.l[t][i] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t0 = tab1[(wd >> (8 * i)) & 15u];
+      const uint32_t t1 = tab1[(wd >> (8 * i + 4)) & 15u];
+      o.h[t][i] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+      o.l[t][i] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
     }
     o.xh[t] = xl[s * 2 * part + xo];
     o.xl[t] = XLO ? xl[s * 2 * part + part + xo] : make_uint4(0, 0, 0, 0);
@@ -233,10 +224,9 @@ __device__ __forceinline__ floatx4 mfma_block(const BlockOps &o) {
 // One line of one 16-row group: xl points at the line's staged A-fragments
 // (hi parts at [s*2*M*4], lo parts M*4 further).  The LDS operands of block
 // j+1 are requested before block j's MFMAs so their latency overlaps.
-template <int XLO, int KIND, int TAB>
+template <int XLO, int KIND>
 __device__ __forceinline__ void compute_line(const LineRegs &R, float amax, const uint4 *xl,
-                                             int M, int xo, const uint32_t *tab1,
-                                             const uint2 *tab2, floatx4 &acc) {
+                                             int M, int xo, const uint32_t *tab1, floatx4 &acc) {
   uint32_t sw[8];
   {
     auto p = __builtin_amdgcn_permlane32_swap(R.c0.x, R.c0.y, false, false);
@@ -255,10 +245,10 @@ __device__ __forceinline__ void compute_line(const LineRegs &R, float amax, cons
   const float amax127 = amax * (1.0f / 127.0f);
   const int part = M * 4;
   BlockOps ops[2];
-  fetch_block<XLO, TAB>(ops[0], sw, 0, xl, part, xo, tab1, tab2);
+  fetch_block<XLO>(ops[0], sw, 0, xl, part, xo, tab1);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if (j < 3) fetch_block<XLO, TAB>(ops[(j + 1) & 1], sw, j + 1, xl, part, xo, tab1, tab2);
+    if (j < 3) fetch_block<XLO>(ops[(j + 1) & 1], sw, j + 1, xl, part, xo, tab1);
     const floatx4 d = mfma_block<XLO>(ops[j & 1]);
     float sc;
     if (KIND == 0) {
@@ -281,7 +271,7 @@ constexpr int kSplitBatch = 8;  // slice partials loaded together
 // covers rows [16 tile, 16 tile + 16) and lines [NL slice / S, NL (slice+1) / S).
 // Dynamic LDS: the slice's A-fragments (lines * kFragsPerLine * M uint4),
 // reused by the epilogue.
-template <int XLO, int KIND, int TAB>
+template <int XLO, int KIND>
 __global__ __launch_bounds__(256) void k_dmain(DevQW w, int M, int S, const uint4 *__restrict__ xf,
                                                const float *__restrict__ t1,
                                                const float *__restrict__ lb, int r,
@@ -289,7 +279,6 @@ __global__ __launch_bounds__(256) void k_dmain(DevQW w, int M, int S, const uint
                                                unsigned *__restrict__ counters,
                                                float *__restrict__ y) {
   extern __shared__ uint4 xs[];
-  __shared__ uint2 tab2[TAB == 1 ? 256 : 1];
   __shared__ uint32_t tab1[16];
   __shared__ float lbs[16 * 64];  // rows n0.. of B (16 x r)
   __shared__ float t1s[16 * 64];  // T1 (M x r)
@@ -314,10 +303,7 @@ __global__ __launch_bounds__(256) void k_dmain(DevQW w, int M, int S, const uint
   // Every LDS fill of the prologue is a global_load_lds: an ordinary LDS
   // store here would make the compiler wait for all of them (and, in
   // issue order, for the code lines behind them).
-  if (TAB == 1)
-    copy_to_lds<true, 1>(tab2, c_tab.pair, 128);
-  else
-    copy_to_lds<false, 1>(tab1, c_tab.nib, 16);
+  copy_to_lds<false, 1>(tab1, c_tab.nib, 16);
   const int64_t per_line = kFragsPerLine * (int64_t)M;
   copy_to_lds<true, kStage>(xs, xf + SL0 * per_line, (int)(nls * per_line));
   const int nrows = (int)(N - n0 < 16 ? N - n0 : 16);
@@ -357,8 +343,8 @@ __global__ __launch_bounds__(256) void k_dmain(DevQW w, int M, int S, const uint
   for (int d = 0; d < kRing; ++d) {
     if (d < nw) {
       const float amax = ((n * KB + 4 * (wl0 + d)) >> 8) == g0 ? am0 : am1;
-      compute_line<XLO, KIND, TAB>(R[d], amax, xs + (wl0 + d - SL0) * kFragsPerLine * M, M,
-                                   xo, tab1, tab2, acc);
+      compute_line<XLO, KIND>(R[d], amax, xs + (wl0 + d - SL0) * kFragsPerLine * M, M, xo,
+                              tab1, acc);
     }
   }
 
@@ -770,16 +756,15 @@ hipError_t run_t1p(int x_bf16, const void *x, int64_t K, const float *a, int r, 
   return qh_launch(k_t1p<0, M>, grid, dim3(256), 0, st, x, K, a, r, t1p);
 }
 
-int g_decode_table = 0;     // 0 = nibble table, 1 = byte-pair table
-int g_split_target = 512;  // workgroups the K split aims for
+constexpr int kSplitTarget = 512;  // workgroups the K split aims for
 
-// Split of K over workgroups: the grid reaches g_split_target workgroups
+// Split of K over workgroups: the grid reaches kSplitTarget workgroups
 // (at most kMaxSplits slices for that), and more slices are taken while a
 // slice's staged A-fragments exceed 256 * kStage uint4 of LDS or a wave
 // would own more than kRing lines.
 int64_t decode_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t NL = K / kLine, ntiles = (N + 15) / 16;
-  int64_t s = (g_split_target + ntiles - 1) / ntiles;
+  int64_t s = (kSplitTarget + ntiles - 1) / ntiles;
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > NL) s = NL;
   if (s < 1) s = 1;
@@ -804,10 +789,7 @@ hipError_t run_main(const DevQW &w, int M, int S, const uint4 *xf, const float *
   const int64_t ntiles = (w.rows + 15) / 16;
   const dim3 grid((unsigned)(ntiles * S));
   const uint32_t lds = (uint32_t)main_lds_bytes(M, w.cols, S);
-  if (g_decode_table == 1)
-    return qh_launch(k_dmain<XLO, KIND, 1>, grid, dim3(256), lds, st, w, M, S, xf, t1, lb, r, s,
-                     part, counters, y);
-  return qh_launch(k_dmain<XLO, KIND, 0>, grid, dim3(256), lds, st, w, M, S, xf, t1, lb, r, s,
+  return qh_launch(k_dmain<XLO, KIND>, grid, dim3(256), lds, st, w, M, S, xf, t1, lb, r, s,
                    part, counters, y);
 }
 
@@ -833,10 +815,10 @@ DecodeScratch carve(void *scratch, int64_t M, int64_t N, int64_t K, int64_t r) {
 }
 
 // Small-batch split: waves own at most kRing lines and the grid aims at
-// g_split_target workgroups (at most kMaxSplits slices for that).
+// kSplitTarget workgroups (at most kMaxSplits slices for that).
 int64_t fused_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t NL = K / kLine, ntiles = (N + 15) / 16;
-  int64_t s = (g_split_target + ntiles - 1) / ntiles;
+  int64_t s = (kSplitTarget + ntiles - 1) / ntiles;
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > NL) s = NL;
   if (s < 1) s = 1;
@@ -846,8 +828,6 @@ int64_t fused_splits(int64_t M, int64_t N, int64_t K) {
 
 }  // namespace
 
-void set_decode_table(int t) { g_decode_table = t ? 1 : 0; }
-void set_decode_split_target(int t) { g_split_target = t > 0 ? t : 512; }
 
 bool decode_ok(const DevQW &w, int64_t M, int64_t r) {
   return M >= 1 && M <= 16 && r <= 64 && w.bs == 64 && w.cols % kLine == 0 &&

@@ -247,6 +247,12 @@ struct T1Slice {
   }
 };
 
+// Tagged T1 words.  A word is one 64-bit agent-scope atomic (tag << 32 |
+// value bits), stored once and read with one 64-bit atomic load, so a
+// reader that sees the expected tag sees the value stored with it: the
+// protocol needs no ordering between different words, hence no fence.  The
+// epoch counters are relaxed read-modify-writes of single locations, whose
+// modification order alone gives every launch its new epoch.
 __device__ __forceinline__ void st_dev64(uint64_t *p, uint64_t v) {
   __hip_atomic_store((unsigned long long *)p, (unsigned long long)v, __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -861,10 +867,7 @@ StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r) {
   p.sa.inv_r = r > 0 ? 1.0f / (float)r : 1.0f;
   p.sa.mact = mact;
   p.sa.t1ext = nullptr;
-  // Tests force the path a workgroup takes when published T1 slices never
-  // arrive (it must give the same bits).
-  const char *fb = getenv("QH_STREAM_T1_FALLBACK");
-  p.sa.t1_fallback = fb && atoi(fb) != 0;
+  p.sa.t1_fallback = 0;
   p.R = (int)R;
   p.KLW = (int)KLW;
   p.G = (int)G;
@@ -947,14 +950,18 @@ hipError_t launch_decode_stream_t1(const DevQW &w, const void *x, int x_bf16, in
 
 hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M, int64_t m0,
                                 const float *a, int64_t r, const float *lb, float s, float *y,
-                                float *t1_out, unsigned *tickets, hipStream_t st) {
+                                float *t1_out, unsigned *tickets, bool force_t1_recompute,
+                                hipStream_t st) {
   if (!decode_stream_ok(w, M, r) || m0 < 0 || m0 >= M || m0 % decode_stream_chunk(M) != 0)
     return hipErrorInvalidValue;
   uint64_t *epochs = (uint64_t *)(tickets + kStreamEpochWord);
   uint64_t *t1w = (uint64_t *)(tickets + kTicketWords);
   const int ri = (int)r;
   if (M <= 2) {
-    const StreamPlan p = stream_plan(w, (int)M, (int)M, r);
+    StreamPlan p = stream_plan(w, (int)M, (int)M, r);
+    // Tests force the path a workgroup takes when published T1 slices never
+    // arrive (it must give the same bits).
+    p.sa.t1_fallback = force_t1_recompute ? 1 : 0;
     if (M == 1) return dispatch_rows<1>(x_bf16, w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st);
     return dispatch_rows<2>(x_bf16, w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st);
   }

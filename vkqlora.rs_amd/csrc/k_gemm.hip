@@ -428,7 +428,7 @@ hipError_t run(const GemmArgs &g0, float *partial, hipStream_t s) {
 // 128x128 tiles from this many full tiles on: below one tile per CU the
 // 64x64 grid (4x the workgroups) measured 25-35 % faster (C4's 2048-token
 // projections), above it the same or slower.
-int g_t128_min = 256;
+constexpr int kT128Min = 256;
 
 // Tile shape by problem size: 128x128 for big outputs, 64x64 otherwise.
 template <int AF, int AE, int BF, int BE, int B2F>
@@ -448,12 +448,9 @@ hipError_t pick_ae(const GemmArgs &g, float *partial, hipStream_t s) {
 bool nf4_fast_ok(const DevQW &w) { return w.bs == 64 && w.cols % 64 == 0; }
 
 bool gemm_uses_t128(int64_t M, int64_t N) {
-  return M >= 128 && N >= 128 && (M / 128) * (N / 128) >= g_t128_min;
+  return M >= 128 && N >= 128 && (M / 128) * (N / 128) >= kT128Min;
 }
 
-void set_gemm_t128_min(int t) {
-  if (t > 0) g_t128_min = t;
-}
 
 hipError_t launch_gemm(const GemmArgs &g, float *partial, hipStream_t s) {
   if (g.M == 0 || g.N == 0) return hipSuccess;

@@ -5,7 +5,8 @@
 // Layout (a valid safetensors file; readers that convert to fp32, like
 // qlora-io's read_safetensors, still parse it):
 //   u64 LE header length, JSON header padded with spaces to a multiple of 8,
-//   then the tensors' bytes back to back in header order.
+//   then the tensors' bytes back to back in header order: every F32 tensor
+//   first, then the U8 ones, so F32 data starts 4-byte aligned.
 //   "__metadata__": {"format": "qlora-hip-nf4/1",
 //                    "<name>": "<rows>,<cols>,<block_size>", ...}
 //   "<name>.nf4_codes":       U8  [ceil(n/2)]   two codes per byte, low nibble first
@@ -14,6 +15,7 @@
 // or, for fp32 block scales,
 //   "<name>.nf4_scales":      F32 [nb]
 // with n = rows * cols and nb = ceil(n / block_size) (quant.rs:93-100).
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -244,11 +246,16 @@ qh_status tensor_view(const Header &h, const std::string &key, const char *dtype
   if (t.dtype != dtype)
     return host_fail(QH_ERR_UNSUPPORTED,
                      "tensor \"" + key + "\" has dtype " + t.dtype + ", expected " + dtype);
-  uint64_t numel = 1;
+  uint64_t numel = 1, bytes = 0;
   for (uint64_t d : t.shape)
     if (__builtin_mul_overflow(numel, d, &numel)) return malformed("tensor shape overflows");
-  if (t.end - t.start != numel * isz)
+  if (__builtin_mul_overflow(numel, (uint64_t)isz, &bytes)) return malformed("tensor shape overflows");
+  if (t.end - t.start != bytes)
     return malformed("tensor \"" + key + "\": byte range does not match its shape");
+  // the view is handed out as a typed pointer: it must be aligned for it
+  if ((reinterpret_cast<uintptr_t>(h.data + t.start) % isz) != 0)
+    return malformed("tensor \"" + key + "\": data is not " + std::to_string(isz) +
+                     "-byte aligned in memory");
   if (numel != want) {
     // from_raw_parts (quant.rs:184-197): the part lengths follow from the shape
     char m[256];
@@ -260,13 +267,31 @@ qh_status tensor_view(const Header &h, const std::string &key, const char *dtype
   return QH_OK;
 }
 
+// "<rows>,<cols>,<block_size>": three decimal integers, nothing else.
+bool parse_dims(const std::string &t, uint64_t out[3]) {
+  size_t i = 0;
+  for (int k = 0; k < 3; ++k) {
+    if (k > 0 && (i >= t.size() || t[i++] != ',')) return false;
+    const size_t start = i;
+    uint64_t v = 0;
+    for (; i < t.size() && t[i] >= '0' && t[i] <= '9'; ++i) {
+      const uint64_t d = (uint64_t)(t[i] - '0');
+      if (v > (UINT64_MAX - d) / 10) return false;
+      v = v * 10 + d;
+    }
+    if (i == start) return false;
+    out[k] = v;
+  }
+  return i == t.size();
+}
+
 qh_status view_of(const Header &h, const std::string &name, qh_qweight *out) {
   auto it = h.meta.find(name);
   if (it == h.meta.end()) return malformed("no weight \"" + name + "\" in the file");
-  unsigned long long r, c, b;
-  char tail;
-  if (sscanf(it->second.c_str(), "%llu,%llu,%llu%c", &r, &c, &b, &tail) != 3)
+  uint64_t dims[3];
+  if (!parse_dims(it->second, dims))
     return malformed("weight \"" + name + "\": metadata is not rows,cols,block_size");
+  const uint64_t r = dims[0], c = dims[1], b = dims[2];
   if (b == 0) return host_fail(QH_ERR_INVALID_CONFIG, "block_size must be > 0");
   Sizes s;
   if (!sizes_of((size_t)r, (size_t)c, (size_t)b, &s))
@@ -365,6 +390,10 @@ qh_status layout(const qh_qweight *ws, const char *const *names, size_t count,
     }
   }
   meta += '}';
+  // F32 parts ahead of the U8 ones: the data section starts 8-byte aligned
+  // and every F32 part is a whole number of floats, so each starts aligned
+  std::stable_partition(parts->begin(), parts->end(),
+                        [](const Part &p) { return std::strcmp(p.dtype, "F32") == 0; });
   std::string o = "{" + meta;
   uint64_t off = 0;
   for (const Part &p : *parts) {

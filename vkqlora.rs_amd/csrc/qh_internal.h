@@ -154,19 +154,13 @@ hipError_t launch_decode_stream_t1(const DevQW &w, const void *x, int x_bf16, in
 // The launch for rows [m0, m0 + decode_stream_chunk(M)).
 hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64_t M, int64_t m0,
                                 const float *a, int64_t r, const float *lb, float s, float *y,
-                                float *t1_out, unsigned *tickets, hipStream_t st);
-// Tuning knobs of the decode GEMV: codebook table (0 = 16-entry nibble
-// table, 1 = 256-entry byte-pair table) and the workgroup count the K split
-// aims for.
-void set_decode_table(int t);
-// Tuning knob of the tile engine: 128x128 tiles when the output holds at
-// least this many of them (else 64x64).
-void set_gemm_t128_min(int t);
-void set_decode_split_target(int t);
+                                float *t1_out, unsigned *tickets, bool force_t1_recompute,
+                                hipStream_t st);
 
 // ---- k_elem.hip ----
 hipError_t launch_axpy_inplace(float *y, const float *x, int64_t n,
                                hipStream_t s);  // y += x
+hipError_t launch_zero(float *y, int64_t n, hipStream_t s);
 hipError_t launch_bf16_to_f32(const uint16_t *x, float *y, int64_t n,
                               hipStream_t s);
 

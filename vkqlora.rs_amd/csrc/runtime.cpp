@@ -26,9 +26,6 @@ using qh::Operand;
 namespace {
 
 thread_local std::string g_err;
-// 0 = one-launch decode where it applies, else the small-batch pair, else
-// prep + main; 1 = prep + main only; 2 = no one-launch decode.
-int g_decode_path = 0;
 
 qh_status fail(qh_status st, const std::string &msg) {
   // Display formats of QloraError (qlora-core/src/error.rs:16-24).
@@ -132,6 +129,7 @@ struct qh_ctx {
   unsigned *tickets = nullptr;
   char name[256] = {0};
   bool timing = false;
+  uint32_t test_flags = 0;  // QH_TEST_* hooks
   std::vector<TimedLaunch> pending;
   std::vector<hipEvent_t> event_pool;
   std::map<std::string, std::pair<uint64_t, double>> totals;
@@ -263,6 +261,8 @@ qh_status validate_weight(const qh_qweight *w) {
 qh_status validate_lora(const qh_lora *l, size_t in_dim, size_t out_dim) {
   if (!l) return QH_OK;
   if (l->r == 0) return fail(QH_ERR_INVALID_CONFIG, "rank r must be > 0");
+  if ((l->a_len && !l->a) || (l->b_len && !l->b))
+    return fail(QH_ERR_SHAPE_MISMATCH, "the adapter's A or B is NULL");
   if (l->a_len != l->r * in_dim)
     return fail(QH_ERR_SHAPE_MISMATCH,
                 fmt("a.len() = %zu but r*in_dim = %zu", l->a_len, l->r * in_dim));
@@ -386,15 +386,48 @@ size_t partial_floats(const GemmArgs &g) {
   return g.splits > 1 ? (size_t)g.splits * g.M * g.N : 0;
 }
 
+// T1 = X . A^T (M x r) on its own (lora.rs:94-97), for the shapes where no
+// GEMM follows it.
+void t1_dev(qh_ctx *ctx, const void *x, int xe, int64_t M, int64_t K, const qh_lora *l,
+            float *t1, hipStream_t s) {
+  const int64_t r = (int64_t)l->r;
+  if (qh::rank_gemm_ok(K, r)) {
+    timed(ctx, "t1_gemm", s, [&] {
+      return qh::launch_rank_gemm(x, xe == qh::E_BF16, K, l->a, 0, K, t1, r, M, K, r, 1.0f, s);
+    });
+    return;
+  }
+  GemmArgs g = gemm_args(M, r, K, op(x, K, qh::ROWK, xe), op(l->a, K, qh::ROWK, qh::E_F32),
+                         t1, r, 1.0f);
+  g.splits = choose_splits(M, r, K);
+  Carve c;
+  size_t ip = c.add(partial_floats(g) * 4);
+  auto p = c.bind(ctx->scratch);
+  timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(g, (float *)p[ip], s); });
+}
+
+void zero_dev(float *p, size_t n, hipStream_t s) {
+  if (n) check(qh::launch_zero(p, (int64_t)n, s), "zero fill");
+}
+
 // ---- fused forward on device pointers -----------------------------------
 void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
                  int xdt, size_t batch, float *y, float *t1_out, hipStream_t s) {
   const int64_t M = (int64_t)batch, N = W.rows, K = W.cols;
-  if (M == 0 || N == 0) return;
   const bool lora = l != nullptr;
   const int64_t r = lora ? (int64_t)l->r : 0;
   const float sc = lora ? l->alpha / (float)l->r : 0.0f;  // lora.rs:64-66
   const int xe = xdt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
+  if (M == 0) return;
+  if (K == 0) {  // empty reductions: Y = 0 and T1 = 0 (qlora.rs:86-107)
+    zero_dev(y, (size_t)M * N, s);
+    if (lora && t1_out) zero_dev(t1_out, (size_t)M * r, s);
+    return;
+  }
+  if (N == 0) {  // no outputs, but the caller may still want T1
+    if (lora && t1_out) t1_dev(ctx, x, xe, M, K, l, t1_out, s);
+    return;
+  }
   const bool fast = qh::nf4_fast_ok(W);
   // Small batches: the MFMA decode kernels (batch <= 16, K % 256 == 0), else
   // the VALU GEMV (batch <= 4, K % 64 == 0).  Both take T1 = X A^T from a
@@ -418,7 +451,7 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     return;
   }
 
-  if (decode && g_decode_path == 0 && qh::decode_stream_ok(W, M, r)) {
+  if (decode && qh::decode_stream_ok(W, M, r)) {
     const int xb = xe == qh::E_BF16;
     if (M > 2 && lora)
       timed(ctx, "decode_stream_t1", s, [&] {
@@ -427,12 +460,13 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     for (int64_t m0 = 0; m0 < M; m0 += qh::decode_stream_chunk(M))
       timed(ctx, "decode_stream", s, [&] {
         return qh::launch_decode_stream(W, x, xb, M, m0, lora ? l->a : nullptr, r,
-                                        lora ? l->b : nullptr, sc, y, t1_out, ctx->tickets, s);
+                                        lora ? l->b : nullptr, sc, y, t1_out, ctx->tickets,
+                                        (ctx->test_flags & QH_TEST_FORCE_T1_RECOMPUTE) != 0, s);
       });
     return;
   }
 
-  if (decode && g_decode_path != 1 && qh::decode_small_ok(W, M, r)) {
+  if (decode && qh::decode_small_ok(W, M, r)) {
     Carve cd;
     size_t i_sc = cd.add(qh::decode_small_scratch_bytes(M, N, K, r));
     auto pd = cd.bind(ctx->scratch);
@@ -518,7 +552,17 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   const float sc = lora ? l->alpha / (float)l->r : 0.0f;
   const int ae = adt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
   const bool fast = qh::nf4_fast_ok(W);
-  if (K == 0) return;
+  // Empty reductions (qlora.rs:116-165): with in_dim = 0, T1 = 0, so
+  // grad_B = 0 and grad_x, grad_A are empty; with out_dim = 0, Ds = 0, so
+  // grad_x = 0 and grad_A = 0; with no tokens, grad_A = grad_B = 0.
+  if (K == 0 || N == 0 || M == 0) {
+    if (lora) {
+      zero_dev(gb, (size_t)N * r, s);
+      zero_dev(ga, (size_t)r * K, s);
+    }
+    zero_dev(gx, (size_t)M * K, s);
+    return;
+  }
 
   GemmArgs gt1{}, gds{}, ggb{}, gga{};
   const bool t1_rank = lora && qh::rank_gemm_ok(K, r);
@@ -548,7 +592,7 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   size_t i_p2 = c.add(lora ? partial_floats(gds) * 4 : 0);
   size_t i_p3 = c.add(lora ? partial_floats(ggb) * 4 : 0);
   size_t i_p4 = c.add(lora ? partial_floats(gga) * 4 : 0);
-  const int gx_splits = M > 0 ? base_splits(M, K, N) : 1;
+  const int gx_splits = base_splits(M, K, N);
   size_t i_p5 = c.add(gx_splits > 1 ? (size_t)gx_splits * M * K * 4 : 0);
   auto p = c.bind(ctx->scratch);
 
@@ -578,7 +622,7 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
       gds.C = ds;
       timed(ctx, "ds_gemm", s, [&] { return qh::launch_gemm(gds, (float *)p[i_p2], s); });
     }
-    if (M > 0 && qh::rank_tgemm_ok(M, r)) {
+    if (qh::rank_tgemm_ok(M, r)) {
       // grad_B (N x r) = s dY^T T1, grad_A (r x K) = Ds^T X
       timed(ctx, "grad_b_gemm", s, [&] {
         return qh::launch_rank_tgemm(dy, ae == qh::E_BF16, N, t1, r, gb, r, 0, M, N, r, sc, s);
@@ -586,17 +630,13 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
       timed(ctx, "grad_a_gemm", s, [&] {
         return qh::launch_rank_tgemm(x, ae == qh::E_BF16, K, ds, r, ga, K, 1, M, K, r, 1.0f, s);
       });
-    } else if (M > 0) {
+    } else {
       ggb.B.p = t1;
       timed(ctx, "grad_b_gemm", s, [&] { return qh::launch_gemm(ggb, (float *)p[i_p3], s); });
       gga.A.p = ds;
       timed(ctx, "grad_a_gemm", s, [&] { return qh::launch_gemm(gga, (float *)p[i_p4], s); });
-    } else {
-      check(hipMemsetAsync(gb, 0, (size_t)N * r * 4, s), "memset");
-      check(hipMemsetAsync(ga, 0, (size_t)r * K * 4, s), "memset");
     }
   }
-  if (M == 0) return;
   Operand B;
   if (fast) {
     B = op(W.codes, K, qh::KROW, qh::E_NF4);
@@ -676,10 +716,6 @@ qh_status qh_ctx_create(qh_ctx **out) {
   qh_ctx *c = new (std::nothrow) qh_ctx();
   if (!c) return fail(QH_ERR_GPU, "host allocation failed");
   if (hipGetDevice(&c->device) != hipSuccess) c->device = 0;
-  if (const char *t = getenv("QH_DECODE_TABLE")) qh::set_decode_table(atoi(t));
-  if (const char *t = getenv("QH_DECODE_SPLIT_TARGET")) qh::set_decode_split_target(atoi(t));
-  if (const char *t = getenv("QH_DECODE_PATH")) g_decode_path = atoi(t);
-  if (const char *t = getenv("QH_GEMM_T128_MIN")) qh::set_gemm_t128_min(atoi(t));
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, c->device) == hipSuccess)
     snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
@@ -731,6 +767,13 @@ qh_status qh_ctx_set_timing(qh_ctx *ctx, int enable) {
     ctx->timing = enable != 0;
     return QH_OK;
   });
+}
+
+qh_status qh_ctx_set_test_flags(qh_ctx *ctx, uint32_t flags) {
+  if (!ctx) return fail(QH_ERR_GPU, "context is NULL");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->test_flags = flags;
+  return QH_OK;
 }
 
 qh_status qh_ctx_timing_report(qh_ctx *ctx, char *buf, size_t len, int reset) {
@@ -987,6 +1030,14 @@ qh_status qh_qlora_backward(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lor
   });
 }
 
+// A device buffer that a call reads or writes must not be NULL: the kernels
+// would dereference it.  `elems` is the buffer's element count for the call.
+static qh_status need_buf(const void *p, size_t elems, const char *what) {
+  if (p == nullptr && elems != 0)
+    return fail(QH_ERR_SHAPE_MISMATCH, fmt("%s is NULL but holds %zu elements", what, elems));
+  return QH_OK;
+}
+
 qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
                                const void *d_x, int x_dtype, size_t batch, float *d_y,
                                float *d_t1, void *stream) {
@@ -995,6 +1046,10 @@ qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *
   if ((st = validate_lora(lora, w->cols, w->rows)) != QH_OK) return st;
   if (x_dtype != QH_F32 && x_dtype != QH_BF16)
     return fail(QH_ERR_INVALID_CONFIG, "x_dtype must be QH_F32 or QH_BF16");
+  if ((st = need_buf(d_x, batch * w->cols, "x")) != QH_OK ||
+      (st = need_buf(d_y, batch * w->rows, "y")) != QH_OK ||
+      (st = need_buf(w->codes, w->rows * w->cols, "the weight's codes")) != QH_OK)
+    return st;
   return guarded(ctx, [&] {
     forward_dev(ctx, make_devqw(*w), lora, d_x, x_dtype, batch, d_y, d_t1,
                 pick_stream(ctx, stream));
@@ -1011,6 +1066,16 @@ qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora 
   if ((st = validate_lora(lora, w->cols, w->rows)) != QH_OK) return st;
   if (act_dtype != QH_F32 && act_dtype != QH_BF16)
     return fail(QH_ERR_INVALID_CONFIG, "act_dtype must be QH_F32 or QH_BF16");
+  const size_t in_dim = w->cols, out_dim = w->rows, r = lora ? lora->r : 0;
+  // grad_A and grad_B are written whenever an adapter is given, even when
+  // they come out zero
+  if ((st = need_buf(d_grad_a, r * in_dim, "grad_a")) != QH_OK ||
+      (st = need_buf(d_grad_b, out_dim * r, "grad_b")) != QH_OK ||
+      (st = need_buf(d_dy, batch * out_dim, "dy")) != QH_OK ||
+      (st = need_buf(d_grad_x, batch * in_dim, "grad_x")) != QH_OK ||
+      (st = need_buf(d_x, lora ? batch * in_dim : 0, "x")) != QH_OK ||
+      (st = need_buf(w->codes, w->rows * w->cols, "the weight's codes")) != QH_OK)
+    return st;
   return guarded(ctx, [&] {
     backward_dev(ctx, make_devqw(*w), lora, d_x, d_dy, act_dtype, batch, d_t1, d_grad_x,
                  d_grad_a, d_grad_b, pick_stream(ctx, stream));

@@ -25,11 +25,12 @@ QH_SCALES_F32 = 0
 QH_SCALES_DQ_INT8 = 1
 QH_F32 = 0
 QH_BF16 = 1
+QH_TEST_FORCE_T1_RECOMPUTE = 1
 QH_MM_NN, QH_MM_TN, QH_MM_NT = 0, 1, 2
 
 EXPORTED = [
     "qh_abi_version", "qh_ctx_create", "qh_ctx_destroy", "qh_last_error",
-    "qh_ctx_device_name", "qh_ctx_synchronize", "qh_ctx_set_timing",
+    "qh_ctx_device_name", "qh_ctx_synchronize", "qh_ctx_set_timing", "qh_ctx_set_test_flags",
     "qh_ctx_timing_report", "qh_codes_len", "qh_num_blocks",
     "qh_num_absmax", "qh_storage_bytes", "qh_quantize_nf4", "qh_block_scales",
     "qh_dequantize", "qh_matmul", "qh_matmul_trans_a", "qh_matmul_trans_b",
@@ -120,6 +121,7 @@ def load() -> C.CDLL:
         L.qh_ctx_device_name.argtypes = [vp, C.c_char_p, sz]
         L.qh_ctx_synchronize.argtypes = [vp]
         L.qh_ctx_set_timing.argtypes = [vp, i32]
+        L.qh_ctx_set_test_flags.argtypes = [vp, C.c_uint32]
         L.qh_ctx_timing_report.argtypes = [vp, C.c_char_p, sz, i32]
         for fn in ("qh_codes_len", "qh_num_blocks", "qh_num_absmax"):
             getattr(L, fn).restype = sz
@@ -224,6 +226,10 @@ class Context:
 
     def set_timing(self, on: bool):
         check(self.lib.qh_ctx_set_timing(self.h, 1 if on else 0))
+
+    def set_test_flags(self, flags: int):
+        """Test hooks (QH_TEST_* flags of the C header); 0 for products."""
+        check(self.lib.qh_ctx_set_test_flags(self.h, flags))
 
     def timing_report(self, reset: bool = True) -> dict:
         """{kernel: (launches, total_ms)} of the launches timed so far."""

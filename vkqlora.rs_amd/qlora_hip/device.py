@@ -157,6 +157,8 @@ def backward(w: DeviceWeight, lora, x: torch.Tensor, dy: torch.Tensor, batch: in
     ctx = ctx or default_context()
     if x.dtype != dy.dtype:
         raise TypeError("x and dy must share a dtype")
+    if lora is not None and (ga is None or gb is None):
+        raise ValueError("grad_a and grad_b buffers are required with an adapter")
     s = qw if qw is not None else w.struct()
     check(ctx.lib.qh_qlora_backward_dev(
         ctx.h, C.byref(s), None if lora is None else C.byref(lora), _p(x), _p(dy),
