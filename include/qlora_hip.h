@@ -242,6 +242,25 @@ QH_API qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w,
                                        size_t batch, const float *d_t1,
                                        float *d_grad_x, float *d_grad_a,
                                        float *d_grad_b, void *stream);
+/* Allocation-free fused backward: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Arguments, results
+ * and kernels are those of qh_qlora_backward_dev, but its scratch (T1 when
+ * d_t1 is NULL, Ds = s.dY.B, split-K partial sums) lives in a fixed region of
+ * QH_NOALLOC_SCRATCH_BYTES that each GPU holds from the first context created
+ * on it until the process ends; the call allocates nothing.  A call that
+ * would need more scratch fails with QH_ERR_INVALID_CONFIG before any
+ * launch.  Every call on one GPU shares that GPU's region: calls that
+ * overlap on one GPU (other streams, other contexts, other threads) race,
+ * and the caller must order them.  Kernel timing (qh_ctx_set_timing) does
+ * not apply to it. */
+#define QH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+QH_API qh_status qh_qlora_backward_dev_noalloc(qh_ctx *ctx, const qh_qweight *w,
+                                               const qh_lora *lora, const void *d_x,
+                                               const void *d_dy, int act_dtype,
+                                               size_t batch, const float *d_t1,
+                                               float *d_grad_x, float *d_grad_a,
+                                               float *d_grad_b, void *stream);
 
 /* ---- the glue of a decoder block around its projections ----------------
  * qlora-model/src/llama.rs calls these between the QLoRA projections of

@@ -250,3 +250,28 @@ def test_weight_upload_validation():
     assert L.qh_weight_upload(None, C.byref(q), C.byref(h)) == 3
     assert L.qh_last_error().decode() == "gpu error: context is NULL"
     L.qh_dweight_destroy(None)
+
+
+def test_noalloc_backward_checks_before_any_launch():
+    """The allocation-free backward validates like qh_qlora_backward_dev and
+    refuses a call whose scratch exceeds its fixed region, with no device."""
+    L = qlora_hip.load()
+    codes = np.zeros(64 * 64 // 2, np.uint8)
+    sc = np.ones(64, np.float32)
+    w = QWeight(rows=64, cols=64, block_size=64, codes=codes.ctypes.data,
+                scale_kind=0, scales=sc.ctypes.data)
+    buf = np.ones(64 * 64, np.float32)
+    bp = C.c_void_p(buf.ctypes.data)
+    lora = Lora(a=buf.ctypes.data, a_len=64 * 64, b=buf.ctypes.data, b_len=64 * 64, r=64,
+                alpha=1)
+    f = L.qh_qlora_backward_dev_noalloc
+    assert f(None, C.byref(w), C.byref(lora), bp, bp, 0, 8, None, bp, None, bp, None) == 1
+    assert _err(L) == "shape mismatch: grad_a is NULL but holds 4096 elements"
+    # 300000 tokens at r = 64: T1 and Ds (2 x 76.8 MB) plus the split-K
+    # partials of grad_A and grad_B (2 x 32 splits x 64 x 64 floats)
+    assert f(None, C.byref(w), C.byref(lora), bp, bp, 0, 300000, None, bp, bp, bp,
+             None) == 2
+    assert _err(L) == ("invalid config: the call needs 154648576 bytes of scratch but the "
+                       f"allocation-free backward has {_lib.QH_NOALLOC_SCRATCH_BYTES}")
+    # within the region: reaches the context check (a GPU error without one)
+    assert f(None, C.byref(w), C.byref(lora), bp, bp, 0, 8, None, bp, bp, bp, None) == 3

@@ -1,0 +1,87 @@
+"""GPU parity of the allocation-free backward (qh_qlora_backward_dev_noalloc)
+against qh_qlora_backward_dev, through the C ABI: the same kernels with the
+scratch in the library's fixed per-GPU region, so grad_x, grad_A and grad_B
+must be the same bits.  Two calls in a row, the second smaller (the region
+keeps the first call's contents), with and without a T1 from the forward,
+fp32 and bf16 activations, split-K partials in the region; a call that
+needs more than the region is refused before any launch."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from parity import SEED
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _case(QD, ctx, N, K, r, M, seed, act):
+    dev = torch.device("cuda:0")
+    g = O.Rng(seed)
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K))
+    b = g.normal(N * r, 0.01)
+    x = torch.from_numpy(g.normal(M * K)).to(dev).view(M, K).to(act)
+    dy = torch.from_numpy(g.normal(M * N)).to(dev).view(M, N).to(act)
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r, 16.0)
+    t1 = torch.empty(M, r, device=dev)
+    QD.forward(W, lora, x, M, torch.empty(M, N, device=dev), t1=t1, ctx=ctx)
+    return W, lora, x, dy, t1
+
+
+def _backward(QD, ctx, fn, W, lora, x, dy, t1, M):
+    dev = x.device
+    N, K, r = W.rows, W.cols, lora.r
+    gx = torch.full((M, K), float("nan"), device=dev)
+    ga = torch.full((r, K), float("nan"), device=dev)
+    gb = torch.full((N, r), float("nan"), device=dev)
+    s = W.struct()
+    QD.check(fn(ctx.h, C.byref(s), C.byref(lora), QD._p(x), QD._p(dy), QD._dt(x), M,
+                QD._p(t1), QD._p(gx), QD._p(ga), QD._p(gb),
+                C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    return gx, ga, gb
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_t1", [True, False])
+def test_noalloc_backward_same_bits_two_calls(ctx, act, with_t1):
+    from qlora_hip import device as QD
+    # first: 2100 tokens (grad_A / grad_B on the split-K tile engine, partials
+    # in the region); second, smaller: a C4 down projection (grad_x split-K)
+    shapes = [(1024, 1024, 16, 2100), (576, 1536, 8, 300)]
+    for i, (N, K, r, M) in enumerate(shapes):
+        print(f"no-alloc backward call {i}: N={N} K={K} r={r} M={M} act={act} "
+              f"t1={with_t1}", flush=True)
+        W, lora, x, dy, t1 = _case(QD, ctx, N, K, r, M, SEED ^ (N + K + M), act)
+        t1p = t1 if with_t1 else None
+        want = _backward(QD, ctx, ctx.lib.qh_qlora_backward_dev, W, lora, x, dy, t1p, M)
+        got = _backward(QD, ctx, ctx.lib.qh_qlora_backward_dev_noalloc, W, lora, x, dy, t1p, M)
+        torch.cuda.synchronize()
+        for gname, gv, wv in zip(("grad_x", "grad_a", "grad_b"), got, want):
+            assert not torch.isnan(wv).any(), gname
+            assert torch.equal(gv.view(torch.int32), wv.view(torch.int32)), gname
+
+
+def test_noalloc_backward_refuses_oversized_calls(ctx):
+    from qlora_hip import device as QD
+    from qlora_hip._lib import QH_NOALLOC_SCRATCH_BYTES
+    # T1 and Ds of 300000 tokens at r = 64 need 2 x 76.8 MB of scratch
+    N, K, r, M = 64, 64, 64, 300000
+    dev = torch.device("cuda:0")
+    W = QD.DeviceWeight.quantize(torch.zeros(N, K, device=dev), ctx=ctx)
+    a = torch.zeros(r, K, device=dev)
+    b = torch.zeros(N, r, device=dev)
+    lora = QD.lora_struct(a, b, r, 8.0)
+    x = torch.zeros(1, device=dev)  # never read: the call is refused first
+    s = W.struct()
+    st = ctx.lib.qh_qlora_backward_dev_noalloc(ctx.h, C.byref(s), C.byref(lora), QD._p(x),
+                                               QD._p(x), 0, M, None, QD._p(x), QD._p(a),
+                                               QD._p(b), None)
+    assert st == 2
+    msg = ctx.lib.qh_last_error().decode()
+    assert msg.startswith("invalid config: the call needs ") and \
+        msg.endswith(f"the allocation-free backward has {QH_NOALLOC_SCRATCH_BYTES}"), msg

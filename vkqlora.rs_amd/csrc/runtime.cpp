@@ -93,14 +93,28 @@ struct Carve {
     for (size_t s : sizes) t += s;
     return t;
   }
-  std::vector<char *> bind(DevBuf &b) {
-    char *base = (char *)b.ensure(total());
+  std::vector<char *> bind(DevBuf &b) { return bind_at((char *)b.ensure(total())); }
+  std::vector<char *> bind_at(char *base) {
     std::vector<char *> out;
     for (size_t s : sizes) {
       out.push_back(base);
       base += s;
     }
     return out;
+  }
+};
+
+// Where a call's device scratch comes from: the context's growable buffer,
+// or a fixed region of known capacity (the allocation-free entry point,
+// whose callers have checked the size before any launch).
+struct ScratchSrc {
+  DevBuf *grow = nullptr;
+  char *fixed = nullptr;
+  size_t cap = 0;
+  std::vector<char *> bind(Carve &c) {
+    if (grow) return c.bind(*grow);
+    if (c.total() > cap) throw GpuError{"scratch larger than the fixed region"};
+    return c.bind_at(fixed);
   }
 };
 
@@ -130,6 +144,10 @@ struct qh_ctx {
   char name[256] = {0};
   bool timing = false;
   uint32_t test_flags = 0;  // QH_TEST_* hooks
+  // This device's copy of the allocation-free backward's scratch region
+  // (from hipGetSymbolAddress), or null with the error that prevented it.
+  void *noalloc = nullptr;
+  hipError_t noalloc_err = hipSuccess;
   std::vector<TimedLaunch> pending;
   std::vector<hipEvent_t> event_pool;
   std::map<std::string, std::pair<uint64_t, double>> totals;
@@ -543,9 +561,13 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
 }
 
 // ---- fused backward on device pointers ----------------------------------
+// With `plan_bytes` set, nothing is launched: the scratch bytes the call
+// would need are stored there.  `src` (default: the context's growable
+// buffer) provides the scratch.
 void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
                   const void *dy, int adt, size_t batch, const float *t1_in,
-                  float *gx, float *ga, float *gb, hipStream_t s) {
+                  float *gx, float *ga, float *gb, hipStream_t s,
+                  ScratchSrc *src = nullptr, size_t *plan_bytes = nullptr) {
   const int64_t M = (int64_t)batch, N = W.rows, K = W.cols;
   const bool lora = l != nullptr;
   const int64_t r = lora ? (int64_t)l->r : 0;
@@ -556,6 +578,10 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   // grad_B = 0 and grad_x, grad_A are empty; with out_dim = 0, Ds = 0, so
   // grad_x = 0 and grad_A = 0; with no tokens, grad_A = grad_B = 0.
   if (K == 0 || N == 0 || M == 0) {
+    if (plan_bytes) {
+      *plan_bytes = 0;
+      return;
+    }
     if (lora) {
       zero_dev(gb, (size_t)N * r, s);
       zero_dev(ga, (size_t)r * K, s);
@@ -594,7 +620,12 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   size_t i_p4 = c.add(lora ? partial_floats(gga) * 4 : 0);
   const int gx_splits = base_splits(M, K, N);
   size_t i_p5 = c.add(gx_splits > 1 ? (size_t)gx_splits * M * K * 4 : 0);
-  auto p = c.bind(ctx->scratch);
+  if (plan_bytes) {
+    *plan_bytes = c.total();
+    return;
+  }
+  ScratchSrc grow{&ctx->scratch, nullptr, 0};
+  auto p = (src ? *src : grow).bind(c);
 
   const float *t1 = nullptr;
   float *ds = nullptr;
@@ -695,6 +726,44 @@ qh_status guarded(qh_ctx *ctx, F &&f) {
 
 }  // namespace
 
+// ---- the allocation-free backward's scratch region --------------------------
+// One region per GPU, in the library's code object: every device the library
+// runs on holds its own copy until the process ends.  In host code the
+// array's name is only a handle for hipGetSymbolAddress, never an address:
+// kernels get the per-device address that call returns.
+static __device__ __align__(256) unsigned char scratch[QH_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// The region's address on `dev`, looked up once per device (with `dev`
+// current, as the lookup requires) and kept for every later context.
+hipError_t noalloc_region(int dev, void **out) {
+  static std::mutex mu;
+  static std::map<int, void *> addr;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = addr.find(dev);
+  if (it != addr.end()) {
+    *out = it->second;
+    return hipSuccess;
+  }
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  addr[dev] = p;
+  *out = p;
+  return hipSuccess;
+}
+
+// Timing off for the duration of a call (it would create events).
+struct NoTiming {
+  qh_ctx *c;
+  bool was;
+  explicit NoTiming(qh_ctx *ctx) : c(ctx), was(ctx->timing) { c->timing = false; }
+  ~NoTiming() { c->timing = was; }
+};
+
+}  // namespace
+
 // ===========================================================================
 extern "C" {
 
@@ -731,6 +800,10 @@ qh_status qh_ctx_create(qh_ctx **out) {
     delete c;
     return fail(QH_ERR_GPU, hipGetErrorString(e));
   }
+  // The allocation-free backward's region on this device (the device is
+  // current here); a failure is kept and reported by that entry point only.
+  c->noalloc_err = noalloc_region(c->device, &c->noalloc);
+  if (c->noalloc_err != hipSuccess) (void)hipGetLastError();
   *out = c;
   return QH_OK;
 }
@@ -1057,10 +1130,10 @@ qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *
   });
 }
 
-qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
-                                const void *d_x, const void *d_dy, int act_dtype,
-                                size_t batch, const float *d_t1, float *d_grad_x,
-                                float *d_grad_a, float *d_grad_b, void *stream) {
+static qh_status validate_backward_dev(const qh_qweight *w, const qh_lora *lora,
+                                       const void *d_x, const void *d_dy, int act_dtype,
+                                       size_t batch, float *d_grad_x, float *d_grad_a,
+                                       float *d_grad_b) {
   qh_status st = validate_weight(w);
   if (st != QH_OK) return st;
   if ((st = validate_lora(lora, w->cols, w->rows)) != QH_OK) return st;
@@ -1076,9 +1149,47 @@ qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora 
       (st = need_buf(d_x, lora ? batch * in_dim : 0, "x")) != QH_OK ||
       (st = need_buf(w->codes, w->rows * w->cols, "the weight's codes")) != QH_OK)
     return st;
+  return QH_OK;
+}
+
+qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
+                                const void *d_x, const void *d_dy, int act_dtype,
+                                size_t batch, const float *d_t1, float *d_grad_x,
+                                float *d_grad_a, float *d_grad_b, void *stream) {
+  qh_status st = validate_backward_dev(w, lora, d_x, d_dy, act_dtype, batch, d_grad_x,
+                                       d_grad_a, d_grad_b);
+  if (st != QH_OK) return st;
   return guarded(ctx, [&] {
     backward_dev(ctx, make_devqw(*w), lora, d_x, d_dy, act_dtype, batch, d_t1, d_grad_x,
                  d_grad_a, d_grad_b, pick_stream(ctx, stream));
+    return QH_OK;
+  });
+}
+
+qh_status qh_qlora_backward_dev_noalloc(qh_ctx *ctx, const qh_qweight *w, const qh_lora *lora,
+                                        const void *d_x, const void *d_dy, int act_dtype,
+                                        size_t batch, const float *d_t1, float *d_grad_x,
+                                        float *d_grad_a, float *d_grad_b, void *stream) {
+  qh_status st = validate_backward_dev(w, lora, d_x, d_dy, act_dtype, batch, d_grad_x,
+                                       d_grad_a, d_grad_b);
+  if (st != QH_OK) return st;
+  // The same plan as qh_qlora_backward_dev; its scratch must fit the region.
+  size_t need = 0;
+  backward_dev(ctx, make_devqw(*w), lora, d_x, d_dy, act_dtype, batch, d_t1, d_grad_x,
+               d_grad_a, d_grad_b, nullptr, nullptr, &need);
+  if (need > QH_NOALLOC_SCRATCH_BYTES)
+    return fail(QH_ERR_INVALID_CONFIG,
+                fmt("the call needs %zu bytes of scratch but the allocation-free backward has "
+                    "%zu",
+                    need, (size_t)QH_NOALLOC_SCRATCH_BYTES));
+  return guarded(ctx, [&] {
+    if (!ctx->noalloc)
+      throw GpuError{std::string("no scratch region on this device: ") +
+                     hipGetErrorString(ctx->noalloc_err)};
+    NoTiming nt(ctx);
+    ScratchSrc src{nullptr, (char *)ctx->noalloc, (size_t)QH_NOALLOC_SCRATCH_BYTES};
+    backward_dev(ctx, make_devqw(*w), lora, d_x, d_dy, act_dtype, batch, d_t1, d_grad_x,
+                 d_grad_a, d_grad_b, pick_stream(ctx, stream), &src);
     return QH_OK;
   });
 }

@@ -26,6 +26,7 @@ QH_SCALES_DQ_INT8 = 1
 QH_F32 = 0
 QH_BF16 = 1
 QH_TEST_FORCE_T1_RECOMPUTE = 1
+QH_NOALLOC_SCRATCH_BYTES = 64 << 20
 QH_MM_NN, QH_MM_TN, QH_MM_NT = 0, 1, 2
 
 EXPORTED = [
@@ -38,7 +39,7 @@ EXPORTED = [
     "qh_adam8bit_create", "qh_adam8bit_destroy", "qh_adam8bit_step",
     "qh_adam8bit_step_dev", "qh_adam8bit_state_bytes", "qh_adam8bit_get_state",
     "qh_quantize_nf4_dev", "qh_dequantize_dev", "qh_matmul_dev",
-    "qh_qlora_forward_dev", "qh_qlora_backward_dev",
+    "qh_qlora_forward_dev", "qh_qlora_backward_dev", "qh_qlora_backward_dev_noalloc",
     "qh_rmsnorm", "qh_rmsnorm_dev", "qh_rmsnorm_backward", "qh_rmsnorm_backward_dev",
     "qh_swiglu", "qh_swiglu_dev", "qh_swiglu_backward", "qh_swiglu_backward_dev",
     "qh_softmax_cross_entropy", "qh_softmax_cross_entropy_dev",
@@ -157,6 +158,7 @@ def load() -> C.CDLL:
                                            vp, i32, sz, vp, vp, vp]
         L.qh_qlora_backward_dev.argtypes = [vp, C.POINTER(QWeight), C.POINTER(Lora),
                                             vp, vp, i32, sz, vp, vp, vp, vp, vp]
+        L.qh_qlora_backward_dev_noalloc.argtypes = L.qh_qlora_backward_dev.argtypes
         f32 = C.c_float
         L.qh_rmsnorm.argtypes = [vp, vp, sz, vp, sz, f32, vp]
         L.qh_rmsnorm_dev.argtypes = [vp, vp, vp, sz, sz, f32, vp, vp]
