@@ -383,27 +383,58 @@ def _fwd_bwd_flops(L):
     return 4 * M * N * K + 6 * M * r * (K + N)
 
 
-def _adam_step_ms(torch, ctx, tensors, reps=3, max_resident_pages=None):
+def _adam_step_ms(torch, ctx, tensors, reps=24, max_resident_pages=None):
     """Device 8-bit Adam step over `tensors` (list of (param, grad) CUDA
-    tensors); the first step creates the state and is not timed."""
+    tensors).  The step's working set (params, grads, int8 state) is copied
+    until the copies pass 512 MB (at most 64 copies), each copy with its own
+    optimizer, and the timed steps cycle through them, so that each step's
+    data has left the 256 MB MALL.  `kernel_ms` is the Adam kernel's own
+    duration (GPU-stamped events around each launch) averaged over `reps`
+    steps; `step_ms` is the eager step between events (host launch cost
+    included).  The first step of each copy creates its state, untimed."""
     import ctypes as C
     import qlora_hip as QH
-    opt = QH.Adam8bit(lr=1e-3, max_resident_pages=max_resident_pages, ctx=ctx)
-    cnt = len(tensors)
-    pp = (C.c_void_p * cnt)(*[p.data_ptr() for p, _ in tensors])
-    gp = (C.c_void_p * cnt)(*[g_.data_ptr() for _, g_ in tensors])
-    ll = (C.c_size_t * cnt)(*[p.numel() for p, _ in tensors])
-    st = QH._lib.AdamStats()
-    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-    def step():
-        QH._lib.check(ctx.lib.qh_adam8bit_step_dev(opt.h, pp, gp, ll, cnt, C.byref(st), stream))
-    ms = _timed_ms(torch, step, reps)
     n = sum(p.numel() for p, _ in tensors)
     blocks = sum(-(-p.numel() // 256) for p, _ in tensors)
     nbytes = 16 * n + 16 * blocks
-    return dict(ms=ms, elements=n, tensors=cnt, bytes=nbytes, gbs=nbytes / (ms * 1e6),
-                frac_hbm=nbytes / (ms * 1e6) / HBM_PEAK_GBS)
+    copies = max(1, min(64, math.ceil(512e6 / nbytes)))
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sets = []
+    for i in range(copies):
+        ts = tensors if i == 0 else [(p.clone(), g_.clone()) for p, g_ in tensors]
+        opt = QH.Adam8bit(lr=1e-3, max_resident_pages=max_resident_pages, ctx=ctx)
+        cnt = len(ts)
+        sets.append(dict(
+            ts=ts, opt=opt, cnt=cnt,
+            pp=(C.c_void_p * cnt)(*[p.data_ptr() for p, _ in ts]),
+            gp=(C.c_void_p * cnt)(*[g_.data_ptr() for _, g_ in ts]),
+            ll=(C.c_size_t * cnt)(*[p.numel() for p, _ in ts])))
+    st = QH._lib.AdamStats()
+
+    def step(k):
+        S = sets[k % copies]
+        QH._lib.check(ctx.lib.qh_adam8bit_step_dev(S["opt"].h, S["pp"], S["gp"], S["ll"],
+                                                   S["cnt"], C.byref(st), stream))
+    for k in range(copies):  # state creation
+        step(k)
+    torch.cuda.synchronize()
+    reps = max(reps, copies)
+    ctx.set_timing(True)
+    ctx.timing_report(reset=True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for k in range(reps):
+        step(k)
+    e1.record()
+    torch.cuda.synchronize()
+    rep = ctx.timing_report(reset=True)
+    ctx.set_timing(False)
+    step_ms = e0.elapsed_time(e1) / reps
+    launches, total = rep.get("adam", (reps, step_ms * reps))
+    kms = total / max(launches, 1)
+    return dict(kernel_ms=kms, step_ms=step_ms, ms=kms, elements=n, tensors=len(tensors),
+                bytes=nbytes, gbs=nbytes / (kms * 1e6), frac_hbm=nbytes / (kms * 1e6) / HBM_PEAK_GBS,
+                copies=copies, rotated_bytes=copies * nbytes, reps=reps)
 
 
 def extra_bench(args, ctx, torch, dev, QD):
@@ -445,7 +476,7 @@ def extra_bench(args, ctx, torch, dev, QD):
     tens = []
     for L in Ls:
         tens += [(L["a"].clone(), L["ga"]), (L["b"].clone(), L["gb"])]
-    ad = _adam_step_ms(torch, ctx, tens, reps=5, max_resident_pages=4)
+    ad = _adam_step_ms(torch, ctx, tens, max_resident_pages=4)
     out["C4"] = dict(workload=("fwd+bwd of q/k/v/o/gate/up/down (SmolLM-135M shapes, "
                                "2048 tokens, r=8), then one 8-bit Adam step over the "
                                "14 adapter tensors"),
@@ -476,7 +507,7 @@ def extra_bench(args, ctx, torch, dev, QD):
         tens += [(L["a"].clone(), L["ga"].clone()), (L["b"].clone(), L["gb"].clone())]
         del L
         torch.cuda.empty_cache()
-    c5.update(quantize=qs, fwd_bwd=fbs, adam=_adam_step_ms(torch, ctx, tens, reps=5))
+    c5.update(quantize=qs, fwd_bwd=fbs, adam=_adam_step_ms(torch, ctx, tens))
     out["C5"] = c5
     return out
 

@@ -214,6 +214,48 @@ def test_adam_bit_exact_multi_tensor(ctx):
         assert sg["step"] == 4
 
 
+@pytest.mark.parametrize("block_size,big", [(256, 0), (512, 0), (1024, 0), (256, 1300001),
+                                            (256, 2600001)])
+def test_adam_wave_kernel_block_sizes_ragged_and_misaligned(ctx, block_size, big):
+    """Device path: ragged tensors (numel not a multiple of 4 or of the
+    block), a tensor shorter than one block, steps of thousands of blocks,
+    and a parameter tensor that is
+    not 16-byte aligned (the whole step then takes the one-element-per-thread
+    kernel); three steps bit-exact against the oracle, state included."""
+    import ctypes as C
+    import torch
+    _say(f"adam block_size={block_size} big={big}")
+    # `big` adds a tensor of ~5 000 or ~10 000 blocks
+    lens = [4099, 1000, 3, block_size * 3, 777] + ([big] if big else [])
+    g = O.Rng(SEED ^ block_size)
+    for misaligned in (False, True):
+        p_np = [g.normal(n, 0.05) for n in lens]
+        base = [torch.from_numpy(np.concatenate([[0.0], p]).astype(np.float32)).cuda()
+                if misaligned and i == 1 else torch.from_numpy(p).cuda()
+                for i, p in enumerate(p_np)]
+        p_dev = [t[1:] if misaligned and i == 1 else t for i, t in enumerate(base)]
+        og = QH.Adam8bit(lr=1e-3, block_size=block_size, ctx=ctx)
+        oo = O.Adam8bit(lr=1e-3, block_size=block_size)
+        for step in range(3):
+            gr = [g.normal(n, 0.01) for n in lens]
+            g_dev = [torch.from_numpy(x).cuda() for x in gr]
+            cnt = len(lens)
+            pp = (C.c_void_p * cnt)(*[t.data_ptr() for t in p_dev])
+            gp = (C.c_void_p * cnt)(*[t.data_ptr() for t in g_dev])
+            ll = (C.c_size_t * cnt)(*lens)
+            st = QH._lib.AdamStats()
+            QH._lib.check(ctx.lib.qh_adam8bit_step_dev(og.h, pp, gp, ll, cnt, C.byref(st),
+                                                       None))
+            oo.step(p_np, gr)
+            torch.cuda.synchronize()
+            for i, (t, p) in enumerate(zip(p_dev, p_np)):
+                assert _same_bits(t.cpu().numpy(), p), (misaligned, step, i)
+        for i, n in enumerate(lens):
+            sg, so = og.state(i, n), oo.state(i, n)
+            for key in ("m_codes", "m_scales", "v_codes", "v_scales"):
+                assert _same_bits(sg[key], so[key]), (misaligned, i, key)
+
+
 def test_adam_reference_behaviour(ctx):
     # tests/optim.rs:62-131 through the GPU path
     g = np.array([((i * 7) % 43) / 43 - 0.5 for i in range(256)], np.float32)

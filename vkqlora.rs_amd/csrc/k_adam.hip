@@ -6,9 +6,23 @@
 // The host computes b1t = 1 - beta1^t and b2t = 1 - beta2^t with the same
 // libm powf the reference calls and passes them in.
 //
-// One workgroup per state block (all tensors of one step in one launch):
-// dequantize m and v, update p, stage the new m and v in LDS, reduce the
-// block absmax, requantize.  16 B of HBM traffic per element.
+// All tensors of one step go in one launch.  16 B of HBM traffic per
+// element (p read and written, g read, the m and v codes read and written)
+// plus 16 B per state block (the two scales read and written).
+//
+//  * k_adam_wave (block sizes 256, 512, 1024; p and g 16-byte aligned): one
+//    wave per state block, four waves per workgroup.  Lane l owns elements
+//    [4l, 4l + 4) of every 256-element chunk of its block: one float4 load
+//    of p and of g and one u32 load of the m and of the v codes per chunk.
+//    The new m and v stay in registers; the block absmax is a wave
+//    reduction (max is exact, so its order does not matter); the codes are
+//    stored as u32.  No LDS and no workgroup barrier.  Divisions by 127, by
+//    b1t and b2t and by the block absmax are double products with the
+//    divisor's reciprocal rounded once to float (`div_by`: the IEEE float
+//    quotient bit for bit); the one division by a per-element value stays a
+//    float division.
+//  * k_adam (any other block size or alignment): one workgroup per block,
+//    one element per thread, m and v staged in LDS.
 #include "qh_internal.h"
 #include "qh_nf4.h"
 
@@ -23,6 +37,188 @@ struct AdamBatch {
 
 __device__ __forceinline__ float deq_i8(uint8_t c, float absmax) {
   return (float)(int8_t)c / 127.0f * absmax;
+}
+
+// Float quotients without a float division, bit for bit the IEEE ones: an
+// exact quotient of two floats is never a float midpoint and lies at least
+// 2^-49 (relative) from every midpoint, while RN_d(x * RN_d(1/y)) is within
+// 2^-52 of x/y, so its rounding to float is RN_f(x/y).  `inv` is the
+// divisor's double reciprocal (1 / (double)y, correctly rounded).
+__device__ __forceinline__ float div_by(float x, double inv) {
+  return (float)((double)x * inv);
+}
+__device__ __forceinline__ float deq_i8_fast(uint8_t c, float absmax) {
+  return div_by((float)(int8_t)c, 1.0 / 127.0) * absmax;  // (c / 127) * absmax
+}
+
+// One element's update in the reference's operation order (optim.rs:227-241).
+struct Upd {
+  float lr, beta1, beta2, eps, one_m_b1, one_m_b2, b1t, b2t;
+  __device__ __forceinline__ float step(float &m, float &v, float p, float g) const {
+    m = beta1 * m + one_m_b1 * g;
+    const float var = beta2 * v * v + one_m_b2 * g * g;
+    v = sqrtf(var);
+    const float mh = m / b1t;
+    const float vh = var / b2t;
+    return p - lr * mh / (sqrtf(vh) + eps);
+  }
+  // The same with m / b1t and var / b2t through div_by (same bits).
+  __device__ __forceinline__ float step_fast(float &m, float &v, float p, float g, double ib1,
+                                             double ib2) const {
+    m = beta1 * m + one_m_b1 * g;
+    const float var = beta2 * v * v + one_m_b2 * g * g;
+    v = sqrtf(var);
+    const float mh = div_by(m, ib1);
+    const float vh = div_by(var, ib2);
+    return p - lr * mh / (sqrtf(vh) + eps);
+  }
+};
+
+__device__ __forceinline__ uint32_t q8(float x, float absmax) {
+  return absmax != 0.0f ? (uint32_t)(uint8_t)(int8_t)qh_round_clamp127(x / absmax * 127.0f) : 0u;
+}
+// q8 with x / absmax through div_by (`inv` = 1 / (double)absmax; absmax != 0).
+__device__ __forceinline__ uint32_t q8_fast(float x, double inv) {
+  return (uint32_t)(uint8_t)(int8_t)qh_round_clamp127(div_by(x, inv) * 127.0f);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// The tensor of global block gb (wave-uniform: gb is).
+__device__ __forceinline__ int tensor_of(const AdamBatch &B, int64_t gb) {
+  int ti = 0;
+  while (ti + 1 < B.n && B.t[ti + 1].block_offset <= gb) ++ti;
+  return ti;
+}
+
+// One state block's view for one lane: where it lives and, for every full
+// 4-element chunk of the lane, the loaded p, g and codes.
+template <int NC>
+struct BlockRegs {
+  AdamTensor T;  // a copy of the fields: a pointer into the kernel argument
+                 // would move the whole argument to scratch memory
+  int64_t b, s;
+  int len;
+  float ms, vs;
+  float4 p4[NC], g4[NC];
+  uint32_t mc[NC], vc[NC];
+};
+
+template <int NC>
+__device__ __forceinline__ void load_block(BlockRegs<NC> &R, const AdamBatch &B, int64_t gb,
+                                           int lane) {
+  R.T = B.t[tensor_of(B, gb)];
+  R.b = gb - R.T.block_offset;
+  R.s = R.b * (256 * NC);
+  const int64_t rem = R.T.numel - R.s;
+  R.len = rem < 256 * NC ? (int)rem : 256 * NC;
+  R.ms = R.T.m_scales[R.b];
+  R.vs = R.T.v_scales[R.b];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j0 = 256 * c + 4 * lane;
+    if (j0 + 4 <= R.len) {
+      R.g4[c] = *(const float4 *)(R.T.g + R.s + j0);
+      R.p4[c] = *(const float4 *)(R.T.p + R.s + j0);
+      R.mc[c] = *(const uint32_t *)(R.T.m_codes + R.s + j0);
+      R.vc[c] = *(const uint32_t *)(R.T.v_codes + R.s + j0);
+    }
+  }
+}
+
+template <int NC>
+__device__ __forceinline__ void update_block(const BlockRegs<NC> &R, const Upd &u0, int lane) {
+  const AdamTensor &T = R.T;
+  Upd u = u0;
+  u.b1t = T.b1t;
+  u.b2t = T.b2t;
+  float m[NC][4], v[NC][4];
+  float am = 0.0f, av = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j0 = 256 * c + 4 * lane;
+    if (j0 + 4 <= R.len) {
+      float pp[4] = {R.p4[c].x, R.p4[c].y, R.p4[c].z, R.p4[c].w};
+      const float gg[4] = {R.g4[c].x, R.g4[c].y, R.g4[c].z, R.g4[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        m[c][e] = deq_i8_fast((uint8_t)(R.mc[c] >> (8 * e)), R.ms);
+        v[c][e] = deq_i8_fast((uint8_t)(R.vc[c] >> (8 * e)), R.vs);
+        pp[e] = u.step_fast(m[c][e], v[c][e], pp[e], gg[e], T.inv_b1t, T.inv_b2t);
+        am = fmaxf(am, fabsf(m[c][e]));
+        av = fmaxf(av, fabsf(v[c][e]));
+      }
+      *(float4 *)(T.p + R.s + j0) = make_float4(pp[0], pp[1], pp[2], pp[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        m[c][e] = v[c][e] = 0.0f;
+        if (j0 + e < R.len) {
+          const int64_t i = R.s + j0 + e;
+          m[c][e] = deq_i8_fast(T.m_codes[i], R.ms);
+          v[c][e] = deq_i8_fast(T.v_codes[i], R.vs);
+          T.p[i] = u.step_fast(m[c][e], v[c][e], T.p[i], T.g[i], T.inv_b1t, T.inv_b2t);
+          am = fmaxf(am, fabsf(m[c][e]));
+          av = fmaxf(av, fabsf(v[c][e]));
+        }
+      }
+    }
+  }
+  am = wave_max(am);
+  av = wave_max(av);
+  // a zero absmax quantizes to 0 (optim.rs:88-90); the reciprocal is then unused
+  const double iam = 1.0 / (double)(am != 0.0f ? am : 1.0f);
+  const double iav = 1.0 / (double)(av != 0.0f ? av : 1.0f);
+  const uint32_t mz = am != 0.0f ? 0xFFu : 0u, vz = av != 0.0f ? 0xFFu : 0u;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j0 = 256 * c + 4 * lane;
+    if (j0 + 4 <= R.len) {
+      uint32_t mc = 0, vc = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        mc |= (q8_fast(m[c][e], iam) & mz) << (8 * e);
+        vc |= (q8_fast(v[c][e], iav) & vz) << (8 * e);
+      }
+      *(uint32_t *)(T.m_codes + R.s + j0) = mc;
+      *(uint32_t *)(T.v_codes + R.s + j0) = vc;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (j0 + e < R.len) {
+          T.m_codes[R.s + j0 + e] = (uint8_t)(q8_fast(m[c][e], iam) & mz);
+          T.v_codes[R.s + j0 + e] = (uint8_t)(q8_fast(v[c][e], iav) & vz);
+        }
+      }
+    }
+  }
+  if (lane == 0) {
+    T.m_scales[R.b] = am;
+    T.v_scales[R.b] = av;
+  }
+}
+
+// NC 256-element chunks per block, one block per wave (measured against
+// two and four blocks per wave with every load issued up front: one is
+// fastest, as more waves hide the latency better than more loads per wave).
+template <int NC>
+__global__ __launch_bounds__(256) void k_adam_wave(AdamBatch B, int64_t first_block,
+                                                   int64_t total_blocks, float lr, float beta1,
+                                                   float beta2, float eps) {
+  const int lane = threadIdx.x & 63;
+  // the wave index is uniform: say so, so that block and tensor lookups and
+  // the tensors' pointers live in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t gb = first_block + (int64_t)blockIdx.x * 4 + wave;
+  if (gb >= total_blocks) return;
+  const Upd u{lr, beta1, beta2, eps, 1.0f - beta1, 1.0f - beta2, 1.0f, 1.0f};
+  BlockRegs<NC> R;
+  load_block<NC>(R, B, gb, lane);
+  update_block<NC>(R, u, lane);
 }
 
 __device__ float block_max(float v, float *red) {
@@ -41,26 +237,18 @@ __global__ __launch_bounds__(256) void k_adam(AdamBatch B, int64_t first_block,
   extern __shared__ float smem[];  // m[bs], v[bs]
   __shared__ float red[8];
   const int64_t gb = first_block + blockIdx.x;
-  int ti = 0;
-  while (ti + 1 < B.n && B.t[ti + 1].block_offset <= gb) ++ti;
-  const AdamTensor &T = B.t[ti];
+  const AdamTensor &T = B.t[tensor_of(B, gb)];
   const int64_t b = gb - T.block_offset;
   const int64_t s = b * bs;
   const int64_t len = (s + bs < T.numel ? s + bs : T.numel) - s;
   float *sm = smem, *sv = smem + bs;
   const float ms = T.m_scales[b], vs = T.v_scales[b];
-  const float one_m_b1 = 1.0f - beta1, one_m_b2 = 1.0f - beta2;
+  const Upd u{lr, beta1, beta2, eps, 1.0f - beta1, 1.0f - beta2, T.b1t, T.b2t};
   float am = 0.0f, av = 0.0f;
   for (int64_t j = threadIdx.x; j < len; j += blockDim.x) {
-    const float gj = T.g[s + j];
     float m = deq_i8(T.m_codes[s + j], ms);
     float v = deq_i8(T.v_codes[s + j], vs);
-    m = beta1 * m + one_m_b1 * gj;
-    const float var = beta2 * v * v + one_m_b2 * gj * gj;
-    v = sqrtf(var);
-    const float mh = m / T.b1t;
-    const float vh = var / T.b2t;
-    T.p[s + j] = T.p[s + j] - lr * mh / (sqrtf(vh) + eps);
+    T.p[s + j] = u.step(m, v, T.p[s + j], T.g[s + j]);
     sm[j] = m;
     sv[j] = v;
     am = fmaxf(am, fabsf(m));
@@ -69,11 +257,8 @@ __global__ __launch_bounds__(256) void k_adam(AdamBatch B, int64_t first_block,
   am = block_max(am, red);
   av = block_max(av, red + 4);
   for (int64_t j = threadIdx.x; j < len; j += blockDim.x) {
-    int32_t qm = 0, qv = 0;
-    if (am != 0.0f) qm = qh_round_clamp127(sm[j] / am * 127.0f);
-    if (av != 0.0f) qv = qh_round_clamp127(sv[j] / av * 127.0f);
-    T.m_codes[s + j] = (uint8_t)(int8_t)qm;
-    T.v_codes[s + j] = (uint8_t)(int8_t)qv;
+    T.m_codes[s + j] = (uint8_t)q8(sm[j], am);
+    T.v_codes[s + j] = (uint8_t)q8(sv[j], av);
   }
   if (threadIdx.x == 0) {
     T.m_scales[b] = am;
@@ -81,23 +266,41 @@ __global__ __launch_bounds__(256) void k_adam(AdamBatch B, int64_t first_block,
   }
 }
 
+bool aligned16(const void *p) { return (((uintptr_t)p) & 15) == 0; }
+
 }  // namespace
 
 hipError_t launch_adam(const AdamTensor *tensors, int ntensors,
                        int64_t total_blocks, int64_t block_size, float lr,
                        float beta1, float beta2, float eps, hipStream_t s) {
   (void)total_blocks;
-  const size_t shmem = (size_t)block_size * 2 * sizeof(float);
   for (int i0 = 0; i0 < ntensors; i0 += kMaxTensors) {
     AdamBatch B;
     B.n = ntensors - i0 < kMaxTensors ? ntensors - i0 : kMaxTensors;
     int64_t blocks = 0;
+    bool wave_ok = block_size == 256 || block_size == 512 || block_size == 1024;
     for (int i = 0; i < B.n; ++i) {
       B.t[i] = tensors[i0 + i];
       B.t[i].block_offset = blocks;
       blocks += B.t[i].nblocks;
+      wave_ok = wave_ok && aligned16(B.t[i].p) && aligned16(B.t[i].g) &&
+                (((uintptr_t)B.t[i].m_codes | (uintptr_t)B.t[i].v_codes) & 3) == 0;
     }
     if (blocks == 0) continue;
+    if (wave_ok) {
+      constexpr int64_t kMaxGroups = (int64_t)1 << 20;  // four blocks each
+      for (int64_t b0 = 0; b0 < blocks; b0 += 4 * kMaxGroups) {
+        const int64_t groups = std::min<int64_t>((blocks - b0 + 3) / 4, kMaxGroups);
+        auto k = block_size == 512    ? k_adam_wave<2>
+                 : block_size == 1024 ? k_adam_wave<4>
+                                      : k_adam_wave<1>;
+        hipError_t e = qh_launch(k, dim3((unsigned)groups), dim3(256), 0, s, B, b0, blocks, lr,
+                                 beta1, beta2, eps);
+        if (e != hipSuccess) return e;
+      }
+      continue;
+    }
+    const size_t shmem = (size_t)block_size * 2 * sizeof(float);
     for (int64_t b0 = 0; b0 < blocks; b0 += 65535) {
       int64_t nbk = blocks - b0 < 65535 ? blocks - b0 : 65535;
       hipError_t e = qh_launch(k_adam, dim3((unsigned)nbk), dim3(256), (uint32_t)shmem, s,

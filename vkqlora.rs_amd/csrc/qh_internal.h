@@ -172,6 +172,7 @@ struct AdamTensor {
   float *m_scales, *v_scales;
   int64_t numel, nblocks, block_offset;  // block_offset: prefix over tensors
   float b1t, b2t;
+  double inv_b1t, inv_b2t;  // 1 / (double)b1t and 1 / (double)b2t
 };
 hipError_t launch_adam(const AdamTensor *d_tensors, int ntensors,
                        int64_t total_blocks, int64_t block_size, float lr,

@@ -1289,6 +1289,8 @@ static qh_status adam_step_core(qh_adam8bit *o, float *const *d_params,
     at.block_offset = blocks;
     at.b1t = 1.0f - powf(c.beta1, t);  // optim.rs:209-210
     at.b2t = 1.0f - powf(c.beta2, t);
+    at.inv_b1t = 1.0 / (double)at.b1t;
+    at.inv_b2t = 1.0 / (double)at.b2t;
     blocks += at.nblocks;
     pages += st.nb;
     ts.push_back(at);
