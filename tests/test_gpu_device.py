@@ -237,3 +237,44 @@ def test_empty_reductions(ctx, QD, N, K, M):
     for got, want in ((y, yo), (gx, gxo), (ga, gao), (gb, gbo)):
         assert np.array_equal(got.cpu().numpy().ravel(), want)
     assert nerr(t1.cpu().numpy().ravel(), t1o, K, x, a) < TOL_F32
+
+
+@pytest.mark.parametrize("N,K,M,r", [
+    (4200, 4160, 1100, 16),   # ragged M, N (256 x 128 tiles) and grad_x reduction (4200 rows)
+    (4200, 4160, 1100, 0),    # no adapter
+    (4096, 4096, 1024, 64),   # 256 x 256 tiles for grad_x, two LoRA steps
+])
+def test_bf16_mfma_path_parity(ctx, QD, N, K, M, r):
+    """bf16 activations on bf16 MFMA (weight as hi + lo bf16 parts, LoRA as
+    three MFMAs): forward and grad_x against the oracle.  The bar is 2e-4,
+    tighter than bf16's 5e-3: the hi/lo split leaves ~1e-5, while dropping
+    the lo part would leave ~1e-3."""
+    _say(f"bf16 MFMA path N={N} K={K} M={M} r={r}")
+    rr = max(r, 1)
+    d = _setup(QD, ctx, N, K, rr, M, SEED ^ (N + K + M + r), torch.bfloat16)
+    dev = torch.device("cuda:0")
+    lora = QD.lora_struct(d["ta"], d["tb"], r, 16.0) if r else None
+    y = torch.empty(M, N, device=dev)
+    t1 = torch.empty(M, rr, device=dev) if r else None
+    gx = torch.empty(M, K, device=dev)
+    ga = torch.empty(rr, K, device=dev) if r else None
+    gb = torch.empty(N, rr, device=dev) if r else None
+    ctx.set_timing(True)
+    ctx.timing_report(reset=True)
+    QD.forward(d["W"], lora, d["tx"], M, y, t1=t1, ctx=ctx)
+    QD.backward(d["W"], lora, d["tx"], d["tdy"], M, gx, ga, gb, t1=t1, ctx=ctx)
+    torch.cuda.synchronize()
+    rep = ctx.timing_report(reset=True)
+    ctx.set_timing(False)
+    assert "forward_gemm_bf16" in rep and "grad_x_gemm_bf16" in rep, rep
+    wd = O.dequantize(O.quantize(d["w"]))
+    rows = [0, 1, 255, 256, M // 2, M - 1]
+    xs = d["x"].reshape(M, K)[rows].ravel()
+    dys = d["dy"].reshape(M, N)[rows].ravel()
+    a, b = (d["a"], d["b"]) if r else (None, None)
+    yo = O.qlora_forward(wd, N, K, a, b, r, 16.0, xs, len(rows))
+    gxo, _, _ = O.qlora_backward(wd, N, K, a, b, r, 16.0, xs, dys, len(rows))
+    ey = nerr(y.cpu().numpy()[rows].ravel(), yo, K, xs, wd)
+    egx = nerr(gx.cpu().numpy()[rows].ravel(), gxo, N, dys, wd)
+    _say(dict(y=ey, gx=egx))
+    assert ey < 2e-4 and egx < 2e-4, (ey, egx)

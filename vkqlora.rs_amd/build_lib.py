@@ -22,7 +22,8 @@ PROBE_OUT = os.path.join(HERE, "qlora_hip", "libqh_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["runtime.cpp", "nf4_file.cpp", "k_quant.hip", "k_gemm.hip", "k_gemv.hip",
+SOURCES = ["runtime.cpp", "nf4_file.cpp", "k_quant.hip", "k_gemm.hip", "k_gemm_bf16.hip",
+           "k_gemv.hip",
            "k_decode.hip", "k_dstream.hip", "k_adam.hip", "k_elem.hip",
            "k_block.hip", "k_rank.hip"]
 

@@ -78,6 +78,28 @@ struct GemmArgs {
   int64_t split_stride;
 };
 
+// ---- k_gemm_bf16.hip: NF4 GEMMs on bf16 MFMA for bf16 activations ----
+// C (M x N) = alpha * (A . Wop + A2 . B2), A bf16 row-major (M x K, lda).
+// w_form ROWK: Wop[k][n] = W[n][k] (forward, W is N x K); KROW: Wop[k][n] =
+// W[k][n] (input gradient, W is K x N).  Segment 2 (K2 > 0): fp32 A2 (M x
+// K2, row-major, lda2) and B2, scaled by b2scale, in form b2form (ROWK:
+// B2[k][n] = p[n * ldb2 + k]; KROW: p[k * ldb2 + n]).
+struct Bf16GemmArgs {
+  int64_t M, N, K;
+  const uint16_t *A;
+  int64_t lda;
+  DevQW w;
+  const float *A2, *B2;
+  int64_t lda2, ldb2, K2;
+  float b2scale;
+  int b2form;
+  float *C;
+  int64_t ldc;
+  float alpha;
+};
+bool bf16_gemm_ok(const DevQW &w, int64_t M, int64_t N);
+hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, hipStream_t s);
+
 // ---- k_quant.hip ----
 hipError_t launch_quantize(const float *w, int64_t n, int64_t bs, int dq,
                            uint8_t *codes, float *scales, uint8_t *scale_codes,
