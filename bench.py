@@ -152,10 +152,10 @@ def decode_bench(args, ctx, torch, dev, QD):
         ys = [torch.empty(batch, L["N"], device=dev) for L in layers]
 
         def step(i):
-            for li, L in enumerate(layers):
-                c = (i * len(layers) + li) % copies
-                QD.forward(None, L["lora"], xs[li], batch, ys[li], ctx=ctx,
-                           qw=L["structs"][c])
+            # both layers in one call: at batch 1 they share one launch
+            QD.forward_group([(L["structs"][(i * len(layers) + li) % copies], L["lora"],
+                               xs[li], ys[li], None) for li, L in enumerate(layers)],
+                             batch, ctx=ctx)
 
         n_graph = copies  # one graph covers every weight copy once
 
@@ -222,8 +222,8 @@ def decode_bench(args, ctx, torch, dev, QD):
         full_bytes = gemv_bytes + sum(4 * L["a"].numel() for L in layers)
         flops = sum(2 * batch * L["N"] * L["K"] + 2 * batch * r * (L["N"] + L["K"])
                     for L in layers)
-        main_name = next((k for k in ("decode_stream", "decode_small", "decode", "gemv", "forward_gemm")
-                          if k in kern), None)
+        main_name = next((k for k in ("decode_stream2", "decode_stream", "decode_small", "decode",
+                                      "gemv", "forward_gemm") if k in kern), None)
         main = kern.get(main_name) if main_name else None
         res = dict(
             ms_per_step=ms_step, wall_ms_per_step=wall_step,
@@ -232,11 +232,16 @@ def decode_bench(args, ctx, torch, dev, QD):
             tflops=flops / (ms_step * 1e9),
             kernels=kern, steps=reps * n_graph)
         if main:
-            # the one-launch kernel also reads LoRA A (its T1 producers); the
-            # two-kernel paths read it in their T1 kernel
-            kb = (full_bytes if main_name == "decode_stream" else gemv_bytes) / 2
-            kms = main["avg_ms"]
+            # the one-launch kernels also read LoRA A (their T1 producers);
+            # the two-kernel paths read it in their T1 kernel
             per_step = main["launches"] / (4 * n_graph)
+            # bytes one launch reads: both layers for the two-layer launch,
+            # one layer otherwise (each 8-row launch of a wider batch reads
+            # its layer's weights again)
+            per_launch_layers = 2 if main_name == "decode_stream2" else 1
+            kb = ((full_bytes if main_name.startswith("decode_stream") else gemv_bytes)
+                  * per_launch_layers / len(layers))
+            kms = main["avg_ms"]
             if set(kern) == {main_name}:
                 # the step is nothing but these launches: their duration in
                 # the replayed graph (back to back, as the step runs; the

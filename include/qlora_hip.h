@@ -234,6 +234,22 @@ QH_API qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w,
                                       const qh_lora *lora, const void *d_x,
                                       int x_dtype, size_t batch, float *d_y,
                                       float *d_t1, void *stream);
+/* Forward of `count` independent layers on one stream: layer i is exactly
+ * qh_qlora_forward_dev(ctx, &ws[i], loras[i], d_xs[i], x_dtype, batch,
+ * d_ys[i], d_t1s ? d_t1s[i] : NULL, stream), bit for bit (loras[i] NULL = no
+ * adapter).  No counterpart in the reference, whose forward takes one layer
+ * per call (qlora-wgpu/src/kernels.rs:262-296): at batch 1, consecutive
+ * layers that the one-launch decode kernel serves run in pairs, one launch
+ * per pair (no kernel boundary between them, one codebook table), as in a
+ * decoder block's independent projections (q / k / v, gate / up) or two
+ * layers of a decode step.  Arguments are validated for every layer before
+ * any launch. */
+QH_API qh_status qh_qlora_forward_group_dev(qh_ctx *ctx, size_t count,
+                                            const qh_qweight *ws,
+                                            const qh_lora *const *loras,
+                                            const void *const *d_xs, int x_dtype,
+                                            size_t batch, float *const *d_ys,
+                                            float *const *d_t1s, void *stream);
 /* Fused backward.  x and dy in `act_dtype`.  d_t1: X.A^T from the forward
  * (NULL = recompute). */
 QH_API qh_status qh_qlora_backward_dev(qh_ctx *ctx, const qh_qweight *w,

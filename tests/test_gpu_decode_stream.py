@@ -278,3 +278,124 @@ def test_stream_t1_fallback_same_bits(ctx, QD, N, K, M, r):
     wd = O.dequantize(O.quantize(w))
     yo = O.qlora_forward(wd, N, K, a, b, r, 16.0, x.cpu().numpy().ravel(), M)
     assert nerr(y1.cpu().numpy().ravel(), yo, K, x.cpu().numpy().ravel(), wd) < TOL_F32
+
+
+# ---- two layers in one launch (qh_qlora_forward_group_dev) --------------------
+def _layer(QD, ctx, N, K, r, seed, act):
+    g = O.Rng(seed)
+    dev = torch.device("cuda:0")
+    w = g.normal(N * K, 0.02)
+    a = g.uniform(r * K, -1 / np.sqrt(K), 1 / np.sqrt(K)) if r else None
+    b = g.normal(N * r, 0.01) if r else None
+    x = g.normal(K)
+    if act == torch.bfloat16:
+        x = bf16_round(x)
+    W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+    lora = QD.lora_struct(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), r,
+                          2.0 * r) if r else None
+    return dict(N=N, K=K, r=r, w=w, a=a, b=b, x=x, W=W, lora=lora,
+                tx=torch.from_numpy(x).to(dev).view(1, K).to(act))
+
+
+def _single(QD, ctx, L):
+    dev = torch.device("cuda:0")
+    y = torch.empty(1, L["N"], device=dev)
+    t1 = torch.empty(1, max(L["r"], 1), device=dev)
+    QD.forward(L["W"], L["lora"], L["tx"], 1, y, t1=t1 if L["r"] else None, ctx=ctx)
+    return y, t1
+
+
+def _group(QD, ctx, Ls):
+    dev = torch.device("cuda:0")
+    outs = [(torch.full((1, L["N"]), float("nan"), device=dev),
+             torch.full((1, max(L["r"], 1)), float("nan"), device=dev)) for L in Ls]
+    QD.forward_group([(L["W"], L["lora"], L["tx"], y, t1 if L["r"] else None)
+                      for L, (y, t1) in zip(Ls, outs)], 1, ctx=ctx)
+    return outs
+
+
+@pytest.mark.parametrize("shapes", [[(11008, 4096), (4096, 11008)],
+                                    [(4096, 11008), (11008, 4096)],
+                                    [(4096, 4096), (4096, 4096)]])
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_two_layer_launch_same_bits(ctx, QD, shapes, act):
+    """A pair of batch-1 layers in one launch gives each layer's outputs of
+    its own launch bit for bit, through launches of both kinds in turn (the
+    pair's second layer keeps its own launch counters and T1 words), and
+    matches the oracle."""
+    _say(f"two-layer launch {shapes} act={act}")
+    Ls = [_layer(QD, ctx, N, K, 16, SEED ^ (N * 3 + K + i), act) for i, (N, K) in enumerate(shapes)]
+    ref = [_single(QD, ctx, L) for L in Ls]
+    ctx.set_timing(True)
+    ctx.timing_report(reset=True)
+    got = _group(QD, ctx, Ls)
+    torch.cuda.synchronize()
+    rep = ctx.timing_report(reset=True)
+    ctx.set_timing(False)
+    assert "decode_stream2" in rep and "decode_stream" not in rep, rep
+    for (y, t1), (yr, t1r) in zip(got, ref):
+        assert torch.equal(y, yr) and torch.equal(t1, t1r)
+    # singles and pairs in turn, new inputs each time: every launch's tags new
+    for it in range(3):
+        for L in Ls:
+            L["tx"] = L["tx"] * 1.5 - 0.25
+        ref = [_single(QD, ctx, L) for L in Ls]
+        got = _group(QD, ctx, Ls)
+        again = [_single(QD, ctx, L) for L in Ls]
+        torch.cuda.synchronize()
+        for (y, t1), (yr, t1r), (ya, t1a) in zip(got, ref, again):
+            assert torch.equal(y, yr) and torch.equal(t1, t1r), it
+            assert torch.equal(ya, yr) and torch.equal(t1a, t1r), it
+    tol = TOL_F32 if act == torch.float32 else TOL_BF16
+    for L, (y, _) in zip(Ls, got):
+        wd = O.dequantize(O.quantize(L["w"]))
+        x = L["tx"].float().cpu().numpy().ravel()
+        yo = O.qlora_forward(wd, L["N"], L["K"], L["a"], L["b"], L["r"], 2.0 * L["r"], x, 1)
+        assert nerr(y.cpu().numpy().ravel(), yo, L["K"], x, wd) < tol
+
+
+def test_two_layer_launch_recompute_and_fallbacks(ctx, QD):
+    """The forced T1-recompute path inside a pair gives the same bits; a
+    group of three runs a pair and a single; layers without an adapter pair;
+    batch 2 is never paired (per-layer launches) and still matches."""
+    from qlora_hip._lib import QH_TEST_FORCE_T1_RECOMPUTE
+    Ls = [_layer(QD, ctx, 11008, 4096, 16, SEED ^ 0x71, torch.float32),
+          _layer(QD, ctx, 4096, 11008, 16, SEED ^ 0x72, torch.float32),
+          _layer(QD, ctx, 4096, 4096, 8, SEED ^ 0x73, torch.float32)]
+    ref = [_single(QD, ctx, L) for L in Ls]
+    ctx.set_test_flags(QH_TEST_FORCE_T1_RECOMPUTE)
+    try:
+        got = _group(QD, ctx, Ls[:2])
+    finally:
+        ctx.set_test_flags(0)
+    torch.cuda.synchronize()
+    for (y, t1), (yr, t1r) in zip(got, ref):
+        assert torch.equal(y, yr) and torch.equal(t1, t1r)
+    ctx.set_timing(True)
+    ctx.timing_report(reset=True)
+    got = _group(QD, ctx, Ls)
+    torch.cuda.synchronize()
+    rep = ctx.timing_report(reset=True)
+    ctx.set_timing(False)
+    assert rep["decode_stream2"][0] == 1 and rep["decode_stream"][0] == 1, rep
+    for (y, t1), (yr, t1r) in zip(got, ref):
+        assert torch.equal(y, yr) and torch.equal(t1, t1r)
+    # no adapters
+    Z = [_layer(QD, ctx, 4096, 4096, 0, SEED ^ (0x80 + i), torch.float32) for i in range(2)]
+    refz = [_single(QD, ctx, L)[0] for L in Z]
+    gotz = _group(QD, ctx, Z)
+    torch.cuda.synchronize()
+    for (y, _), yr in zip(gotz, refz):
+        assert torch.equal(y, yr)
+    # batch 2: per-layer launches
+    dev = torch.device("cuda:0")
+    xs = [torch.randn(2, L["K"], device=dev) for L in Ls[:2]]
+    ys = [torch.empty(2, L["N"], device=dev) for L in Ls[:2]]
+    yr = [torch.empty(2, L["N"], device=dev) for L in Ls[:2]]
+    for L, x, y in zip(Ls[:2], xs, yr):
+        QD.forward(L["W"], L["lora"], x, 2, y, ctx=ctx)
+    QD.forward_group([(L["W"], L["lora"], x, y, None) for L, x, y in zip(Ls[:2], xs, ys)], 2,
+                     ctx=ctx)
+    torch.cuda.synchronize()
+    for y, r_ in zip(ys, yr):
+        assert torch.equal(y, r_)

@@ -315,18 +315,21 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 // The weight's pointers, X and the shape lead the arguments: the first 16
 // argument dwords arrive preloaded in SGPRs (no kernel-argument load before
 // the first code line goes out).
+// One layer's share of workgroup c (of the layer's G workgroups).  The
+// codebook table is written when `build_table` is set; a workgroup that ran
+// another layer before keeps it (no layer writes LDS below kTabBytes).
 template <int XBF16, int KIND, int M, int R, int KLW>
-__global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict__ codes,
-                                                      const void *__restrict__ scales,
-                                                      const float *__restrict__ absmax,
-                                                      const void *__restrict__ x, int64_t N,
-                                                      int64_t K, const float *__restrict__ a,
-                                                      int r,
-                                                      const float *__restrict__ lb,
-                                                      float s_lora, uint64_t *__restrict__ t1w,
-                                                      uint64_t *__restrict__ epochs,
-                                                      float *__restrict__ t1_out,
-                                                      float *__restrict__ y, StreamArgs sa) {
+__device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
+                                             const void *__restrict__ scales,
+                                             const float *__restrict__ absmax,
+                                             const void *__restrict__ x, int64_t N, int64_t K,
+                                             const float *__restrict__ a, int r,
+                                             const float *__restrict__ lb, float s_lora,
+                                             uint64_t *__restrict__ t1w,
+                                             uint64_t *__restrict__ epochs,
+                                             float *__restrict__ t1_out, float *__restrict__ y,
+                                             StreamArgs sa, const int c, const int G,
+                                             const bool build_table) {
   static_assert(R * KLW <= kMaxLines, "code lines per wave");
   static_assert(M == 1 || M == 2 || M == 4 || M == 8, "batch rows");
   constexpr int M2 = 2 * M;
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   w.scale_codes = (const uint8_t *)scales;
   w.absmax = absmax;
   const int64_t KB = K >> 6;
-  const int KL = (int)(K / kLine), c = blockIdx.x;
+  const int KL = (int)(K / kLine);
   const int64_t n0 = (int64_t)c * R * 16;
   const int kl0 = KL * wave / kLW, nkl = KL * (wave + 1) / kLW - kl0;
   const int nl = lane & 15, g = lane >> 4;
@@ -398,7 +401,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   if (kT1In && r > 0 && wave == 0) ev = ld_dev64(epochs + (c & 15));
   __builtin_amdgcn_sched_barrier(0);
 
-  const int G = gridDim.x, MR = M * r, P = sa.P, r16 = sa.r16;
+  const int MR = M * r, P = sa.P, r16 = sa.r16;
   // B rows and T1 have rows of r16 floats, zero past r
   const uint32_t o_x = kTabBytes;  // one K-line of X fragments per wave
   const uint32_t o_lb = o_x + (uint32_t)kLW * kFragLine;
@@ -418,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   // Lh[q] | Ll[q] << 16, lo = 4 (wave & 3) + lane / 16 and hi = wave / 4 +
   // 2 i (uniform in the wave).  nib goes into lane q of a register from
   // immediates (indexed selects would become a constant-memory load).
-  {
+  if (build_table) {
     constexpr Tables kTab = make_tables();
     int nv = 0;
 #pragma unroll
@@ -782,6 +785,57 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
   }
 }
 
+template <int XBF16, int KIND, int M, int R, int KLW>
+__global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict__ codes,
+                                                      const void *__restrict__ scales,
+                                                      const float *__restrict__ absmax,
+                                                      const void *__restrict__ x, int64_t N,
+                                                      int64_t K, const float *__restrict__ a,
+                                                      int r,
+                                                      const float *__restrict__ lb,
+                                                      float s_lora, uint64_t *__restrict__ t1w,
+                                                      uint64_t *__restrict__ epochs,
+                                                      float *__restrict__ t1_out,
+                                                      float *__restrict__ y, StreamArgs sa) {
+  stream_layer<XBF16, KIND, M, R, KLW>(codes, scales, absmax, x, N, K, a, r, lb, s_lora, t1w,
+                                       epochs, t1_out, y, sa, (int)blockIdx.x, (int)gridDim.x,
+                                       true);
+}
+
+// One layer of a two-layer launch: its arguments and its workgroup count.
+struct StreamLayer {
+  const uint8_t *codes;
+  const void *scales;
+  const float *absmax;
+  const void *x;
+  int64_t N, K;
+  const float *a;
+  int r;
+  const float *lb;
+  float s_lora;
+  uint64_t *t1w, *epochs;  // the layer's own T1 words and launch counters
+  float *t1_out, *y;
+  StreamArgs sa;
+  int G;
+};
+
+// Two independent layers (batch 1) in one launch: workgroup c runs its share
+// of the first layer, then of the second, without a kernel boundary between
+// them and with the codebook table written once.
+template <int XBF16, int KIND, int R1, int KLW1, int R2, int KLW2>
+__global__ __launch_bounds__(kThreads) void k_dstream2(StreamLayer L1, StreamLayer L2) {
+  const int c = (int)blockIdx.x;
+  if (c < L1.G)
+    stream_layer<XBF16, KIND, 1, R1, KLW1>(L1.codes, L1.scales, L1.absmax, L1.x, L1.N, L1.K,
+                                           L1.a, L1.r, L1.lb, L1.s_lora, L1.t1w, L1.epochs,
+                                           L1.t1_out, L1.y, L1.sa, c, L1.G, true);
+  __syncthreads();  // the first layer's LDS reads are done before the second's writes
+  if (c < L2.G)
+    stream_layer<XBF16, KIND, 1, R2, KLW2>(L2.codes, L2.scales, L2.absmax, L2.x, L2.N, L2.K,
+                                           L2.a, L2.r, L2.lb, L2.s_lora, L2.t1w, L2.epochs,
+                                           L2.t1_out, L2.y, L2.sa, c, L2.G, c >= L1.G);
+}
+
 // ---- host side --------------------------------------------------------------
 struct StreamPlan {
   int R = 0, KLW = 0, G = 0;
@@ -920,7 +974,99 @@ hipError_t dispatch_rows(int x_bf16, const DevQW &w, const void *x, const float 
 #undef QH_ARGS
 }
 
+// Layer pairs of the two-layer launch (R1, KLW1, R2, KLW2): the Llama MLP
+// shapes in both orders (11008 x 4096 then 4096 x 11008 and back) and two
+// layers of 4096 x 4096-class shapes.
+#define QH_STREAM_PAIRS(F) F(3, 2, 1, 6) F(1, 6, 3, 2) F(1, 2, 1, 2)
+
+bool pair_compiled(int R1, int KLW1, int R2, int KLW2) {
+#define QH_PAIR_EQ(a, b, c, d) if (R1 == a && KLW1 == b && R2 == c && KLW2 == d) return true;
+  QH_STREAM_PAIRS(QH_PAIR_EQ)
+#undef QH_PAIR_EQ
+  return false;
+}
+
+StreamLayer layer_of(const DevQW &w, const void *x, const float *a, int64_t r, const float *lb,
+                     float s, uint64_t *t1w, uint64_t *epochs, float *t1_out, float *y,
+                     const StreamPlan &p) {
+  StreamLayer L;
+  L.codes = w.codes;
+  L.scales = w.kind == 0 ? (const void *)w.scales : (const void *)w.scale_codes;
+  L.absmax = w.absmax;
+  L.x = x;
+  L.N = w.rows;
+  L.K = w.cols;
+  L.a = a;
+  L.r = (int)r;
+  L.lb = lb;
+  L.s_lora = s;
+  L.t1w = t1w;
+  L.epochs = epochs;
+  L.t1_out = t1_out;
+  L.y = y;
+  L.sa = p.sa;
+  L.G = p.G;
+  return L;
+}
+
+template <int XBF16, int KIND, int R1, int KLW1, int R2, int KLW2>
+hipError_t run_stream2(const StreamLayer &L1, const StreamLayer &L2, uint32_t lds,
+                       hipStream_t st) {
+  auto k = k_dstream2<XBF16, KIND, R1, KLW1, R2, KLW2>;
+  static bool attr = false;  // per instantiation; the attribute is per function
+  if (!attr) {
+    const hipError_t e = hipFuncSetAttribute((const void *)k,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)kLdsLimit);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const int G = std::max(L1.G, L2.G);
+  return qh_launch(k, dim3((unsigned)G), dim3(kThreads), lds, st, L1, L2);
+}
+
+template <int XBF16, int KIND>
+hipError_t dispatch_pair(const StreamPlan &p1, const StreamPlan &p2, const StreamLayer &L1,
+                         const StreamLayer &L2, hipStream_t st) {
+  const uint32_t lds = std::max(p1.lds, p2.lds);
+#define QH_PAIR_CASE(a, b, c, d)                                        \
+  if (p1.R == a && p1.KLW == b && p2.R == c && p2.KLW == d)             \
+    return run_stream2<XBF16, KIND, a, b, c, d>(L1, L2, lds, st);
+  QH_STREAM_PAIRS(QH_PAIR_CASE)
+#undef QH_PAIR_CASE
+  return hipErrorInvalidValue;
+}
+
 }  // namespace
+
+bool decode_stream2_ok(const DevQW &w1, int64_t r1, const DevQW &w2, int64_t r2) {
+  if (w1.kind != w2.kind) return false;
+  const StreamPlan p1 = stream_plan(w1, 1, 1, r1), p2 = stream_plan(w2, 1, 1, r2);
+  return p1.ok && p2.ok && pair_compiled(p1.R, p1.KLW, p2.R, p2.KLW);
+}
+
+hipError_t launch_decode_stream2(const DevQW &w1, const void *x1, const float *a1, int64_t r1,
+                                 const float *lb1, float s1, float *y1, float *t1_out1,
+                                 const DevQW &w2, const void *x2, const float *a2, int64_t r2,
+                                 const float *lb2, float s2, float *y2, float *t1_out2,
+                                 int x_bf16, unsigned *tickets, bool force_t1_recompute,
+                                 hipStream_t st) {
+  if (!decode_stream2_ok(w1, r1, w2, r2)) return hipErrorInvalidValue;
+  StreamPlan p1 = stream_plan(w1, 1, 1, r1), p2 = stream_plan(w2, 1, 1, r2);
+  p1.sa.t1_fallback = p2.sa.t1_fallback = force_t1_recompute ? 1 : 0;
+  // the first layer uses the single-layer launches' counters and T1 words,
+  // the second its own
+  uint64_t *e1 = (uint64_t *)(tickets + kStreamEpochWord);
+  uint64_t *w1t = (uint64_t *)(tickets + kTicketWords);
+  uint64_t *e2 = (uint64_t *)(tickets + kStreamSlot2Word);
+  uint64_t *w2t = (uint64_t *)(tickets + kStreamSlot2Word + 32);
+  const StreamLayer L1 = layer_of(w1, x1, a1, r1, lb1, s1, w1t, e1, t1_out1, y1, p1);
+  const StreamLayer L2 = layer_of(w2, x2, a2, r2, lb2, s2, w2t, e2, t1_out2, y2, p2);
+  if (x_bf16) return w1.kind == 0 ? dispatch_pair<1, 0>(p1, p2, L1, L2, st)
+                                  : dispatch_pair<1, 1>(p1, p2, L1, L2, st);
+  return w1.kind == 0 ? dispatch_pair<0, 0>(p1, p2, L1, L2, st)
+                      : dispatch_pair<0, 1>(p1, p2, L1, L2, st);
+}
 
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r) {
   if (M < 1 || M > kStreamMaxRows) return false;

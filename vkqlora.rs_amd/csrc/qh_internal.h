@@ -165,6 +165,19 @@ constexpr int kStreamEpochWord = 32;
 constexpr int kStreamT1Words = 128 * 64 * 2;
 constexpr int kStreamT1ExtWords = 16 * 64;
 constexpr int kStreamMaxRows = 16;
+// The second layer of a two-layer launch keeps its own 16 launch counters
+// (32 words) and tagged T1 partials (kStreamT1Words words) from this word on.
+constexpr int kStreamSlot2Word = kTicketWords + kStreamT1Words + kStreamT1ExtWords;
+constexpr int kTicketsTotalWords = kStreamSlot2Word + 32 + kStreamT1Words;
+// Two independent batch-1 layers in one launch (k_dstream2): each layer as
+// launch_decode_stream would compute it, bit for bit.
+bool decode_stream2_ok(const DevQW &w1, int64_t r1, const DevQW &w2, int64_t r2);
+hipError_t launch_decode_stream2(const DevQW &w1, const void *x1, const float *a1, int64_t r1,
+                                 const float *lb1, float s1, float *y1, float *t1_out1,
+                                 const DevQW &w2, const void *x2, const float *a2, int64_t r2,
+                                 const float *lb2, float s2, float *y2, float *t1_out2,
+                                 int x_bf16, unsigned *tickets, bool force_t1_recompute,
+                                 hipStream_t st);
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r);
 // Rows per launch (M for batches of 1-2, else 8).
 int64_t decode_stream_chunk(int64_t M);

@@ -428,6 +428,17 @@ void zero_dev(float *p, size_t n, hipStream_t s) {
   if (n) check(qh::launch_zero(p, (int64_t)n, s), "zero fill");
 }
 
+// True when forward_dev serves this layer with one k_dstream launch (batch
+// 1-2 on the one-launch decode kernel): the layers a two-layer launch may
+// pair.
+bool takes_stream(const DevQW &W, const qh_lora *l, const void *x, int64_t M) {
+  const int64_t K = W.cols, r = l ? (int64_t)l->r : 0;
+  if (M == 0 || K == 0 || W.rows == 0) return false;
+  const bool aligned = (((uintptr_t)x) & 15) == 0 && (K % 8) == 0 &&
+                       (!l || (((uintptr_t)l->a) & 15) == 0);
+  return aligned && qh::decode_ok(W, M, r) && qh::decode_stream_ok(W, M, r);
+}
+
 // ---- fused forward on device pointers -----------------------------------
 void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
                  int xdt, size_t batch, float *y, float *t1_out, hipStream_t s) {
@@ -815,10 +826,8 @@ qh_status qh_ctx_create(qh_ctx **out) {
     snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
   if ((e = hipSetDevice(c->device)) != hipSuccess ||
       (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
-      (e = hipMalloc((void **)&c->tickets, (qh::kTicketWords + qh::kStreamT1Words + qh::kStreamT1ExtWords) * 4)) !=
-          hipSuccess ||
-      (e = hipMemset(c->tickets, 0, (qh::kTicketWords + qh::kStreamT1Words + qh::kStreamT1ExtWords) * 4)) !=
-          hipSuccess ||
+      (e = hipMalloc((void **)&c->tickets, (size_t)qh::kTicketsTotalWords * 4)) != hipSuccess ||
+      (e = hipMemset(c->tickets, 0, (size_t)qh::kTicketsTotalWords * 4)) != hipSuccess ||
       (e = hipDeviceSynchronize()) != hipSuccess) {
     if (c->tickets) (void)hipFree(c->tickets);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -1151,6 +1160,62 @@ qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *
   return guarded(ctx, [&] {
     forward_dev(ctx, make_devqw(*w), lora, d_x, x_dtype, batch, d_y, d_t1,
                 pick_stream(ctx, stream));
+    return QH_OK;
+  });
+}
+
+qh_status qh_qlora_forward_group_dev(qh_ctx *ctx, size_t count, const qh_qweight *ws,
+                                     const qh_lora *const *loras, const void *const *d_xs,
+                                     int x_dtype, size_t batch, float *const *d_ys,
+                                     float *const *d_t1s, void *stream) {
+  if (count == 0) return QH_OK;
+  if (!ws || !d_xs || !d_ys)
+    return fail(QH_ERR_SHAPE_MISMATCH, "ws, d_xs and d_ys must be given for count > 0");
+  if (x_dtype != QH_F32 && x_dtype != QH_BF16)
+    return fail(QH_ERR_INVALID_CONFIG, "x_dtype must be QH_F32 or QH_BF16");
+  for (size_t i = 0; i < count; ++i) {
+    const qh_qweight *w = &ws[i];
+    const qh_lora *l = loras ? loras[i] : nullptr;
+    qh_status st = validate_weight(w);
+    if (st == QH_OK) st = validate_lora(l, w->cols, w->rows);
+    if (st == QH_OK) st = need_buf(d_xs[i], batch * w->cols, "x");
+    if (st == QH_OK) st = need_buf(d_ys[i], batch * w->rows, "y");
+    if (st == QH_OK) st = need_buf(w->codes, w->rows * w->cols, "the weight's codes");
+    if (st != QH_OK) {
+      // name the layer after the message's kind: "<kind>: layer i: <text>"
+      const size_t pos = g_err.find(": ");
+      if (pos != std::string::npos) g_err.insert(pos + 2, fmt("layer %zu: ", i));
+      return st;
+    }
+  }
+  return guarded(ctx, [&] {
+    hipStream_t s = pick_stream(ctx, stream);
+    const int xb = x_dtype == QH_BF16;
+    const bool force = (ctx->test_flags & QH_TEST_FORCE_T1_RECOMPUTE) != 0;
+    for (size_t i = 0; i < count; ++i) {
+      const qh_lora *l1 = loras ? loras[i] : nullptr;
+      float *t1o1 = d_t1s ? d_t1s[i] : nullptr;
+      const DevQW W1 = make_devqw(ws[i]);
+      if (batch == 1 && i + 1 < count && takes_stream(W1, l1, d_xs[i], 1)) {
+        const qh_lora *l2 = loras ? loras[i + 1] : nullptr;
+        const DevQW W2 = make_devqw(ws[i + 1]);
+        const int64_t r1 = l1 ? (int64_t)l1->r : 0, r2 = l2 ? (int64_t)l2->r : 0;
+        if (takes_stream(W2, l2, d_xs[i + 1], 1) && qh::decode_stream2_ok(W1, r1, W2, r2)) {
+          float *t1o2 = d_t1s ? d_t1s[i + 1] : nullptr;
+          timed(ctx, "decode_stream2", s, [&] {
+            return qh::launch_decode_stream2(
+                W1, d_xs[i], l1 ? l1->a : nullptr, r1, l1 ? l1->b : nullptr,
+                l1 ? l1->alpha / (float)l1->r : 0.0f, d_ys[i], t1o1, W2, d_xs[i + 1],
+                l2 ? l2->a : nullptr, r2, l2 ? l2->b : nullptr,
+                l2 ? l2->alpha / (float)l2->r : 0.0f, d_ys[i + 1], t1o2, xb, ctx->tickets,
+                force, s);
+          });
+          ++i;
+          continue;
+        }
+      }
+      forward_dev(ctx, W1, l1, d_xs[i], x_dtype, batch, d_ys[i], t1o1, s);
+    }
     return QH_OK;
   });
 }

@@ -150,6 +150,30 @@ def forward(w: DeviceWeight, lora, x: torch.Tensor, batch: int, y: torch.Tensor,
         batch, _p(y), _p(t1), C.c_void_p(_stream())))
 
 
+def forward_group(layers, batch: int, ctx=None) -> None:
+    """The forward of several independent layers on the current stream
+    (qh_qlora_forward_group_dev): ``layers`` holds (weight, lora, x, y, t1)
+    per layer, weight a DeviceWeight or a QWeight view, lora a ``Lora``
+    struct or None, t1 a tensor or None.  Each layer's outputs are those of
+    ``forward`` bit for bit; at batch 1, consecutive layers served by the
+    one-launch decode kernel run in pairs, one launch per pair."""
+    ctx = ctx or default_context()
+    n = len(layers)
+    if n == 0:
+        return
+    dts = {_dt(L[2]) for L in layers}
+    if len(dts) != 1:
+        raise TypeError("all layers' x must share a dtype")
+    ws = (QWeight * n)(*[L[0] if isinstance(L[0], QWeight) else L[0].struct() for L in layers])
+    loras = (C.POINTER(Lora) * n)(*[C.pointer(L[1]) if L[1] is not None else C.POINTER(Lora)()
+                                    for L in layers])
+    xs = (C.c_void_p * n)(*[L[2].data_ptr() for L in layers])
+    ys = (C.c_void_p * n)(*[L[3].data_ptr() for L in layers])
+    t1s = (C.c_void_p * n)(*[L[4].data_ptr() if L[4] is not None else None for L in layers])
+    check(ctx.lib.qh_qlora_forward_group_dev(ctx.h, n, ws, loras, xs, dts.pop(), batch, ys,
+                                             t1s, C.c_void_p(_stream())))
+
+
 def backward(w: DeviceWeight, lora, x: torch.Tensor, dy: torch.Tensor, batch: int,
              gx: torch.Tensor, ga: Optional[torch.Tensor] = None,
              gb: Optional[torch.Tensor] = None, t1: Optional[torch.Tensor] = None,
