@@ -78,15 +78,16 @@ struct GemmArgs {
   int64_t split_stride;
 };
 
-// ---- k_gemm_bf16.hip: NF4 GEMMs on bf16 MFMA for bf16 activations ----
-// C (M x N) = alpha * (A . Wop + A2 . B2), A bf16 row-major (M x K, lda).
+// ---- k_gemm_bf16.hip: the large NF4 GEMMs on bf16 MFMA ----
+// C (M x N) = alpha * (A . Wop + A2 . B2), A row-major (M x K, lda), bf16 or
+// (a_f32) fp32 split into bf16 hi and lo parts.
 // w_form ROWK: Wop[k][n] = W[n][k] (forward, W is N x K); KROW: Wop[k][n] =
 // W[k][n] (input gradient, W is K x N).  Segment 2 (K2 > 0): fp32 A2 (M x
 // K2, row-major, lda2) and B2, scaled by b2scale, in form b2form (ROWK:
 // B2[k][n] = p[n * ldb2 + k]; KROW: p[k * ldb2 + n]).
 struct Bf16GemmArgs {
   int64_t M, N, K;
-  const uint16_t *A;
+  const void *A;
   int64_t lda;
   DevQW w;
   const float *A2, *B2;
@@ -98,7 +99,7 @@ struct Bf16GemmArgs {
   float alpha;
 };
 bool bf16_gemm_ok(const DevQW &w, int64_t M, int64_t N);
-hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, hipStream_t s);
+hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, int a_f32, hipStream_t s);
 
 // ---- k_quant.hip ----
 hipError_t launch_quantize(const float *w, int64_t n, int64_t bs, int dq,

@@ -560,17 +560,19 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     timed(ctx, "dequantize", s, [&] { return qh::launch_dequantize(W, w32, s); });
     B = op(w32, K, qh::ROWK, qh::E_F32);
   }
-  if (fast && xe == qh::E_BF16 && qh::bf16_gemm_ok(W, M, N)) {
-    // bf16 activations: X exact in bf16 MFMA against the weight's hi / lo
-    // bf16 parts, the LoRA term T1 . (s B)^T in the same kernel
+  if (fast && qh::bf16_gemm_ok(W, M, N)) {
+    // bf16 MFMA against the weight's hi / lo bf16 parts (X exact when bf16,
+    // split into hi / lo when fp32), the LoRA term T1 . (s B)^T in the same
+    // kernel
     qh::Bf16GemmArgs b{};
-    b.M = M, b.N = N, b.K = K, b.A = (const uint16_t *)x, b.lda = K, b.w = W;
+    b.M = M, b.N = N, b.K = K, b.A = x, b.lda = K, b.w = W;
     if (lora) {
       b.A2 = t1, b.lda2 = r, b.B2 = l->b, b.ldb2 = r, b.b2scale = sc, b.b2form = qh::ROWK;
       b.K2 = r;
     }
     b.C = y, b.ldc = N, b.alpha = 1.0f;
-    timed(ctx, "forward_gemm_bf16", s, [&] { return qh::launch_gemm_bf16(b, qh::ROWK, s); });
+    timed(ctx, "forward_gemm_bf16", s,
+          [&] { return qh::launch_gemm_bf16(b, qh::ROWK, xe == qh::E_F32, s); });
     return;
   }
   gm = gemm_args(M, N, K, op(x, K, qh::ROWK, xe), B, y, N, 1.0f);
@@ -692,16 +694,17 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
       timed(ctx, "grad_a_gemm", s, [&] { return qh::launch_gemm(gga, (float *)p[i_p4], s); });
     }
   }
-  if (fast && ae == qh::E_BF16 && qh::bf16_gemm_ok(W, M, K)) {
-    // grad_x = dY . W + Ds . A with dY exact in bf16 MFMA
+  if (fast && qh::bf16_gemm_ok(W, M, K)) {
+    // grad_x = dY . W + Ds . A on bf16 MFMA (dY exact when bf16, split when fp32)
     qh::Bf16GemmArgs b{};
-    b.M = M, b.N = K, b.K = N, b.A = (const uint16_t *)dy, b.lda = N, b.w = W;
+    b.M = M, b.N = K, b.K = N, b.A = dy, b.lda = N, b.w = W;
     if (lora) {
       b.A2 = ds, b.lda2 = r, b.B2 = l->a, b.ldb2 = K, b.b2scale = 1.0f, b.b2form = qh::KROW;
       b.K2 = r;
     }
     b.C = gx, b.ldc = K, b.alpha = 1.0f;
-    timed(ctx, "grad_x_gemm_bf16", s, [&] { return qh::launch_gemm_bf16(b, qh::KROW, s); });
+    timed(ctx, "grad_x_gemm_bf16", s,
+          [&] { return qh::launch_gemm_bf16(b, qh::KROW, ae == qh::E_F32, s); });
     return;
   }
   Operand B;
