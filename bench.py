@@ -51,32 +51,79 @@ def parse():
                     help="skip the RMSNorm / SwiGLU / cross-entropy measurements")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU-baseline budget per workload")
-    ap.add_argument("--probe", action="store_true",
-                    help="counter probe: a few eager C2 batch-1 launches of each layer "
-                         "and a 256 MiB device copy (the HBM-traffic calibration), "
-                         "for rocprofv3 --pmc; prints no JSON line")
+    ap.add_argument("--probe", choices=("decode", "prefill", "hbm"), default=None,
+                    help="counter probe for rocprofv3 --pmc (prints no JSON line): a few "
+                         "eager launches of one workload's kernels (decode: the C2 batch-1 "
+                         "two-layer launch; prefill: C3 fwd+bwd, fp32 and bf16; hbm: the "
+                         "C5 Adam step, quantize and the 70B-class cross-entropy), then a "
+                         "256 MiB device copy (the HBM-traffic calibration)")
+    ap.add_argument("--phases", default="decode,prefill,extra,glue,load,mlp",
+                    help="comma list of the measurements to run (for per-phase profiles); "
+                         "the JSON line always needs decode")
     return ap.parse_args()
 
 
-def probe(ctx, torch, dev, QD):
-    """Kernels for the HBM-traffic counters: each C2 layer's batch-1 forward
-    five times (eager, distinct weight copies) and a plain 256 MiB copy."""
-    r, alpha = 16, 32.0
+def probe(kind, ctx, torch, dev, QD):
+    """Kernels for the counter runs, then a plain 256 MiB copy."""
     g = torch.Generator(device="cuda").manual_seed(0x1234)
-    for N, K in [(11008, 4096), (4096, 11008)]:
-        w = torch.randn(N, K, device=dev, generator=g) * 0.02
-        base = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
-        del w
-        a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) / math.sqrt(K)
-        b = torch.randn(N, r, device=dev, generator=g) * 0.01
-        lora = QD.lora_struct(a, b, r, alpha)
-        x = torch.randn(1, K, device=dev, generator=g)
-        y = torch.empty(1, N, device=dev)
-        copies = [base.clone() for _ in range(5)]
-        for c in copies:
-            QD.forward(c, lora, x, 1, y, ctx=ctx)
+    if kind == "decode":
+        # the C2 batch-1 step: both layers in one launch, five weight copies
+        r, alpha = 16, 32.0
+        layers = []
+        for N, K in [(11008, 4096), (4096, 11008)]:
+            w = torch.randn(N, K, device=dev, generator=g) * 0.02
+            base = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+            del w
+            a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) / math.sqrt(K)
+            b = torch.randn(N, r, device=dev, generator=g) * 0.01
+            layers.append(dict(copies=[base.clone() for _ in range(5)], a=a, b=b,
+                               lora=QD.lora_struct(a, b, r, alpha),
+                               x=torch.randn(1, K, device=dev, generator=g),
+                               y=torch.empty(1, N, device=dev)))
+        for i in range(5):
+            QD.forward_group([(L["copies"][i], L["lora"], L["x"], L["y"], None)
+                              for L in layers], 1, ctx=ctx)
         torch.cuda.synchronize()
-        del copies
+        del layers
+    elif kind == "prefill":
+        for act in (torch.float32, torch.bfloat16):
+            L = _layer(torch, dev, QD, ctx, g, 4096, 4096, 4096, 64, 16.0, act=act)
+            for _ in range(2):
+                _fwd_bwd(QD, ctx, L)
+            torch.cuda.synchronize()
+            del L
+    else:
+        # C5 Adam step (four r=64 adapter tensors), C5 quantize, 70B-class CE
+        import ctypes as C
+        import qlora_hip as QH
+        r = 64
+        tens = []
+        for N, K in ((28672, 8192), (8192, 28672)):
+            tens += [(torch.randn(r * K, device=dev, generator=g),
+                      torch.randn(r * K, device=dev, generator=g) * 0.01),
+                     (torch.randn(N * r, device=dev, generator=g),
+                      torch.randn(N * r, device=dev, generator=g) * 0.01)]
+        opt = QH.Adam8bit(lr=1e-3, ctx=ctx)
+        cnt = len(tens)
+        pp = (C.c_void_p * cnt)(*[p.data_ptr() for p, _ in tens])
+        gp = (C.c_void_p * cnt)(*[g_.data_ptr() for _, g_ in tens])
+        ll = (C.c_size_t * cnt)(*[p.numel() for p, _ in tens])
+        st = QH._lib.AdamStats()
+        for _ in range(3):
+            QH._lib.check(ctx.lib.qh_adam8bit_step_dev(opt.h, pp, gp, ll, cnt, C.byref(st),
+                                                       None))
+        w = torch.randn(28672, 8192, device=dev, generator=g) * 0.02
+        for _ in range(2):
+            QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+        del w
+        logits = torch.randn(2048, 128256, device=dev, generator=g)
+        targets = torch.randint(0, 128256, (2048,), device=dev, dtype=torch.int32,
+                                generator=g)
+        for _ in range(2):
+            QD.softmax_cross_entropy(logits, targets, ctx=ctx)
+        torch.cuda.synchronize()
+        del logits
+    torch.cuda.empty_cache()
     src = torch.empty(64 << 20, device=dev)  # 256 MiB of fp32
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -85,20 +132,24 @@ def probe(ctx, torch, dev, QD):
     print("# probe done", file=sys.stderr, flush=True)
 
 
-def measured_traffic():
-    """HBM bytes per decode launch from the committed counter summary
-    (profiles/decode_c2_traffic.md: FETCH_SIZE + WRITE_SIZE per dispatch of
-    the decode kernel, scaled by the same counters on a copy of known size),
-    or None when that summary is absent."""
-    path = os.path.join(ROOT, "profiles", "decode_c2_traffic.md")
+def profile_value(name, key):
+    """A figure from a committed counter summary under profiles/ (a line
+    `key: value`, e.g. the HBM bytes per launch from FETCH_SIZE + WRITE_SIZE
+    scaled by the same counters on a copy of known size), or None when the
+    summary or the line is absent."""
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return float(line.split(":", 1)[1])
     except OSError:
         pass
     return None
+
+
+def measured_traffic():
+    """HBM bytes per batch-1 decode launch (profiles/decode_c2_traffic.md)."""
+    return profile_value("decode_c2_traffic.md", "traffic_bytes_per_launch")
 
 
 # ---------------------------------------------------------------------------
@@ -121,6 +172,72 @@ def hbm_copy_peak(torch, dev, nbytes=1 << 30, reps=10):
     del a, b
     return dict(gbs=2 * nbytes / (ms * 1e6), bytes=2 * nbytes, ms=ms,
                 kernel="torch copy_ of 1 GiB (read + write)")
+
+
+def read_ceiling(torch, dev, sizes=(24 << 20, 48 << 20, 1 << 30)):
+    """What ONE launch of a plain streaming read reaches at a given size:
+    libqh_probe.so's qh_probe_read (16-byte loads, a contiguous slice per
+    workgroup), best over a small sweep of grid, block, unroll and
+    non-temporal loads, timed as graph replays over enough distinct buffers
+    (>= 600 MiB) that no launch finds its bytes in the 256 MiB MALL. Returns
+    {MiB: {gbs, us, groups, threads, unroll, nt}}, or None when the probe
+    library is not built."""
+    import ctypes as C
+    path = os.path.join(ROOT, "vkqlora.rs_amd", "qlora_hip", "libqh_probe.so")
+    if not os.path.exists(path):
+        return None
+    P = C.CDLL(path)
+    P.qh_probe_read.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_void_p]
+    P.qh_probe_read.restype = C.c_int
+    sink = torch.empty(1 << 13, dtype=torch.int32, device=dev)
+    out = {}
+    for nbytes in sizes:
+        copies = max(1, -(-(600 << 20) // nbytes))
+        bufs = [torch.full((nbytes // 4,), i + 1, dtype=torch.int32, device=dev)
+                for i in range(copies)]
+        best = None
+        for groups in (512, 1024, 2048):
+            for threads in (512, 1024):
+                for unroll in (4, 8):
+                    for nt in (0, 1):
+                        def launch(b, groups=groups, threads=threads, unroll=unroll, nt=nt):
+                            rc = P.qh_probe_read(
+                                b.data_ptr(), nbytes, sink.data_ptr(), groups, threads,
+                                unroll, nt, torch.cuda.current_stream().cuda_stream)
+                            if rc != 0:
+                                raise RuntimeError(f"qh_probe_read: HIP error {rc}")
+                        s = torch.cuda.Stream()
+                        s.wait_stream(torch.cuda.current_stream())
+                        with torch.cuda.stream(s):
+                            for b in bufs:
+                                launch(b)
+                        torch.cuda.current_stream().wait_stream(s)
+                        torch.cuda.synchronize()
+                        gr = torch.cuda.CUDAGraph()
+                        with torch.cuda.graph(gr):
+                            for b in bufs:
+                                launch(b)
+                        gr.replay()
+                        torch.cuda.synchronize()
+                        reps = max(3, 48 // copies)
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        for _ in range(reps):
+                            gr.replay()
+                        e1.record()
+                        torch.cuda.synchronize()
+                        ms = e0.elapsed_time(e1) / (reps * copies)
+                        del gr
+                        gbs = nbytes / (ms * 1e6)
+                        if best is None or gbs > best["gbs"]:
+                            best = dict(gbs=gbs, us=ms * 1e3, groups=groups,
+                                        threads=threads, unroll=unroll, nt=nt)
+        out[str(nbytes >> 20)] = best
+        del bufs
+        torch.cuda.empty_cache()
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -159,7 +276,7 @@ def decode_bench(args, ctx, torch, dev, QD):
 
         n_graph = copies  # one graph covers every weight copy once
 
-        def capture():
+        def capture(nsteps):
             gr = torch.cuda.CUDAGraph()
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
@@ -168,7 +285,7 @@ def decode_bench(args, ctx, torch, dev, QD):
             torch.cuda.current_stream().wait_stream(s)
             torch.cuda.synchronize()
             with torch.cuda.graph(gr):
-                for i in range(n_graph):
+                for i in range(nsteps):
                     step(i)
             return gr
 
@@ -176,17 +293,19 @@ def decode_bench(args, ctx, torch, dev, QD):
         step(0)
         torch.cuda.synchronize()
         ref = [y.clone() for y in ys]
-        graph = capture()
+        graph = capture(n_graph)
         # the graph must reproduce the eager result on every replay
         for _ in range(2):
             graph.replay()
             torch.cuda.synchronize()
             for y, rr in zip(ys, ref):
                 assert torch.equal(y, rr), "graph replay differs from eager run"
-
-        reps = max(1, -(-args.steps // n_graph))
-        wreps = max(1, -(-args.warmup // n_graph))
-        for _ in range(wreps):
+        # exactly args.steps timed steps: whole passes over the weight
+        # copies, then a graph of the remaining steps
+        reps, rem = divmod(max(args.steps, 1), n_graph)
+        tail = capture(rem) if rem else None
+        nsteps = reps * n_graph + rem
+        for _ in range(max(1, -(-args.warmup // n_graph))):
             graph.replay()
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
@@ -195,10 +314,12 @@ def decode_bench(args, ctx, torch, dev, QD):
         e0.record()
         for _ in range(reps):
             graph.replay()
+        if tail is not None:
+            tail.replay()
         e1.record()
         torch.cuda.synchronize()
-        wall_step = (time.perf_counter() - t0) / (reps * n_graph) * 1e3
-        ms_step = e0.elapsed_time(e1) / (reps * n_graph)
+        wall_step = (time.perf_counter() - t0) / nsteps * 1e3
+        ms_step = e0.elapsed_time(e1) / nsteps
 
         # Per-kernel durations: with timing on, the library launches each
         # hot-path kernel with start/stop events that the GPU stamps at that
@@ -230,7 +351,7 @@ def decode_bench(args, ctx, torch, dev, QD):
             weight_gbs=wbytes / (ms_step * 1e6),
             total_gbs=full_bytes / (ms_step * 1e6),
             tflops=flops / (ms_step * 1e9),
-            kernels=kern, steps=reps * n_graph)
+            kernels=kern, steps=nsteps)
         if main:
             # the one-launch kernels also read LoRA A (their T1 producers);
             # the two-kernel paths read it in their T1 kernel
@@ -331,16 +452,40 @@ def prefill_bench(args, ctx, torch, dev, QD, act_dtype):
     flops = 4 * M * N * K + 6 * M * r * (K + N)  # fwd 2MNK + 2Mr(K+N), bwd 2MNK + 4Mr(K+N)
     kern = {k: dict(launches=v[0], avg_ms=v[1] / max(v[0], 1)) for k, v in rep.items()}
     fwd_flops = 2 * M * N * K + 2 * M * r * N
-    fk = kern.get("forward_gemm")
     peak = FP32_MFMA_PEAK_TFLOPS
+    # The large GEMMs run on bf16 MFMA: two MFMAs per product for bf16
+    # activations (x.wh + x.wl), three for fp32 ones (xh.wh + xh.wl + xl.wh).
+    mfma_per_product = 2 if act_dtype == torch.bfloat16 else 3
+    act_name = "bfloat16" if act_dtype == torch.bfloat16 else "float32"
     roof = None
+    fk = kern.get("forward_gemm_bf16") or kern.get("forward_gemm")
     if fk:
+        bf = "forward_gemm_bf16" in kern
         ach = fwd_flops / (fk["avg_ms"] * 1e9)
-        roof = dict(bound="mfma", kernel="forward_gemm (k_gemm NF4 fwd)",
-                    achieved=ach, peak=peak, unit="TFLOP/s", frac=ach / peak,
-                    flops_per_launch=fwd_flops, traffic=None)
+        roof = dict(bound="mfma",
+                    kernel=("forward_gemm_bf16 (k_nf4_bf16 forward: NF4 dequant in the K loop, "
+                            f"{mfma_per_product} bf16 MFMAs per product)" if bf
+                            else "forward_gemm (k_gemm NF4 fwd, fp32 MFMA)"),
+                    achieved=ach, unit="TFLOP/s", flops_per_launch=fwd_flops,
+                    peak=BF16_MFMA_PEAK_TFLOPS / mfma_per_product if bf else peak,
+                    peak_note=(f"bf16 dense MFMA peak / {mfma_per_product} MFMAs per product"
+                               if bf else "fp32 MFMA peak"),
+                    frac=ach / (BF16_MFMA_PEAK_TFLOPS / mfma_per_product if bf else peak),
+                    mfma_busy_frac=(ach * mfma_per_product / BF16_MFMA_PEAK_TFLOPS if bf
+                                    else ach / peak),
+                    mfma_busy_counter=(profile_value(
+                        "prefill_c3_counters.md",
+                        f"mfma_busy_counter[forward_gemm_bf16,{act_name}]")
+                        if bf else None),
+                    frac_fp32_peak=ach / peak,
+                    traffic=(profile_value(
+                        "prefill_c3_counters.md",
+                        f"traffic_bytes_per_launch[forward_gemm_bf16,{act_name}]")
+                        if bf else None))
     return dict(ms_per_step=ms, tflops=flops / (ms * 1e9),
-                frac_fp32_peak=flops / (ms * 1e9) / peak, flops_per_step=flops,
+                frac_fp32_peak=flops / (ms * 1e9) / peak,
+                frac_bf16_peak=flops / (ms * 1e9) / BF16_MFMA_PEAK_TFLOPS,
+                mfma_per_product=mfma_per_product, flops_per_step=flops,
                 steps=steps, kernels=kern, roofline=roof,
                 act_dtype=str(act_dtype).replace("torch.", ""))
 
@@ -759,7 +904,7 @@ def cpu_baseline_prefill(seconds):
     import oracle as O
     N = K = 4096
     r, alpha, M = 64, 16.0, 4096
-    rows = 16
+    rows = 64
     rng = O.Rng(0x1234_5678_9ABC_DEF0 ^ 3)
     w = rng.normal(N * K, 0.02)
     q = O.quantize(w)
@@ -767,20 +912,27 @@ def cpu_baseline_prefill(seconds):
     b = rng.normal(N * r, 0.01)
     x = rng.normal(rows * K)
     dy = rng.normal(rows * N)
+    # the two dequantizations of a step (qlora.rs:97 and :133), timed once
+    t0 = time.perf_counter()
+    wd = O.dequantize(q)
+    wd = O.dequantize(q)
+    t_deq = time.perf_counter() - t0
     t0, steps = time.perf_counter(), 0
     while True:
-        wd = O.dequantize(q)
         O.qlora_forward(wd, N, K, a, b, r, alpha, x, rows)
         O.qlora_backward(wd, N, K, a, b, r, alpha, x, dy, rows)
         steps += 1
         if time.perf_counter() - t0 > seconds or steps >= 20:
             break
-    dt = (time.perf_counter() - t0) / steps
-    flops = 4 * rows * N * K + 6 * rows * r * (K + N)
-    return dict(value=flops / (dt * 1e12), unit="TFLOP/s", cores=1, kind="port",
-                sample=(f"fwd+bwd on a {rows}-row slice of the {M}-token batch "
-                        f"({steps} reps, {dt:.2f} s each incl. 2 dequantizations); "
-                        f"every term is linear in tokens, full step = {M // rows}x"),
+    t_slice = (time.perf_counter() - t0) / steps
+    full = t_deq + (M // rows) * t_slice
+    flops = 4 * M * N * K + 6 * M * r * (K + N)
+    return dict(value=flops / (full * 1e12), unit="TFLOP/s", cores=1, kind="port",
+                step_s=full,
+                sample=(f"fwd+bwd on a {rows}-row slice of the {M}-token batch ({steps} reps, "
+                        f"{t_slice:.2f} s each) scaled by {M // rows} (every GEMM term is "
+                        f"linear in tokens), plus the step's two dequantizations timed once "
+                        f"({t_deq:.2f} s): {full:.1f} s per full step"),
                 nproc=os.cpu_count())
 
 
@@ -803,48 +955,83 @@ def main():
     ctx = qlora_hip.default_context()
     print(f"# device: {ctx.device_name()}", file=sys.stderr, flush=True)
     if args.probe:
-        probe(ctx, torch, dev, QD)
+        probe(args.probe, ctx, torch, dev, QD)
+        return
+    phases = set(args.phases.split(","))
+    if args.skip_prefill:
+        phases.discard("prefill")
+    if args.skip_extra:
+        phases -= {"extra", "load", "mlp"}
+    if args.skip_glue:
+        phases.discard("glue")
+    if "decode" not in phases:
+        # a profiling run of other phases: no JSON line
+        run_phases(args, phases, ctx, torch, dev, QD)
         return
 
     copy_peak = hbm_copy_peak(torch, dev)
     print(f"# HBM copy: {copy_peak['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    read_ceil = read_ceiling(torch, dev)
+    if read_ceil:
+        print("# one-launch read ceiling: " + ", ".join(
+            f"{k} MiB {v['gbs']:.0f} GB/s" for k, v in read_ceil.items()),
+            file=sys.stderr, flush=True)
     dec, dec_cfg = decode_bench(args, ctx, torch, dev, QD)
     print(f"# decode done: {json.dumps({b: round(v['weight_gbs'], 1) for b, v in dec.items()})}",
           file=sys.stderr, flush=True)
+    prefill, extra, glue, load, mlp = run_phases(args, phases, ctx, torch, dev, QD)
+    cpu_dec = cpu_pre = None
+    if not args.no_cpu_baseline:
+        cpu_dec = cpu_baseline_decode(args.cpu_seconds)
+        if "prefill" in phases:
+            cpu_pre = cpu_baseline_prefill(args.cpu_seconds)
+            prefill["cpu_baseline"] = cpu_pre
+    emit(args, copy_peak, read_ceil, dec, dec_cfg, cpu_dec, prefill, extra, glue, load, mlp)
+
+
+def run_phases(args, phases, ctx, torch, dev, QD):
     prefill = {}
-    if not args.skip_prefill:
+    if "prefill" in phases:
         for dt_ in (torch.float32, torch.bfloat16):
             p = prefill_bench(args, ctx, torch, dev, QD, dt_)
             prefill[p["act_dtype"]] = p
             print(f"# prefill {p['act_dtype']}: {p['tflops']:.1f} TFLOP/s",
                   file=sys.stderr, flush=True)
     extra = {}
-    if not args.skip_extra:
+    if "extra" in phases:
         extra = extra_bench(args, ctx, torch, dev, QD)
         print(f"# extra configs done: {sorted(extra)}", file=sys.stderr, flush=True)
-    glue = None
-    if not args.skip_glue:
-        glue = glue_bench(args, ctx, torch, dev, QD)
-    load = None if args.skip_extra else load_bench(args, ctx, torch, dev, QD)
-    mlp = None if args.skip_extra else mlp_block_bench(args, ctx, torch, dev, QD)
-    cpu_dec = cpu_pre = None
-    if not args.no_cpu_baseline:
-        cpu_dec = cpu_baseline_decode(args.cpu_seconds)
-        if not args.skip_prefill:
-            cpu_pre = cpu_baseline_prefill(args.cpu_seconds)
-            prefill["cpu_baseline"] = cpu_pre
+    glue = glue_bench(args, ctx, torch, dev, QD) if "glue" in phases else None
+    load = load_bench(args, ctx, torch, dev, QD) if "load" in phases else None
+    mlp = mlp_block_bench(args, ctx, torch, dev, QD) if "mlp" in phases else None
+    return prefill, extra, glue, load, mlp
 
+
+def _frac_of_read(d1, read_ceil):
+    """The decode launch against one read launch of (about) its own size."""
+    if not read_ceil:
+        return None
+    mib = d1["main_kernel_bytes"] / (1 << 20)
+    key = min(read_ceil, key=lambda k: abs(int(k) - mib))
+    return dict(size_mib=int(key), frac=d1["main_kernel_gbs"] / read_ceil[key]["gbs"])
+
+
+def emit(args, copy_peak, read_ceil, dec, dec_cfg, cpu_dec, prefill, extra, glue, load, mlp):
     d1 = dec[1]
     roof = None
     if "main_kernel_gbs" in d1:
         roof = dict(bound="hbm",
                     kernel=(f"{d1['main_kernel']} (fused NF4 dequant-GEMV + LoRA "
-                            "epilogue, batch 1, mean of the two layers)"),
+                            "epilogue, batch 1"
+                            + (", both layers in one launch)" if d1["main_kernel"] == "decode_stream2"
+                               else ", mean of the two layers)")),
                     achieved=d1["main_kernel_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=d1["main_kernel_gbs"] / HBM_PEAK_GBS,
                     measured_copy_peak=copy_peak,
                     frac_of_measured=(d1["main_kernel_gbs"] / copy_peak["gbs"]
                                       if copy_peak else None),
+                    read_ceiling=read_ceil,
+                    frac_of_read_ceiling=_frac_of_read(d1, read_ceil),
                     bytes_per_launch=d1["main_kernel_bytes"],
                     avg_launch_ms=d1["main_kernel_ms"], traffic=measured_traffic())
     line = {
