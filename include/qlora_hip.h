@@ -291,8 +291,8 @@ QH_API qh_status qh_rmsnorm(qh_ctx *ctx, const float *x, size_t x_len,
 QH_API qh_status qh_rmsnorm_dev(qh_ctx *ctx, const float *d_x, const float *d_w,
                                 size_t rows, size_t h, float eps, float *d_y,
                                 void *stream);
-/* rmsnorm_backward (llama.rs:605-631): dx (rows x h) and, unless dw is NULL,
- * dw (h).  block_backward discards dw (llama.rs:560, 599); pass NULL to skip
+/* rmsnorm_backward (llama.rs:605-628): dx (rows x h) and, unless dw is NULL,
+ * dw (h).  block_backward discards dw (llama.rs:568, 594); pass NULL to skip
  * it.  dx may alias dy only when dw is NULL (the dw pass reads dy after dx
  * is written; the device form rejects that aliasing). */
 QH_API qh_status qh_rmsnorm_backward(qh_ctx *ctx, const float *x, size_t x_len,
@@ -311,7 +311,7 @@ QH_API qh_status qh_swiglu(qh_ctx *ctx, const float *gate, size_t gate_len,
 QH_API qh_status qh_swiglu_dev(qh_ctx *ctx, const float *d_gate,
                                const float *d_up, size_t n, float *d_act,
                                void *stream);
-/* Its backward (llama.rs:546-551, 520-529): dg = d_act * up * silu'(gate),
+/* Its backward (llama.rs:559-562, 520-527): dg = d_act * up * silu'(gate),
  * du = d_act * silu(gate); dg may alias gate, du may alias up. */
 QH_API qh_status qh_swiglu_backward(qh_ctx *ctx, const float *gate,
                                     const float *up, const float *d_act,
@@ -353,7 +353,7 @@ QH_API void qh_dweight_destroy(qh_dweight *w);
 
 /* ---- a decoder block's MLP on device ----------------------------------------
  * The MLP half of `block_forward` / `block_backward` (qlora-model/src/
- * llama.rs:449-463, 543-565) with its three projections as QLoRA layers
+ * llama.rs:449-463, 554-574) with its three projections as QLoRA layers
  * (`Proj::Qlora`, llama.rs:106-140): activations stay in HBM from the norm
  * to the residual add, all on `stream`.  Device pointers throughout. */
 typedef struct qh_mlp_block {
@@ -387,6 +387,62 @@ QH_API qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *blk,
                                      const float *d_dx_out, size_t seq,
                                      float *d_dx_in, float *const *d_grad_a,
                                      float *const *d_grad_b, void *stream);
+
+/* ---- a decoder block's attention projections on device ----------------------
+ * The attention half of `block_forward` / `block_backward` (qlora-model/src/
+ * llama.rs:426-439, 577-601) around the attention itself, which stays with
+ * the caller: RMSNorm and the q/k/v QLoRA projections before it, the o
+ * projection and the residual add after it, and their backward.  Device
+ * pointers throughout, all work on `stream`. */
+typedef struct qh_attn_block {
+  size_t hidden, kv_dim;    /* kv_dim = kv_heads * head_dim */
+  float eps;                /* LlamaConfig::rms_eps */
+  const float *norm_w;      /* attn_norm, hidden floats */
+  qh_qweight q;             /* hidden x hidden */
+  qh_qweight k, v;          /* kv_dim x hidden */
+  qh_qweight o;             /* hidden x hidden */
+  const qh_lora *q_lora, *k_lora, *v_lora, *o_lora; /* NULL = no adapter */
+} qh_attn_block;
+
+/* Activations kept for the backward (caller-owned device buffers). */
+typedef struct qh_attn_cache {
+  float *x_in;              /* seq x hidden: the block's input */
+  float *xn;                /* seq x hidden: rmsnorm(x_in) */
+  float *attn;              /* seq x hidden: the attention output (the
+                               caller writes it; the o projection reads it) */
+  float *t1_q, *t1_k, *t1_v, *t1_o; /* seq x r of each adapter (or NULL) */
+} qh_attn_cache;
+
+/* llama.rs:426-434: xn = rmsnorm(x); q = q(xn) (seq x hidden), k = k(xn),
+ * v = v(xn) (seq x kv_dim).  x is not changed (a copy goes to the cache). */
+QH_API qh_status qh_attn_qkv_forward_dev(qh_ctx *ctx, const qh_attn_block *blk,
+                                         const float *d_x, size_t seq,
+                                         const qh_attn_cache *cache, float *d_q,
+                                         float *d_k, float *d_v, void *stream);
+/* llama.rs:436-439: x (seq x hidden) <- x + o(cache->attn). */
+QH_API qh_status qh_attn_o_forward_dev(qh_ctx *ctx, const qh_attn_block *blk,
+                                       float *d_x, size_t seq,
+                                       const qh_attn_cache *cache, void *stream);
+/* llama.rs:577: the o projection's backward from dx_mid = dL/d(x after
+ * the attention residual): d_attn (seq x hidden) and o's adapter gradients
+ * (ignored without an adapter). */
+QH_API qh_status qh_attn_o_backward_dev(qh_ctx *ctx, const qh_attn_block *blk,
+                                        const qh_attn_cache *cache,
+                                        const float *d_dx_mid, size_t seq,
+                                        float *d_dattn, float *d_grad_a_o,
+                                        float *d_grad_b_o, void *stream);
+/* llama.rs:580-601: q/k/v backward from the attention's dq, dk, dv, the sum
+ * (dxn_q + dxn_k) + dxn_v, RMSNorm's dx (its dw discarded, llama.rs:594)
+ * and the residual: dx_in = dx_mid + dx_norm (dx_in must not alias dx_mid).
+ * Adapter gradients in q, k, v order; entries of projections without an
+ * adapter are ignored. */
+QH_API qh_status qh_attn_qkv_backward_dev(qh_ctx *ctx, const qh_attn_block *blk,
+                                          const qh_attn_cache *cache,
+                                          const float *d_dq, const float *d_dk,
+                                          const float *d_dv, const float *d_dx_mid,
+                                          size_t seq, float *d_dx_in,
+                                          float *const *d_grad_a,
+                                          float *const *d_grad_b, void *stream);
 
 /* ---- packed NF4 files -----------------------------------------------------
  * No counterpart in the reference: its quantized weights leave `quantize`

@@ -322,7 +322,7 @@ def rmsnorm(x, w, rows, h, eps):
 
 
 def rmsnorm_backward(x, w, dy, rows, h, eps):
-    """llama.rs:605-631 -> (dx, dw)"""
+    """llama.rs:605-628 -> (dx, dw)"""
     x, w, dy = _f32(x), _f32(w), _f32(dy)
     dx = np.empty(rows * h, np.float32)
     dw = np.empty(h, np.float32)
@@ -347,7 +347,7 @@ def swiglu(gate, up):
 
 
 def swiglu_backward(gate, up, d_act):
-    """llama.rs:546-551 -> (d_gate, d_up)"""
+    """llama.rs:559-562 -> (d_gate, d_up)"""
     gate, up, d_act = _f32(gate), _f32(up), _f32(d_act)
     dg = np.empty(gate.size, np.float32)
     du = np.empty(gate.size, np.float32)
@@ -382,12 +382,12 @@ def mlp_forward(norm_w, gate, up, down, x, seq, hidden, inter, eps):
     u = proj(up, xn, inter, hidden)
     act = swiglu(g, u)
     dn = proj(down, act, hidden, inter)
-    x_out = (x + dn).astype(np.float32)   # x_i += d (llama.rs:460-462)
+    x_out = (x + dn).astype(np.float32)   # x_i += d (llama.rs:458-460)
     return x_out, dict(x_mid=x, xn=xn, gate=g, up=u, act=act)
 
 
 def mlp_backward(norm_w, gate, up, down, cache, dx_out, seq, hidden, inter, eps):
-    """The MLP branch of block_backward (llama.rs:543-565) -> (dx_in,
+    """The MLP branch of block_backward (llama.rs:554-574) -> (dx_in,
     [(grad_a, grad_b) or None for gate, up, down])."""
     def proj_bwd(p, inp, dy, out_dim, in_dim):
         wd, a, b, r, alpha = p
@@ -401,3 +401,47 @@ def mlp_backward(norm_w, gate, up, down, cache, dx_out, seq, hidden, inter, eps)
     dxn = (dxn_g + dxn_u).astype(np.float32)
     dx_norm, _ = rmsnorm_backward(cache["x_mid"], norm_w, dxn, seq, hidden, eps)
     return (dx_norm + dx_out).astype(np.float32), [gg, gu, gd]
+
+
+def _proj(p, inp, out_dim, in_dim, seq):
+    wd, a, b, r, alpha = p
+    return qlora_forward(wd, out_dim, in_dim, a, b, r, alpha, inp, seq)
+
+
+def _proj_bwd(p, inp, dy, out_dim, in_dim, seq):
+    wd, a, b, r, alpha = p
+    gx, ga, gb = qlora_backward(wd, out_dim, in_dim, a, b, r, alpha, inp, dy, seq)
+    return gx, (None if a is None else (ga, gb))
+
+
+def attn_qkv_forward(norm_w, q, k, v, x, seq, hidden, kv_dim, eps):
+    """The projections before the attention in block_forward
+    (llama.rs:426-434): xn = rmsnorm(x), then q (hidden outputs), k and v
+    (kv_dim outputs) of xn.  Projections as in mlp_forward.  Returns
+    (q_out, k_out, v_out, cache)."""
+    x = _f32(x)
+    xn = rmsnorm(x, norm_w, seq, hidden, eps)
+    return (_proj(q, xn, hidden, hidden, seq), _proj(k, xn, kv_dim, hidden, seq),
+            _proj(v, xn, kv_dim, hidden, seq), dict(x_in=x, xn=xn))
+
+
+def attn_o_forward(o, attn, x, seq, hidden):
+    """llama.rs:436-439: x + o(attn)."""
+    return (_f32(x) + _proj(o, _f32(attn), hidden, hidden, seq)).astype(np.float32)
+
+
+def attn_o_backward(o, attn, dx_mid, seq, hidden):
+    """llama.rs:577: (d_attn, (grad_a, grad_b) or None) of the o projection."""
+    return _proj_bwd(o, _f32(attn), _f32(dx_mid), hidden, hidden, seq)
+
+
+def attn_qkv_backward(norm_w, q, k, v, cache, dq, dk, dv, dx_mid, seq, hidden, kv_dim, eps):
+    """llama.rs:580-601: the q, k, v backward, dxn = (dxn_q + dxn_k) + dxn_v,
+    the norm's dx and the residual: returns (dx_mid + dx_norm,
+    [grads of q, k, v])."""
+    dxn_q, gq = _proj_bwd(q, cache["xn"], _f32(dq), hidden, hidden, seq)
+    dxn_k, gk = _proj_bwd(k, cache["xn"], _f32(dk), kv_dim, hidden, seq)
+    dxn_v, gv = _proj_bwd(v, cache["xn"], _f32(dv), kv_dim, hidden, seq)
+    dxn = ((dxn_q + dxn_k).astype(np.float32) + dxn_v).astype(np.float32)
+    dx_norm, _ = rmsnorm_backward(cache["x_in"], norm_w, dxn, seq, hidden, eps)
+    return (_f32(dx_mid) + dx_norm).astype(np.float32), [gq, gk, gv]

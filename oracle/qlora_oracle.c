@@ -439,7 +439,7 @@ void or_rmsnorm(const float *x, const float *w, size_t rows, size_t h,
   }
 }
 
-/* llama.rs:605-631 */
+/* llama.rs:605-628 */
 void or_rmsnorm_backward(const float *x, const float *w, const float *dy,
                          size_t rows, size_t h, float eps, float *dx,
                          float *dw) {
@@ -463,7 +463,7 @@ void or_rmsnorm_backward(const float *x, const float *w, const float *dy,
   }
 }
 
-/* llama.rs:516-529 */
+/* llama.rs:516-527 */
 float or_silu(float x) { return x / (1.0f + expf(-x)); }
 
 static float or_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -478,7 +478,7 @@ void or_swiglu(const float *gate, const float *up, size_t n, float *act) {
   for (size_t i = 0; i < n; i++) act[i] = or_silu(gate[i]) * up[i];
 }
 
-/* llama.rs:546-551 */
+/* llama.rs:559-562 */
 void or_swiglu_backward(const float *gate, const float *up,
                         const float *d_act, size_t n, float *dg, float *du) {
   for (size_t i = 0; i < n; i++) {

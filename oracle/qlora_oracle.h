@@ -94,16 +94,16 @@ int or_adam_get_state(const or_adam *o, size_t idx, uint8_t *m_codes,
  * per row of h; y may alias x. */
 void or_rmsnorm(const float *x, const float *w, size_t rows, size_t h,
                 float eps, float *y);
-/* rmsnorm_backward (llama.rs:605-631): dx (rows x h) and dw (h). */
+/* rmsnorm_backward (llama.rs:605-628): dx (rows x h) and dw (h). */
 void or_rmsnorm_backward(const float *x, const float *w, const float *dy,
                          size_t rows, size_t h, float eps, float *dx,
                          float *dw);
-/* silu / sigmoid / silu_prime (llama.rs:516-529). */
+/* silu / sigmoid / silu_prime (llama.rs:516-527). */
 float or_silu(float x);
 float or_silu_prime(float x);
 /* MLP activation (llama.rs:452-456): act = silu(gate) * up. */
 void or_swiglu(const float *gate, const float *up, size_t n, float *act);
-/* Its backward (llama.rs:546-551): dg = d_act*up*silu'(gate),
+/* Its backward (llama.rs:559-562): dg = d_act*up*silu'(gate),
  * du = d_act*silu(gate). */
 void or_swiglu_backward(const float *gate, const float *up,
                         const float *d_act, size_t n, float *dg, float *du);

@@ -219,7 +219,7 @@ def test_block_glue_validation_messages():
     assert _err(L) == "invalid config: dx may alias dy only when dw is not requested"
     assert L.qh_swiglu(None, x, 12, x, 11, x) == 1
     assert _err(L) == "shape mismatch: gate.len() = 12 but up.len() = 11"
-    # llama.rs:508 indexes row[targets[t]]: a target >= vocab is rejected
+    # llama.rs:507 indexes row[targets[t]]: a target >= vocab is rejected
     t = np.array([0, 3], np.uint32)
     tp = t.ctypes.data_as(C.c_void_p)
     assert L.qh_softmax_cross_entropy(None, x, 6, tp, 2, 3, None, x) == 1

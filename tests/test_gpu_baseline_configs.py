@@ -7,7 +7,7 @@
   forward + backward, and the 8-bit Adam step over the four adapter tensors
   (optim.rs:164-248), bit-exact;
 * the device MLP block at 70B-class shapes (hidden 8192, MLP 28672, r = 64,
-  2048 tokens; llama.rs:449-463, 543-565);
+  2048 tokens; llama.rs:449-463, 554-574);
 * the backward above 2048 tokens, where grad_A and grad_B leave the
   token-reduction rank kernel for the split-K tile engine.
 

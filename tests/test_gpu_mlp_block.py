@@ -1,6 +1,6 @@
 """GPU parity of the device-resident MLP block (qh_mlp_forward_dev /
 qh_mlp_backward_dev): the MLP half of block_forward / block_backward
-(qlora-model/src/llama.rs:449-463, 543-565) with QLoRA projections, against
+(qlora-model/src/llama.rs:449-463, 554-574) with QLoRA projections, against
 the oracle's composite of the same steps.
 
 Tolerance (fp32, GEMM and row sums in a different order): max |gpu -

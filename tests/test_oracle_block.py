@@ -185,3 +185,99 @@ def test_mlp_block_without_adapters():
     dx, grads = O.mlp_backward(norm, *ps, cache, dy, seq, h, f, 1e-5)
     assert grads[0] is None and grads[2] is None and grads[1] is not None
     assert out.shape == x.shape and dx.shape == x.shape
+
+
+def _tiny_attn(seed, h=8, kv=4, r=2, seq=3, adapters=(True, True, True, True)):
+    g = O.Rng(seed)
+    norm = g.uniform(h, 0.5, 1.5)
+
+    def proj(out_dim, in_dim, ad):
+        q = O.quantize(g.normal(out_dim * in_dim, 0.3))
+        wd = O.dequantize(q)
+        if not ad:
+            return [wd, None, None, 0, 0.0]
+        return [wd, g.uniform(r * in_dim, -0.5, 0.5), g.normal(out_dim * r, 0.5), r, 4.0]
+    ps = [proj(h, h, adapters[0]), proj(kv, h, adapters[1]), proj(kv, h, adapters[2]),
+          proj(h, h, adapters[3])]
+    x = g.normal(seq * h)
+    return norm, ps, x, seq, h, kv
+
+
+def _fd_check(loss, x, got_dx, ps, grads, which_ps, d=1e-2, step_x=3, step_p=5):
+    for k in range(0, x.size, step_x):
+        xp, xm = x.copy(), x.copy()
+        xp[k] += d
+        xm[k] -= d
+        fd = (loss(xp) - loss(xm)) / (2 * d)
+        assert abs(got_dx[k] - fd) < 5e-3 * max(1.0, abs(fd)), (k, got_dx[k], fd)
+    for gi, pi in enumerate(which_ps):
+        for slot in (1, 2):  # A, then B
+            arr = ps[pi][slot]
+            got = grads[gi][slot - 1]
+            for k in range(0, arr.size, step_p):
+                fd = (loss(which=(pi, slot), k=k, val=arr[k] + d)
+                      - loss(which=(pi, slot), k=k, val=arr[k] - d)) / (2 * d)
+                assert abs(got[k] - fd) < 5e-3 * max(1.0, abs(fd)), (pi, slot, k, got[k], fd)
+
+
+def _with(ps, which, k, val):
+    pp = [list(p) for p in ps]
+    if which is not None:
+        arr = pp[which[0]][which[1]].copy()
+        arr[k] = val
+        pp[which[0]][which[1]] = arr
+    return pp
+
+
+def test_attn_qkv_backward_finite_differences():
+    # L = <q, Gq> + <k, Gk> + <v, Gv> + <x, Gmid>: dL/dx is the block's dx_in
+    # for upstream gradients dq = Gq, dk = Gk, dv = Gv and dx_mid = Gmid (the
+    # residual's straight path), as block_backward composes them
+    # (llama.rs:580-601; its own check: qlora-model/tests/backward.rs:168-195)
+    norm, ps, x, seq, h, kv = _tiny_attn(41)
+    eps = 1e-5
+    g = O.Rng(42)
+    gq, gk, gv, gmid = g.normal(seq * h), g.normal(seq * kv), g.normal(seq * kv), g.normal(seq * h)
+
+    def loss(xv=None, which=None, k=None, val=None):
+        pp = _with(ps, which, k, val)
+        xv = x if xv is None else xv
+        q, kk, v, _ = O.attn_qkv_forward(norm, pp[0], pp[1], pp[2], xv, seq, h, kv, eps)
+        f64 = np.float64
+        return float(np.dot(q.astype(f64), gq) + np.dot(kk.astype(f64), gk)
+                     + np.dot(v.astype(f64), gv) + np.dot(xv.astype(f64), gmid))
+
+    _, _, _, cache = O.attn_qkv_forward(norm, ps[0], ps[1], ps[2], x, seq, h, kv, eps)
+    dx, grads = O.attn_qkv_backward(norm, ps[0], ps[1], ps[2], cache, gq, gk, gv, gmid,
+                                    seq, h, kv, eps)
+    _fd_check(loss, x, dx, ps, grads, (0, 1, 2))
+
+
+def test_attn_o_backward_finite_differences():
+    # L = <x + o(attn), G>: dL/dattn and o's adapter gradients (llama.rs:436-439, 577)
+    norm, ps, x, seq, h, kv = _tiny_attn(43)
+    g = O.Rng(44)
+    attn, gout = g.normal(seq * h), g.normal(seq * h)
+
+    def loss(av=None, which=None, k=None, val=None):
+        pp = _with(ps, which, k, val)
+        out = O.attn_o_forward(pp[3], attn if av is None else av, x, seq, h)
+        return float(np.dot(out.astype(np.float64), gout))
+
+    out = O.attn_o_forward(ps[3], attn, x, seq, h)
+    # the straight path: x_out - x is exactly o(attn)
+    np.testing.assert_array_equal(
+        out, (x + O.qlora_forward(ps[3][0], h, h, ps[3][1], ps[3][2], ps[3][3], ps[3][4],
+                                  attn, seq)).astype(np.float32))
+    d_attn, go = O.attn_o_backward(ps[3], attn, gout, seq, h)
+    _fd_check(loss, attn, d_attn, ps, [go], (3,))
+
+
+def test_attn_half_without_adapters():
+    norm, ps, x, seq, h, kv = _tiny_attn(45, adapters=(True, False, True, False))
+    q, k, v, cache = O.attn_qkv_forward(norm, *ps[:3], x, seq, h, kv, 1e-5)
+    assert q.shape == (seq * h,) and k.shape == (seq * kv,) and v.shape == (seq * kv,)
+    dx, grads = O.attn_qkv_backward(norm, *ps[:3], cache, q, k, v, x, seq, h, kv, 1e-5)
+    assert grads[1] is None and grads[0] is not None and grads[2] is not None
+    d_attn, go = O.attn_o_backward(ps[3], q, x, seq, h)
+    assert go is None and d_attn.shape == (seq * h,)

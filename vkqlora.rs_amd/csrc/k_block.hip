@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm(const float *x, const float 
   }
 }
 
-// rmsnorm_backward's dx (llama.rs:605-631), one wave per row.  With
+// rmsnorm_backward's dx (llama.rs:605-628), one wave per row.  With
 // S = mean(x^2) + eps and r = 1/sqrt(S):
 //   ds = sum(dy x w) * (-0.5 / S * r),  dx = dy w r + 2 x / h * ds.
 // r is kept per row (rstd) when the caller asks for dw.  dx may alias dy
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_bwd_reg(const float *__restr
   }
 }
 
-// ---- SwiGLU (llama.rs:452-456, 516-529, 546-551) ------------------------------
+// ---- SwiGLU (llama.rs:452-456, 516-527, 559-562) ------------------------------
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 __device__ __forceinline__ float silu_prime(float v) {

@@ -1796,7 +1796,7 @@ qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *b, const qh_mlp_c
     if (seq == 0) return QH_OK;
     hipStream_t s = pick_stream(ctx, stream);
     const size_t h = b->hidden, f = b->inter;
-    // llama.rs:543-565 (MLP branch of block_backward)
+    // llama.rs:554-574 (MLP branch of block_backward)
     float *d_act = (float *)ctx->block_tmp[0].ensure(seq * f * 4);
     backward_dev(ctx, make_devqw(b->down), b->down_lora, c->act, d_dx_out, QH_F32, seq,
                  b->down_lora ? c->t1_down : nullptr, d_act,
@@ -1816,13 +1816,161 @@ qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *b, const qh_mlp_c
       return qh::launch_axpy_inplace(d_dx_in, dxn_u, (int64_t)(seq * h), s);
     });
     // dx_mid = rmsnorm_backward(x_mid, w, dxn).dx + dx_out (dw is discarded,
-    // llama.rs:560)
+    // llama.rs:568)
     timed(ctx, "rmsnorm_backward", s, [&] {
       return qh::launch_rmsnorm_bwd(c->x_mid, b->norm_w, d_dx_in, d_dx_in, nullptr, nullptr,
                                     (int64_t)seq, (int)h, b->eps, s);
     });
     timed(ctx, "residual_add", s, [&] {
       return qh::launch_axpy_inplace(d_dx_in, d_dx_out, (int64_t)(seq * h), s);
+    });
+    return QH_OK;
+  });
+}
+
+// ---- a decoder block's attention projections on device (llama.rs) -------------
+static qh_status validate_attn(const qh_attn_block *b) {
+  if (!b) return fail(QH_ERR_SHAPE_MISMATCH, "block descriptor is NULL");
+  const size_t h = b->hidden, kv = b->kv_dim;
+  if (h == 0 || kv == 0) return fail(QH_ERR_SHAPE_MISMATCH, "hidden and kv_dim must be > 0");
+  if (h > (size_t)INT32_MAX) return fail(QH_ERR_INVALID_CONFIG, "hidden size above 2^31-1");
+  if (!b->norm_w) return fail(QH_ERR_SHAPE_MISMATCH, "norm weight is NULL");
+  qh_status st;
+  const qh_qweight *ws[4] = {&b->q, &b->k, &b->v, &b->o};
+  const qh_lora *ls[4] = {b->q_lora, b->k_lora, b->v_lora, b->o_lora};
+  const size_t rows[4] = {h, kv, kv, h};
+  const char *nm[4] = {"q", "k", "v", "o"};
+  for (int i = 0; i < 4; ++i) {
+    if ((st = validate_weight(ws[i])) != QH_OK) return st;
+    if (ws[i]->rows != rows[i] || ws[i]->cols != h)
+      return fail(QH_ERR_SHAPE_MISMATCH,
+                  fmt("%s weight is %zu x %zu but the block needs %zu x %zu", nm[i], ws[i]->rows,
+                      ws[i]->cols, rows[i], h));
+    if ((st = validate_lora(ls[i], h, rows[i])) != QH_OK) return st;
+  }
+  return QH_OK;
+}
+
+static qh_status validate_attn_cache(const qh_attn_cache *c) {
+  if (!c || !c->x_in || !c->xn || !c->attn)
+    return fail(QH_ERR_SHAPE_MISMATCH, "cache buffers must not be NULL");
+  return QH_OK;
+}
+
+qh_status qh_attn_qkv_forward_dev(qh_ctx *ctx, const qh_attn_block *b, const float *d_x,
+                                  size_t seq, const qh_attn_cache *c, float *d_q, float *d_k,
+                                  float *d_v, void *stream) {
+  qh_status st = validate_attn(b);
+  if (st != QH_OK) return st;
+  if ((st = validate_attn_cache(c)) != QH_OK) return st;
+  if (seq > 0 && (!d_x || !d_q || !d_k || !d_v))
+    return fail(QH_ERR_SHAPE_MISMATCH, "x, q, k and v must not be NULL");
+  return guarded(ctx, [&] {
+    if (seq == 0) return QH_OK;
+    hipStream_t s = pick_stream(ctx, stream);
+    const size_t h = b->hidden;
+    // llama.rs:426-434: the block input kept, xn = rmsnorm(x), q, k, v of xn
+    check(hipMemcpyAsync(c->x_in, d_x, seq * h * 4, hipMemcpyDeviceToDevice, s), "copy x");
+    timed(ctx, "rmsnorm", s, [&] {
+      return qh::launch_rmsnorm(d_x, b->norm_w, c->xn, (int64_t)seq, (int)h, b->eps, s);
+    });
+    forward_dev(ctx, make_devqw(b->q), b->q_lora, c->xn, QH_F32, seq, d_q,
+                b->q_lora ? c->t1_q : nullptr, s);
+    forward_dev(ctx, make_devqw(b->k), b->k_lora, c->xn, QH_F32, seq, d_k,
+                b->k_lora ? c->t1_k : nullptr, s);
+    forward_dev(ctx, make_devqw(b->v), b->v_lora, c->xn, QH_F32, seq, d_v,
+                b->v_lora ? c->t1_v : nullptr, s);
+    return QH_OK;
+  });
+}
+
+qh_status qh_attn_o_forward_dev(qh_ctx *ctx, const qh_attn_block *b, float *d_x, size_t seq,
+                                const qh_attn_cache *c, void *stream) {
+  qh_status st = validate_attn(b);
+  if (st != QH_OK) return st;
+  if ((st = validate_attn_cache(c)) != QH_OK) return st;
+  if (seq > 0 && !d_x) return fail(QH_ERR_SHAPE_MISMATCH, "x must not be NULL");
+  return guarded(ctx, [&] {
+    if (seq == 0) return QH_OK;
+    hipStream_t s = pick_stream(ctx, stream);
+    const size_t h = b->hidden;
+    // llama.rs:436-439: x += o(attn)
+    float *proj = (float *)ctx->block_tmp[0].ensure(seq * h * 4);
+    forward_dev(ctx, make_devqw(b->o), b->o_lora, c->attn, QH_F32, seq, proj,
+                b->o_lora ? c->t1_o : nullptr, s);
+    timed(ctx, "residual_add", s, [&] {
+      return qh::launch_axpy_inplace(d_x, proj, (int64_t)(seq * h), s);
+    });
+    return QH_OK;
+  });
+}
+
+qh_status qh_attn_o_backward_dev(qh_ctx *ctx, const qh_attn_block *b, const qh_attn_cache *c,
+                                 const float *d_dx_mid, size_t seq, float *d_dattn,
+                                 float *d_grad_a_o, float *d_grad_b_o, void *stream) {
+  qh_status st = validate_attn(b);
+  if (st != QH_OK) return st;
+  if ((st = validate_attn_cache(c)) != QH_OK) return st;
+  if (seq > 0 && (!d_dx_mid || !d_dattn))
+    return fail(QH_ERR_SHAPE_MISMATCH, "dx_mid and dattn must not be NULL");
+  if (b->o_lora && (!d_grad_a_o || !d_grad_b_o))
+    return fail(QH_ERR_SHAPE_MISMATCH, "an adapter's gradient buffer is NULL");
+  return guarded(ctx, [&] {
+    if (seq == 0) return QH_OK;
+    hipStream_t s = pick_stream(ctx, stream);
+    // llama.rs:577: (o_ab, d_attn) = proj_backward(o, attn_out, dx_mid)
+    backward_dev(ctx, make_devqw(b->o), b->o_lora, c->attn, d_dx_mid, QH_F32, seq,
+                 b->o_lora ? c->t1_o : nullptr, d_dattn, b->o_lora ? d_grad_a_o : nullptr,
+                 b->o_lora ? d_grad_b_o : nullptr, s);
+    return QH_OK;
+  });
+}
+
+qh_status qh_attn_qkv_backward_dev(qh_ctx *ctx, const qh_attn_block *b, const qh_attn_cache *c,
+                                   const float *d_dq, const float *d_dk, const float *d_dv,
+                                   const float *d_dx_mid, size_t seq, float *d_dx_in,
+                                   float *const *d_grad_a, float *const *d_grad_b,
+                                   void *stream) {
+  qh_status st = validate_attn(b);
+  if (st != QH_OK) return st;
+  if ((st = validate_attn_cache(c)) != QH_OK) return st;
+  if (seq > 0 && (!d_dq || !d_dk || !d_dv || !d_dx_mid || !d_dx_in))
+    return fail(QH_ERR_SHAPE_MISMATCH, "dq, dk, dv, dx_mid and dx_in must not be NULL");
+  if (d_dx_in == d_dx_mid && seq > 0)
+    return fail(QH_ERR_INVALID_CONFIG, "dx_in must not alias dx_mid (read at the end)");
+  const qh_lora *ls[3] = {b->q_lora, b->k_lora, b->v_lora};
+  for (int i = 0; i < 3; ++i)
+    if (ls[i] && (!d_grad_a || !d_grad_b || !d_grad_a[i] || !d_grad_b[i]))
+      return fail(QH_ERR_SHAPE_MISMATCH, "an adapter's gradient buffer is NULL");
+  return guarded(ctx, [&] {
+    if (seq == 0) return QH_OK;
+    hipStream_t s = pick_stream(ctx, stream);
+    const size_t h = b->hidden;
+    // llama.rs:580-601: dxn = (dxn_q + dxn_k) + dxn_v, then the norm's dx and
+    // the residual's straight path
+    float *tmp = (float *)ctx->block_tmp[1].ensure(seq * h * 4);
+    backward_dev(ctx, make_devqw(b->q), b->q_lora, c->xn, d_dq, QH_F32, seq,
+                 b->q_lora ? c->t1_q : nullptr, d_dx_in, b->q_lora ? d_grad_a[0] : nullptr,
+                 b->q_lora ? d_grad_b[0] : nullptr, s);
+    backward_dev(ctx, make_devqw(b->k), b->k_lora, c->xn, d_dk, QH_F32, seq,
+                 b->k_lora ? c->t1_k : nullptr, tmp, b->k_lora ? d_grad_a[1] : nullptr,
+                 b->k_lora ? d_grad_b[1] : nullptr, s);
+    timed(ctx, "residual_add", s, [&] {
+      return qh::launch_axpy_inplace(d_dx_in, tmp, (int64_t)(seq * h), s);
+    });
+    backward_dev(ctx, make_devqw(b->v), b->v_lora, c->xn, d_dv, QH_F32, seq,
+                 b->v_lora ? c->t1_v : nullptr, tmp, b->v_lora ? d_grad_a[2] : nullptr,
+                 b->v_lora ? d_grad_b[2] : nullptr, s);
+    timed(ctx, "residual_add", s, [&] {
+      return qh::launch_axpy_inplace(d_dx_in, tmp, (int64_t)(seq * h), s);
+    });
+    timed(ctx, "rmsnorm_backward", s, [&] {
+      return qh::launch_rmsnorm_bwd(c->x_in, b->norm_w, d_dx_in, d_dx_in, nullptr, nullptr,
+                                    (int64_t)seq, (int)h, b->eps, s);
+    });
+    // dx_in = dx_mid + dx_norm (llama.rs:596-601; a + b rounds as b + a)
+    timed(ctx, "residual_add", s, [&] {
+      return qh::launch_axpy_inplace(d_dx_in, d_dx_mid, (int64_t)(seq * h), s);
     });
     return QH_OK;
   });

@@ -46,6 +46,8 @@ EXPORTED = [
     "qh_softmax_cross_entropy", "qh_softmax_cross_entropy_dev",
     "qh_nf4_file_size", "qh_nf4_file_write", "qh_nf4_file_count", "qh_nf4_file_entry",
     "qh_nf4_file_find", "qh_weight_upload_dev", "qh_mlp_forward_dev", "qh_mlp_backward_dev",
+    "qh_attn_qkv_forward_dev", "qh_attn_o_forward_dev", "qh_attn_o_backward_dev",
+    "qh_attn_qkv_backward_dev",
     "qh_weight_upload", "qh_dweight_view", "qh_dweight_destroy",
 ]
 
@@ -74,6 +76,20 @@ class MlpCache(C.Structure):
     """qh_mlp_cache (include/qlora_hip.h)."""
     _fields_ = [(n, C.c_void_p) for n in ("x_mid", "xn", "gate", "up", "act", "t1_gate",
                                           "t1_up", "t1_down")]
+
+
+class AttnBlock(C.Structure):
+    """qh_attn_block (include/qlora_hip.h)."""
+    _fields_ = [("hidden", C.c_size_t), ("kv_dim", C.c_size_t), ("eps", C.c_float),
+                ("norm_w", C.c_void_p), ("q", QWeight), ("k", QWeight), ("v", QWeight),
+                ("o", QWeight), ("q_lora", C.POINTER(Lora)), ("k_lora", C.POINTER(Lora)),
+                ("v_lora", C.POINTER(Lora)), ("o_lora", C.POINTER(Lora))]
+
+
+class AttnCache(C.Structure):
+    """qh_attn_cache (include/qlora_hip.h)."""
+    _fields_ = [(n, C.c_void_p) for n in ("x_in", "xn", "attn", "t1_q", "t1_k", "t1_v",
+                                          "t1_o")]
 
 
 class AdamConfig(C.Structure):
@@ -188,6 +204,14 @@ def load() -> C.CDLL:
                                          C.POINTER(MlpCache), vp]
         L.qh_mlp_backward_dev.argtypes = [vp, C.POINTER(MlpBlock), C.POINTER(MlpCache), vp,
                                           sz, vp, vp, vp, vp]
+        L.qh_attn_qkv_forward_dev.argtypes = [vp, C.POINTER(AttnBlock), vp, sz,
+                                              C.POINTER(AttnCache), vp, vp, vp, vp]
+        L.qh_attn_o_forward_dev.argtypes = [vp, C.POINTER(AttnBlock), vp, sz,
+                                            C.POINTER(AttnCache), vp]
+        L.qh_attn_o_backward_dev.argtypes = [vp, C.POINTER(AttnBlock), C.POINTER(AttnCache),
+                                             vp, sz, vp, vp, vp, vp]
+        L.qh_attn_qkv_backward_dev.argtypes = [vp, C.POINTER(AttnBlock), C.POINTER(AttnCache),
+                                               vp, vp, vp, vp, sz, vp, vp, vp, vp]
         _lib = L
         return L
 

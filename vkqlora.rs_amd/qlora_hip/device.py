@@ -16,7 +16,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import (Lora, MlpBlock, MlpCache, QWeight, QH_BF16, QH_F32, QH_SCALES_DQ_INT8,
+from ._lib import (AttnBlock, AttnCache, Lora, MlpBlock, MlpCache, QWeight, QH_BF16, QH_F32, QH_SCALES_DQ_INT8,
                    QH_SCALES_F32, check, default_context)
 
 
@@ -211,7 +211,7 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float,
 
 def rmsnorm_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, eps: float,
                      want_dw: bool = True, ctx=None):
-    """rmsnorm_backward (llama.rs:605-631) -> (dx, dw or None)."""
+    """rmsnorm_backward (llama.rs:605-628) -> (dx, dw or None)."""
     ctx = ctx or default_context()
     for t, n in ((x, "x"), (w, "w"), (dy, "dy")):
         _f32c(t, n)
@@ -237,7 +237,7 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = N
 
 
 def swiglu_backward(gate: torch.Tensor, up: torch.Tensor, d_act: torch.Tensor, ctx=None):
-    """(d_gate, d_up) of act = silu(gate) * up (llama.rs:546-551)."""
+    """(d_gate, d_up) of act = silu(gate) * up (llama.rs:559-562)."""
     ctx = ctx or default_context()
     for t, n in ((gate, "gate"), (up, "up"), (d_act, "d_act")):
         _f32c(t, n)
@@ -292,7 +292,7 @@ def load_nf4(src, device="cuda:0", ctx=None) -> dict:
 
 # ---- a decoder block's MLP on device (qh_mlp_forward_dev / _backward_dev) ----
 class MLPBlock:
-    """The MLP half of a decoder block (llama.rs:449-463, 543-565): RMSNorm,
+    """The MLP half of a decoder block (llama.rs:449-463, 554-574): RMSNorm,
     gate / up / down QLoRA projections, SwiGLU and the residual add, with
     every activation in HBM.  ``loras`` holds (a, b, r, alpha) per
     projection (gate, up, down) or None."""
@@ -354,4 +354,103 @@ class MLPBlock:
         check(self.ctx.lib.qh_mlp_backward_dev(self.ctx.h, C.byref(self.s), C.byref(cs),
                                                _p(dx_out), seq, _p(dx_in), ga, gb,
                                                C.c_void_p(_stream())))
+        return dx_in, grads
+
+
+class AttnProjections:
+    """The projections around a decoder block's attention (llama.rs:426-439,
+    577-601): RMSNorm and the q / k / v QLoRA projections before it, the o
+    projection and the residual add after it, and their backward, with every
+    activation in HBM.  The attention itself is the caller's.  ``loras``
+    holds (a, b, r, alpha) per projection (q, k, v, o) or None."""
+
+    def __init__(self, norm_w: torch.Tensor, q: DeviceWeight, k: DeviceWeight,
+                 v: DeviceWeight, o: DeviceWeight, loras=(None, None, None, None),
+                 eps: float = 1e-5, ctx=None):
+        self.ctx = ctx or default_context()
+        self.norm_w, self.w = _f32c(norm_w, "norm_w"), (q, k, v, o)
+        self.loras = [None if l is None else lora_struct(*l) for l in loras]
+        self.ranks = [0 if l is None else l[2] for l in loras]
+        self.hidden, self.kv_dim = q.rows, k.rows
+        b = AttnBlock()
+        b.hidden, b.kv_dim, b.eps = self.hidden, self.kv_dim, eps
+        b.norm_w = norm_w.data_ptr()
+        b.q, b.k, b.v, b.o = q.struct(), k.struct(), v.struct(), o.struct()
+        b.q_lora, b.k_lora, b.v_lora, b.o_lora = [
+            C.pointer(l) if l is not None else C.POINTER(Lora)() for l in self.loras]
+        self.s = b
+
+    def new_cache(self, seq: int, device="cuda:0") -> dict:
+        e = lambda n: torch.empty(seq, n, device=device)  # noqa: E731
+        c = dict(x_in=e(self.hidden), xn=e(self.hidden), attn=e(self.hidden))
+        for name, r in zip(("t1_q", "t1_k", "t1_v", "t1_o"), self.ranks):
+            c[name] = e(r) if r else None
+        return c
+
+    @staticmethod
+    def _cs(c: dict) -> AttnCache:
+        s = AttnCache()
+        for k in ("x_in", "xn", "attn", "t1_q", "t1_k", "t1_v", "t1_o"):
+            setattr(s, k, None if c[k] is None else c[k].data_ptr())
+        return s
+
+    def _grads(self, idx, dev):
+        grads, ga, gb = [], (C.c_void_p * len(idx))(), (C.c_void_p * len(idx))()
+        for j, i in enumerate(idx):
+            l, w = self.loras[i], self.w[i]
+            if l is None:
+                grads.append(None)
+                continue
+            a = torch.empty(l.r * w.cols, device=dev)
+            b = torch.empty(w.rows * l.r, device=dev)
+            ga[j], gb[j] = a.data_ptr(), b.data_ptr()
+            grads.append((a, b))
+        return grads, ga, gb
+
+    def qkv_forward(self, x: torch.Tensor, cache: dict):
+        """-> (q, k, v) of rmsnorm(x); x is unchanged."""
+        _f32c(x, "x")
+        seq = x.shape[0]
+        q = torch.empty(seq, self.hidden, device=x.device)
+        k = torch.empty(seq, self.kv_dim, device=x.device)
+        v = torch.empty(seq, self.kv_dim, device=x.device)
+        cs = self._cs(cache)
+        check(self.ctx.lib.qh_attn_qkv_forward_dev(self.ctx.h, C.byref(self.s), _p(x), seq,
+                                                   C.byref(cs), _p(q), _p(k), _p(v),
+                                                   C.c_void_p(_stream())))
+        return q, k, v
+
+    def o_forward(self, x: torch.Tensor, cache: dict) -> torch.Tensor:
+        """x (seq, hidden) is updated in place: x + o(cache["attn"])."""
+        _f32c(x, "x")
+        cs = self._cs(cache)
+        check(self.ctx.lib.qh_attn_o_forward_dev(self.ctx.h, C.byref(self.s), _p(x),
+                                                 x.shape[0], C.byref(cs),
+                                                 C.c_void_p(_stream())))
+        return x
+
+    def o_backward(self, cache: dict, dx_mid: torch.Tensor):
+        """-> (d_attn, (grad_a, grad_b) of o or None)."""
+        _f32c(dx_mid, "dx_mid")
+        seq = dx_mid.shape[0]
+        d_attn = torch.empty(seq, self.hidden, device=dx_mid.device)
+        grads, ga, gb = self._grads((3,), dx_mid.device)
+        cs = self._cs(cache)
+        check(self.ctx.lib.qh_attn_o_backward_dev(self.ctx.h, C.byref(self.s), C.byref(cs),
+                                                  _p(dx_mid), seq, _p(d_attn), ga[0], gb[0],
+                                                  C.c_void_p(_stream())))
+        return d_attn, grads[0]
+
+    def qkv_backward(self, cache: dict, dq: torch.Tensor, dk: torch.Tensor,
+                     dv: torch.Tensor, dx_mid: torch.Tensor):
+        """-> (dx_in, [(grad_a, grad_b) or None for q, k, v])."""
+        for t, n in ((dq, "dq"), (dk, "dk"), (dv, "dv"), (dx_mid, "dx_mid")):
+            _f32c(t, n)
+        seq = dx_mid.shape[0]
+        dx_in = torch.empty_like(dx_mid)
+        grads, ga, gb = self._grads((0, 1, 2), dx_mid.device)
+        cs = self._cs(cache)
+        check(self.ctx.lib.qh_attn_qkv_backward_dev(self.ctx.h, C.byref(self.s), C.byref(cs),
+                                                    _p(dq), _p(dk), _p(dv), _p(dx_mid), seq,
+                                                    _p(dx_in), ga, gb, C.c_void_p(_stream())))
         return dx_in, grads
