@@ -617,20 +617,39 @@ def extra_bench(args, ctx, torch, dev, QD):
     projs = [(576, 576), (192, 576), (192, 576), (576, 576), (1536, 576), (1536, 576),
              (576, 1536)]
     Ls = [_layer(torch, dev, QD, ctx, g, N, K, 2048, 8, 16.0) for N, K in projs]
+    # q / k / v read one normed input, gate / up another: each group runs
+    # through the grouped entry points (one launch per stage); o and down
+    # alone
+    groups = [[0, 1, 2], [3], [4, 5], [6]]
 
-    def c4_fb():
+    def c4_per_layer():
         for L in Ls:
             _fwd_bwd(QD, ctx, L)
+
+    def c4_fb():
+        for grp in groups:
+            if len(grp) == 1:
+                _fwd_bwd(QD, ctx, Ls[grp[0]])
+                continue
+            G = [Ls[i] for i in grp]
+            lay = [(L["qw"], L["lora"]) for L in G]
+            QD.forward_shared(lay, G[0]["x"], 2048, [L["y"] for L in G], [L["t1"] for L in G],
+                              ctx=ctx)
+            QD.backward_shared(lay, G[0]["x"], [L["dy"] for L in G], 2048, G[0]["gx"],
+                               [L["ga"] for L in G], [L["gb"] for L in G],
+                               [L["t1"] for L in G], ctx=ctx)
     ms = _timed_ms(torch, c4_fb, 5)
+    ms_pl = _timed_ms(torch, c4_per_layer, 5)
     f = sum(_fwd_bwd_flops(L) for L in Ls)
     tens = []
     for L in Ls:
         tens += [(L["a"].clone(), L["ga"]), (L["b"].clone(), L["gb"])]
     ad = _adam_step_ms(torch, ctx, tens, max_resident_pages=4)
     out["C4"] = dict(workload=("fwd+bwd of q/k/v/o/gate/up/down (SmolLM-135M shapes, "
-                               "2048 tokens, r=8), then one 8-bit Adam step over the "
-                               "14 adapter tensors"),
-                     fwd_bwd_ms=ms, flops=f, tflops=f / (ms * 1e9),
+                               "2048 tokens, r=8; q/k/v and gate/up as groups sharing "
+                               "their input), then one 8-bit Adam step over the 14 "
+                               "adapter tensors"),
+                     fwd_bwd_ms=ms, per_layer_ms=ms_pl, flops=f, tflops=f / (ms * 1e9),
                      frac_fp32_peak=f / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS, adam=ad,
                      step_ms=ms + ad["ms"])
     del Ls, tens

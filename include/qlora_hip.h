@@ -351,6 +351,30 @@ QH_API qh_status qh_weight_upload(qh_ctx *ctx, const qh_qweight *host,
 QH_API qh_status qh_dweight_view(const qh_dweight *w, qh_qweight *view);
 QH_API void qh_dweight_destroy(qh_dweight *w);
 
+/* Projections that read the same activations: the q / k / v projections of
+ * one normed input, or gate / up (no counterpart in the reference, whose
+ * layers run one call each: qlora-wgpu/src/kernels.rs:262-353).  All layers
+ * share in_dim; count <= 8.  The forward gives each layer i what
+ * qh_qlora_forward_dev(ctx, &ws[i], loras[i], d_x, x_dtype, batch, d_ys[i],
+ * d_t1s ? d_t1s[i] : NULL, stream) gives, within the GEMM tolerance; the
+ * backward writes each layer's grad_A / grad_B as qh_qlora_backward_dev does
+ * and d_grad_x = the sum of the layers' input gradients (qlora-model's
+ * block_backward sums them: llama.rs:563-567, 580-593).  Groups of 2-3
+ * layers that fit the grouped kernels run as one launch per stage (T1, the
+ * base GEMMs; Ds, grad_A with grad_B, the input gradient); others run layer
+ * by layer.  loras[i] NULL = no adapter (its gradient entries are ignored). */
+QH_API qh_status qh_qlora_forward_shared_dev(qh_ctx *ctx, size_t count,
+                                             const qh_qweight *ws,
+                                             const qh_lora *const *loras,
+                                             const void *d_x, int x_dtype,
+                                             size_t batch, float *const *d_ys,
+                                             float *const *d_t1s, void *stream);
+QH_API qh_status qh_qlora_backward_shared_dev(
+    qh_ctx *ctx, size_t count, const qh_qweight *ws, const qh_lora *const *loras,
+    const void *d_x, const void *const *d_dys, int act_dtype, size_t batch,
+    const float *const *d_t1s, float *d_grad_x, float *const *d_grad_as,
+    float *const *d_grad_bs, void *stream);
+
 /* ---- a decoder block's MLP on device ----------------------------------------
  * The MLP half of `block_forward` / `block_backward` (qlora-model/src/
  * llama.rs:449-463, 554-574) with its three projections as QLoRA layers

@@ -1,0 +1,151 @@
+"""GPU parity of the grouped projections that read the same activations
+(qh_qlora_forward_shared_dev / qh_qlora_backward_shared_dev): every layer's
+Y, T1, grad_A and grad_B and the summed input gradient against the
+per-layer entry points (themselves oracle-tested), and, at a small size,
+against the oracle (qlora-core's QloraLinear::forward / backward,
+qlora.rs:86-165, with the input gradients added as block_backward adds them,
+qlora-model/src/llama.rs:563-567, 580-593).
+
+Tolerance: the grouped path sums in another order (the input gradient inside
+the GEMM's accumulators instead of an add per layer; no split reduction):
+max |grouped - per-layer| <= 1e-4 * max |per-layer| per tensor; against the
+oracle the GEMM bar max |d| <= 1e-4 * sqrt(K) * rms(a) * rms(b) (fp32) or
+5e-3 (bf16 activations), K the reduction length.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(300)]
+
+torch = pytest.importorskip("torch")
+
+
+def _layers(QD, ctx, g, Ns, K, r, adapters, dev):
+    out = []
+    for N, ad in zip(Ns, adapters):
+        w = torch.randn(N, K, device=dev, generator=g) * 0.02
+        W = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+        lo = None
+        if ad:
+            a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) / math.sqrt(K)
+            b = torch.randn(N, r, device=dev, generator=g) * 0.01
+            lo = (a, b, QD.lora_struct(a, b, r, 16.0))
+        out.append((W, lo))
+    return out
+
+
+def _rel(got, ref):
+    return float((got - ref).abs().max()) / max(float(ref.abs().max()), 1e-30)
+
+
+CASES = [
+    # (Ns, K, M, r, adapters): C4's q/k/v and gate/up (SmolLM-135M, 2048 tokens)
+    ((576, 192, 192), 576, 2048, 8, (True, True, True)),
+    ((1536, 1536), 576, 2048, 8, (True, True)),
+    ((576, 192, 192), 576, 2048, 8, (True, False, True)),
+    # ragged tokens, ranks of 16 and 64
+    ((256, 128), 512, 1000, 16, (True, True)),
+    ((384, 128, 128), 256, 300, 64, (False, True, True)),
+    # layer by layer: in_dim not a multiple of 64, and four layers
+    ((192, 64), 200, 256, 8, (True, True)),
+    ((128, 64, 64, 64), 256, 256, 8, (True, True, True, True)),
+]
+
+
+@pytest.mark.parametrize("act", ["float32", "bfloat16"])
+@pytest.mark.parametrize("Ns,K,M,r,adapters", CASES)
+def test_shared_matches_per_layer(ctx, act, Ns, K, M, r, adapters):
+    from qlora_hip import device as QD
+    print(f"shared Ns={Ns} K={K} M={M} r={r} adapters={adapters} act={act}", flush=True)
+    dev = torch.device("cuda:0")
+    dt = getattr(torch, act)
+    g = torch.Generator(device="cuda").manual_seed(0x5A4ED + M + K)
+    L = _layers(QD, ctx, g, Ns, K, r, adapters, dev)
+    x = torch.randn(M, K, device=dev, generator=g).to(dt)
+    dys = [torch.randn(M, N, device=dev, generator=g).to(dt) for N in Ns]
+    lay = [(W, lo[2] if lo else None) for W, lo in L]
+    # per layer
+    ys0, t10, ga0, gb0 = [], [], [], []
+    gx0 = torch.zeros(M, K, device=dev)
+    for (W, lo), dy in zip(L, dys):
+        y = torch.empty(M, W.rows, device=dev)
+        t1 = torch.empty(M, r, device=dev) if lo else None
+        QD.forward(W, lo[2] if lo else None, x, M, y, t1=t1, ctx=ctx)
+        gx = torch.empty(M, K, device=dev)
+        ga = torch.empty(r, K, device=dev) if lo else None
+        gb = torch.empty(W.rows, r, device=dev) if lo else None
+        QD.backward(W, lo[2] if lo else None, x, dy, M, gx, ga, gb, t1=t1, ctx=ctx)
+        gx0 += gx
+        ys0.append(y), t10.append(t1), ga0.append(ga), gb0.append(gb)
+    # grouped
+    ys = [torch.empty(M, W.rows, device=dev) for W, _ in L]
+    t1s = [torch.empty(M, r, device=dev) if lo else None for _, lo in L]
+    QD.forward_shared(lay, x, M, ys, t1s, ctx=ctx)
+    gx = torch.empty(M, K, device=dev)
+    gas = [torch.empty(r, K, device=dev) if lo else None for _, lo in L]
+    gbs = [torch.empty(W.rows, r, device=dev) if lo else None for W, lo in L]
+    QD.backward_shared(lay, x, dys, M, gx, gas, gbs, t1s, ctx=ctx)
+    torch.cuda.synchronize()
+    tol = 1e-4
+    for i in range(len(L)):
+        assert _rel(ys[i], ys0[i]) <= tol, (i, "y", _rel(ys[i], ys0[i]))
+        if t1s[i] is not None:
+            assert _rel(t1s[i], t10[i]) <= tol, (i, "t1")
+            assert _rel(gas[i], ga0[i]) <= tol, (i, "grad_a", _rel(gas[i], ga0[i]))
+            assert _rel(gbs[i], gb0[i]) <= tol, (i, "grad_b", _rel(gbs[i], gb0[i]))
+    assert _rel(gx, gx0) <= tol, ("grad_x", _rel(gx, gx0))
+
+
+def test_shared_against_oracle(ctx):
+    """q/k/v-shaped group (in_dim 256, outputs 256 / 128 / 128, 130 tokens,
+    r = 8) against qlora-core's forward / backward per layer, input
+    gradients summed."""
+    from qlora_hip import device as QD
+    dev = torch.device("cuda:0")
+    Ns, K, M, r, alpha = (256, 128, 128), 256, 130, 8, 16.0
+    rng = O.Rng(0x5AED)
+    L, ps = [], []
+    for N in Ns:
+        w = rng.normal(N * K, 0.02)
+        W = QD.DeviceWeight.quantize(torch.from_numpy(w).to(dev).view(N, K), ctx=ctx)
+        a = rng.uniform(r * K, -1 / math.sqrt(K), 1 / math.sqrt(K))
+        b = rng.normal(N * r, 0.01)
+        ta, tb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+        L.append((W, QD.lora_struct(ta, tb, r, alpha), ta, tb))
+        ps.append((O.dequantize(O.quantize(w)), a, b))
+    x = rng.normal(M * K)
+    dys = [rng.normal(M * N) for N in Ns]
+    tx = torch.from_numpy(x).to(dev).view(M, K)
+    ys = [torch.empty(M, N, device=dev) for N in Ns]
+    t1s = [torch.empty(M, r, device=dev) for _ in Ns]
+    lay = [(W, lo) for W, lo, _, _ in L]
+    QD.forward_shared(lay, tx, M, ys, t1s, ctx=ctx)
+    gx = torch.empty(M, K, device=dev)
+    gas = [torch.empty(r, K, device=dev) for _ in Ns]
+    gbs = [torch.empty(N, r, device=dev) for N in Ns]
+    QD.backward_shared(lay, tx, [torch.from_numpy(d).to(dev).view(M, N) for d, N in zip(dys, Ns)],
+                       M, gx, gas, gbs, t1s, ctx=ctx)
+    torch.cuda.synchronize()
+
+    def bar(got, ref, kred, ra, rb, what):
+        got = got.detach().cpu().numpy().ravel().astype(np.float64)
+        err = float(np.max(np.abs(got - np.ravel(ref))))
+        lim = 1e-4 * math.sqrt(kred) * ra * rb
+        assert err <= lim, f"{what}: {err:.3e} > {lim:.3e}"
+    rms = lambda v: float(np.sqrt(np.mean(np.square(np.asarray(v, np.float64)))))  # noqa
+    gsum = np.zeros(M * K)
+    for i, ((wd, a, b), N, dy) in enumerate(zip(ps, Ns, dys)):
+        y = O.qlora_forward(wd, N, K, a, b, r, alpha, x, M)
+        gxi, gai, gbi = O.qlora_backward(wd, N, K, a, b, r, alpha, x, dy, M)
+        gsum += gxi
+        t1 = x.reshape(M, K).astype(np.float64) @ a.reshape(r, K).T.astype(np.float64)
+        ds = alpha / r * (dy.reshape(M, N).astype(np.float64) @ b.reshape(N, r))
+        bar(ys[i], y, K, rms(x), rms(wd), f"y[{i}]")
+        bar(gas[i], gai, M, rms(ds), rms(x), f"grad_a[{i}]")
+        bar(gbs[i], gbi, M, alpha / r * rms(dy), rms(t1), f"grad_b[{i}]")
+    bar(gx, gsum, sum(Ns), rms(np.concatenate(dys)), rms(np.concatenate([p[0] for p in ps])),
+        "grad_x")

@@ -419,10 +419,7 @@ hipError_t run(const GemmArgs &g0, float *partial, hipStream_t s) {
             (unsigned)(g.splits > 1 ? g.splits : 1));
   hipError_t e = qh_launch(k_gemm<BM, BN, WM_, AF, AE, BF, BE, B2F>, grid, dim3(NT), 0, s, g);
   if (e != hipSuccess || g.splits <= 1) return e;
-  const int64_t tot = g.M * g.N;
-  k_reduce_splits<<<dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s>>>(
-      partial, g.splits, g.M * g.N, g.M, g.N, out, ldc);
-  return hipGetLastError();
+  return launch_reduce_splits(partial, g.splits, g.M, g.N, out, ldc, s);
 }
 
 // 128x128 tiles from this many full tiles on: below one tile per CU the
@@ -444,6 +441,15 @@ hipError_t pick_ae(const GemmArgs &g, float *partial, hipStream_t s) {
 }
 
 }  // namespace
+
+hipError_t launch_reduce_splits(const float *part, int splits, int64_t M, int64_t N, float *C,
+                                int64_t ldc, hipStream_t s) {
+  const int64_t tot = M * N;
+  if (tot == 0) return hipSuccess;
+  k_reduce_splits<<<dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s>>>(part, splits, tot,
+                                                                             M, N, C, ldc);
+  return hipGetLastError();
+}
 
 bool nf4_fast_ok(const DevQW &w) { return w.bs == 64 && w.cols % 64 == 0; }
 

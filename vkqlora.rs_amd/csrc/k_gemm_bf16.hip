@@ -17,10 +17,15 @@
 //    one fp32 MFMA five-fold.
 //  * The LoRA segment (fp32 operands) always runs as three MFMAs.
 //
-// Tiles: 512 threads = 8 waves (two per SIMD, so that one wave's dequant
-// work and waits overlap the other's MFMAs) in a 2 x 4 grid; a block
-// computes 256 x BN outputs (BN = 256 or 128), a wave 128 x BN/4 of 32 x 32
-// MFMA tiles whose accumulators stay in registers for the whole reduction.
+// Tiles: large problems use 512 threads = 8 waves (two per SIMD, so that one
+// wave's dequant work and waits overlap the other's MFMAs) in a 2 x 4 grid;
+// a block computes 256 x BN outputs (BN = 256 or 128), a wave 128 x BN/4 of
+// 32 x 32 MFMA tiles whose accumulators stay in registers for the whole
+// reduction.  Small problems (a few hundred 256-row tiles or fewer: a decoder
+// block's projections at a few thousand tokens) use 256 threads = 4 waves in
+// a 2 x 2 grid on 64 x 64 tiles, several blocks per CU, loads two steps
+// ahead, and split the reduction across blocks when the tiles alone cannot
+// fill the GPU (partial sums reduced in a fixed order by a second kernel).
 // The reduction runs in steps of 32 through two LDS stages: while the MFMAs
 // read one stage, the next step's activations and codes are already in
 // registers (loaded at the top of the step) and are dequantized, split and
@@ -41,9 +46,26 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 512;    // 8 waves: two per SIMD
-constexpr int kBM = 256;         // output rows per block
 constexpr int kBK = 32;          // reduction per step = one LDS row
+
+// Block shape: T threads (T / 64 waves in a 2 x T/128 grid), BM x BN outputs;
+// a step reduces KS x 32 (KS LDS sub-tiles between two barriers) and its
+// global loads are issued PF steps before its MFMAs.
+template <int T_, int BM_, int BN_, int PF_ = 1, int KS_ = 1>
+struct Cfg {
+  static constexpr int T = T_, BM = BM_, BN = BN_, PF = PF_, KS = KS_;
+  static_assert(PF == 1 || PF == 2, "prefetch depth");
+  static_assert(KS == 1 || KS == 2, "sub-tiles per step");
+  static constexpr int WGN = T / 128;              // wave grid: 2 x WGN
+  static constexpr int WTM = BM / 2, WTN = BN / WGN;  // one wave's outputs
+  static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32 x 32 MFMA tiles per wave
+  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+  static_assert(BN <= T && BM % (T / 4) == 0, "staging maps");
+};
+using CfgL256 = Cfg<512, 256, 256>;
+using CfgL128 = Cfg<512, 256, 128>;
+using CfgM = Cfg<512, 128, 128, 2, 2>;
+using CfgS = Cfg<256, 64, 64, 2, 2>;
 
 __constant__ float c_lut_bf[17] = QH_NF4_LUT17_INIT;  // the codebook (quant.rs:27-44)
 
@@ -73,81 +95,80 @@ struct ScaleRef {
   float a;    // the fp32 scale, or the super-block absmax
   int32_t c;  // the int8 scale code
 };
+// KIND is the weight's scale store (0: fp32 scales, 1: int8 codes + absmax);
+// a template parameter so that the step loop's loads are the same on every
+// path and the compiler can wait for exactly the ones a step needs.
+template <int KIND>
 __device__ __forceinline__ ScaleRef load_scale(const DevQW &w, int64_t blk) {
-  if (w.kind == 0) return ScaleRef{w.scales[blk], 127};
-  return ScaleRef{w.absmax[blk >> 8], (int32_t)(int8_t)w.scale_codes[blk]};
+  if constexpr (KIND == 0) return ScaleRef{w.scales[blk], 127};
+  else return ScaleRef{w.absmax[blk >> 8], (int32_t)(int8_t)w.scale_codes[blk]};
 }
-__device__ __forceinline__ float decode_scale(int kind, ScaleRef r) {
-  if (kind == 0) return r.a;
-  return (float)((double)(float)r.c * (1.0 / 127.0)) * r.a;
+template <int KIND>
+__device__ __forceinline__ float decode_scale(ScaleRef r) {
+  if constexpr (KIND == 0) return r.a;
+  else return (float)((double)(float)r.c * (1.0 / 127.0)) * r.a;
 }
 
-// ---- activation tile: 256 rows x 32 of a row-major (rows x K) matrix ---------
-// Thread t owns rows t / 4 + 128 v and granule t % 4 (elements 8 (t % 4) ...
-// + 8).  bf16 (XF = 0) is copied; fp32 (XF = 1) is split into hi and lo.
-template <int XF>
+// ---- activation tile: BM rows x 32 of a row-major (rows x K) matrix ----------
+// Thread t owns rows t / 4 + (T / 4) v and granule t % 4 (elements 8 (t % 4)
+// ... + 8).  bf16 (XF = 0) is copied; fp32 (XF = 1) is split into hi and lo.
+template <int XF, class C>
 struct ActTile;
 
-template <>
-struct ActTile<0> {
-  uint4 v[2];
+template <class C>
+struct ActTile<0, C> {
+  static constexpr int P = C::BM / (C::T / 4);  // passes
+  uint4 v[P];
   __device__ __forceinline__ void load(const void *pv, int64_t ld, int64_t m0, int64_t M,
-                                       int64_t k0, int64_t K, bool vec) {
+                                       int64_t k0, int64_t K) {
     const uint16_t *p = (const uint16_t *)pv;
     const int c = threadIdx.x & 3;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int64_t row = m0 + (threadIdx.x >> 2) + 128 * i, k = k0 + 8 * c;
-      if (vec && row < M && k + 8 <= K) {
-        v[i] = *(const uint4 *)(p + row * ld + k);
-      } else {
-        uint32_t e[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) e[j] = (row < M && k + j < K) ? p[row * ld + k + j] : 0u;
-        v[i] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
-                          e[6] | (e[7] << 16));
-      }
+    for (int i = 0; i < P; ++i) {
+      const int64_t row = m0 + (threadIdx.x >> 2) + (C::T / 4) * i, k = k0 + 8 * c;
+      const bool ok = row < M && k < K;
+      uint4 t = *(const uint4 *)(p + (ok ? row * ld + k : 0));
+      if (!ok) t = make_uint4(0, 0, 0, 0);
+      v[i] = t;
     }
   }
   __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *) const {
     const int c = threadIdx.x & 3;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) *(uint4 *)(Sh + sw((threadIdx.x >> 2) + 128 * i, c)) = v[i];
+    for (int i = 0; i < P; ++i) *(uint4 *)(Sh + sw((threadIdx.x >> 2) + (C::T / 4) * i, c)) = v[i];
   }
 };
 
-template <>
-struct ActTile<1> {
-  float4 v[2][2];
+template <class C>
+struct ActTile<1, C> {
+  static constexpr int P = C::BM / (C::T / 4);  // passes
+  float4 v[P][2];
   __device__ __forceinline__ void load(const void *pv, int64_t ld, int64_t m0, int64_t M,
-                                       int64_t k0, int64_t K, bool vec) {
+                                       int64_t k0, int64_t K) {
     const float *p = (const float *)pv;
     const int c = threadIdx.x & 3;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int64_t row = m0 + (threadIdx.x >> 2) + 128 * i, k = k0 + 8 * c;
-      if (vec && row < M && k + 8 <= K) {
-        v[i][0] = *(const float4 *)(p + row * ld + k);
-        v[i][1] = *(const float4 *)(p + row * ld + k + 4);
-      } else {
-        float e[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) e[j] = (row < M && k + j < K) ? p[row * ld + k + j] : 0.0f;
-        v[i][0] = make_float4(e[0], e[1], e[2], e[3]);
-        v[i][1] = make_float4(e[4], e[5], e[6], e[7]);
-      }
+    for (int i = 0; i < P; ++i) {
+      const int64_t row = m0 + (threadIdx.x >> 2) + (C::T / 4) * i, k = k0 + 8 * c;
+      const bool ok = row < M && k < K;
+      const float *q = p + (ok ? row * ld + k : 0);
+      float4 t0 = *(const float4 *)q, t1 = *(const float4 *)(q + 4);
+      if (!ok) t0 = z, t1 = z;  // (a select of whole vectors went to scratch)
+      v[i][0] = t0;
+      v[i][1] = t1;
     }
   }
   __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl) const {
     const int c = threadIdx.x & 3;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < P; ++i) {
       uint32_t h[4], l[4];
       split2(v[i][0].x, v[i][0].y, h[0], l[0]);
       split2(v[i][0].z, v[i][0].w, h[1], l[1]);
       split2(v[i][1].x, v[i][1].y, h[2], l[2]);
       split2(v[i][1].z, v[i][1].w, h[3], l[3]);
-      const int o = sw((threadIdx.x >> 2) + 128 * i, c);
+      const int o = sw((threadIdx.x >> 2) + (C::T / 4) * i, c);
       *(uint4 *)(Sh + o) = make_uint4(h[0], h[1], h[2], h[3]);
       *(uint4 *)(Sl + o) = make_uint4(l[0], l[1], l[2], l[3]);
     }
@@ -157,28 +178,29 @@ struct ActTile<1> {
 // ---- NF4 tile, forward orientation: BN W rows (output columns) x 32 ----------
 // W row n = n0 + t / TPR, elements (t % TPR) * EPT ... + EPT of the step
 // (within one 64-element block, so one scale).
-template <int BN>
+template <class C, int KIND>
 struct WTileRow {
-  static constexpr int TPR = kThreads / BN;     // threads per W row: 2 or 4
+  static constexpr int TPR = C::T / C::BN;      // threads per W row: 2 or 4
   static constexpr int EPT = kBK / TPR;         // elements per thread: 16 or 8
+  static_assert(TPR == 2 || TPR == 4, "threads per W row");
   uint2 c;        // EPT / 2 code bytes
   ScaleRef sr;
   __device__ __forceinline__ void load(const DevQW &w, int64_t n0, int64_t k0) {
     const int64_t n = n0 + threadIdx.x / TPR;
     const int64_t k = k0 + (threadIdx.x % TPR) * EPT;
-    c = make_uint2(0, 0);
-    sr = ScaleRef{0.0f, 0};
-    if (n < w.rows) {
-      const int64_t e = n * w.cols + k;
-      if (EPT == 16) c = *(const uint2 *)(w.codes + (e >> 1));
-      else c.x = *(const uint32_t *)(w.codes + (e >> 1));
-      sr = load_scale(w, e >> 6);
-    }
+    const bool ok = n < w.rows && k < w.cols;
+    const int64_t e = ok ? n * w.cols + k : 0;
+    uint2 t;
+    if (EPT == 16) t = *(const uint2 *)(w.codes + (e >> 1));
+    else t = make_uint2(*(const uint32_t *)(w.codes + (e >> 1)), 0u);
+    const ScaleRef r = load_scale<KIND>(w, e >> 6);
+    if (!ok) t = make_uint2(0, 0);
+    c = t;
+    sr = ScaleRef{ok ? r.a : 0.0f, r.c};
   }
-  __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl, const float *lut,
-                                        int kind) const {
+  __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl, const float *lut) const {
     const int row = threadIdx.x / TPR, g0 = (threadIdx.x % TPR) * (EPT / 8);
-    const float s = decode_scale(kind, sr);
+    const float s = decode_scale<KIND>(sr);
     const uint32_t cw[2] = {c.x, c.y};
 #pragma unroll
     for (int q = 0; q < EPT / 8; ++q) {  // 8 elements = one code word = one granule
@@ -196,40 +218,36 @@ struct WTileRow {
 };
 
 // ---- NF4 tile, input-gradient orientation: 32 W rows (reduction) x BN W
-// columns (outputs), written transposed (LDS row = W column).  Lane l of
-// wave w holds one code byte (W columns c0 + 128 (w / 4) + 2 l, + 1) of the
-// RPT W rows n0 + RPT (w % RG) ... + RPT, so consecutive lanes write LDS
-// rows two apart (BN = 256; BN = 128 folds the column halves into the row
-// groups).
-template <int BN>
+// columns (outputs), written transposed (LDS row = W column).  Thread t holds
+// one code byte (W columns c0 + 2 (t % BPR), + 1) of the RPT W rows n0 + RPT
+// (t / BPR) ... + RPT, so consecutive lanes write LDS rows two apart.
+template <class C, int KIND>
 struct WTileCol {
-  static constexpr int RG = BN == 256 ? 4 : 8;  // row groups
+  static constexpr int BPR = C::BN / 2;         // code bytes per W row
+  static constexpr int RG = C::T / BPR;         // row groups
   static constexpr int RPT = kBK / RG;          // rows per thread: 8 or 4
+  static_assert(RPT == 8 || RPT == 4, "rows per thread");
   uint8_t c[RPT];
   ScaleRef sr[RPT];
   __device__ __forceinline__ void load(const DevQW &w, int64_t c0, int64_t n0) {
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t col = c0 + (BN == 256 ? 128 * (wv / RG) : 0) + 2 * lane;
-    const int64_t row0 = n0 + RPT * (wv % RG);
+    const int64_t col = c0 + 2 * (threadIdx.x % BPR);
+    const int64_t row0 = n0 + RPT * (threadIdx.x / BPR);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       const int64_t n = row0 + i;
-      c[i] = 0;
-      sr[i] = ScaleRef{0.0f, 0};
-      if (n < w.rows && col < w.cols) {
-        const int64_t e = n * w.cols + col;
-        c[i] = w.codes[e >> 1];
-        sr[i] = load_scale(w, e >> 6);
-      }
+      const bool ok = n < w.rows && col < w.cols;
+      const int64_t e = ok ? n * w.cols + col : 0;
+      const uint8_t t = w.codes[e >> 1];
+      const ScaleRef r = load_scale<KIND>(w, e >> 6);
+      c[i] = ok ? t : (uint8_t)0;
+      sr[i] = ScaleRef{ok ? r.a : 0.0f, r.c};
     }
   }
-  __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl, const float *lut,
-                                        int kind) const {
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int cl = (BN == 256 ? 128 * (wv / RG) : 0) + 2 * lane, rl = RPT * (wv % RG);
+  __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl, const float *lut) const {
+    const int cl = 2 * (threadIdx.x % BPR), rl = RPT * (threadIdx.x / BPR);
     float s[RPT];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = decode_scale(kind, sr[i]);
+    for (int i = 0; i < RPT; ++i) s[i] = decode_scale<KIND>(sr[i]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {  // W column cl + j: RPT consecutive reduction rows
       float f[RPT];
@@ -252,15 +270,17 @@ struct WTileCol {
 
 // ---- LoRA segment tiles (fp32 operands, split into hi / lo) -----------------
 // R rows x 32 of a row-major fp32 matrix (element (row, k) at p[row * ld + k]),
-// scaled by `scale`: thread t owns rows t / 8 + 64 v, elements 4 (t % 8) ... + 4.
-template <int R>
+// scaled by `scale`: thread t of T owns rows t / 8 + (T / 8) v, elements
+// 4 (t % 8) ... + 4.
+template <int R, int T>
 __device__ __forceinline__ void stage_f32_rowk(const float *p, int64_t ld, int64_t r0, int64_t rlim,
                                                int64_t k0, int64_t klim, float scale,
                                                uint16_t *Sh, uint16_t *Sl) {
+  static_assert(R % (T / 8) == 0, "rows per pass");
   const int c = threadIdx.x & 7;
 #pragma unroll
-  for (int i = 0; i < R / 64; ++i) {
-    const int rl = (threadIdx.x >> 3) + 64 * i;
+  for (int i = 0; i < R / (T / 8); ++i) {
+    const int rl = (threadIdx.x >> 3) + (T / 8) * i;
     const int64_t row = r0 + rl, k = k0 + 4 * c;
     float f[4];
 #pragma unroll
@@ -275,13 +295,14 @@ __device__ __forceinline__ void stage_f32_rowk(const float *p, int64_t ld, int64
 }
 
 // 32 x R of a row-major fp32 matrix read transposed (element (col, k) at
-// p[k * ld + col]): thread t owns reduction rows t / (R / 4) + KS v and
+// p[k * ld + col]): thread t of T owns reduction rows t / (R / 4) + KS v and
 // columns 4 (t % (R / 4)) ... + 4.
-template <int R>
+template <int R, int T>
 __device__ __forceinline__ void stage_f32_krow(const float *p, int64_t ld, int64_t c0, int64_t clim,
                                                int64_t k0, int64_t klim, float scale,
                                                uint16_t *Sh, uint16_t *Sl) {
-  constexpr int CG = R / 4, KS = kThreads / CG;
+  constexpr int CG = R / 4, KS = T / CG;
+  static_assert(KS <= kBK && kBK % KS == 0, "reduction rows per pass");
   const int cl = 4 * (threadIdx.x % CG);
 #pragma unroll
   for (int i = 0; i < kBK / KS; ++i) {
@@ -302,30 +323,40 @@ __device__ __forceinline__ void stage_f32_krow(const float *p, int64_t ld, int64
 
 // ---- the kernel --------------------------------------------------------------
 // WF = ROWK: forward (W rows are the output columns); WF = KROW: grad_x (W
-// rows are the reduction).  XF: activations bf16 (0) or fp32 (1).  8 waves
-// in a 2 x 4 grid, each 128 x BN/4 of the block's 256 x BN outputs.  LDS
-// per stage: Ah[256][32], Al[256][32], Bh[BN][32], Bl[BN][32]; two stages,
-// then the 16-entry codebook.
-template <int BN, int WF, int XF>
-__global__ __launch_bounds__(kThreads, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_n) {
-  constexpr int TM = 4, TN = BN / 128;  // 32 x 32 tiles per wave
-  constexpr int WN = BN / 4;
-  constexpr int A_ELEMS = kBM * kBK, B_ELEMS = BN * kBK;
-  constexpr int STAGE = 2 * A_ELEMS + 2 * B_ELEMS;
+// rows are the reduction).  XF: activations bf16 (0) or fp32 (1).  Waves in
+// a 2 x WGN grid, each WTM x WTN of the block's BM x BN outputs.  LDS per
+// stage: Ah[BM][32], Al[BM][32], Bh[BN][32], Bl[BN][32]; two stages, then the
+// 16-entry codebook.  gridDim.y > 1 splits the reduction: block (x, z)
+// covers steps [z S / Z, (z + 1) S / Z) of the S 32-wide steps and writes its
+// partial sums to C + z * split_stride; the LoRA segment goes to split 0.
+template <class C, int WF, int XF, int KIND>
+__global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_n) {
+  constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN, KS = C::KS;
+  constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
+  constexpr int SUB = 2 * A_ELEMS + 2 * B_ELEMS;  // one 32-wide sub-tile
+  constexpr int STAGE = KS * SUB;
   extern __shared__ __align__(16) uint16_t smem[];
   float *lut = (float *)(smem + 2 * STAGE);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  const int wm0 = (wave >> 2) * 128, wn0 = (wave & 3) * WN;
+  const int wm0 = (wave / C::WGN) * C::WTM, wn0 = (wave % C::WGN) * C::WTN;
   // Blocks go to the 8 XCDs round robin (block b to XCD b % 8): give each
   // XCD a contiguous run of tiles (whole rows of them), so that the blocks
   // sharing an activation panel share an L2.
   const int nb = (int)gridDim.x;
   int tb = (int)blockIdx.x;
   if (nb % 8 == 0) tb = (tb % 8) * (nb / 8) + tb / 8;
-  const int64_t m0 = (int64_t)(tb / tiles_n) * kBM, n0 = (int64_t)(tb % tiles_n) * BN;
+  const int64_t m0 = (int64_t)(tb / tiles_n) * BM, nt = tb % tiles_n;
+  // forward: the output tile's segment (the tiles of segment s start at
+  // seg[s].tile0); input gradient: one output, all segments reduced
+  int sg = 0;
+  if (WF == ROWK)
+    while (sg + 1 < g.nseg && nt >= g.seg[sg + 1].tile0) ++sg;
+  const int64_t n0 = (nt - (WF == ROWK ? g.seg[sg].tile0 : 0)) * BN;
+  const int64_t n_end = WF == ROWK ? g.seg[sg].len : g.N;  // output columns
+  const int z = (int)blockIdx.y, nz = (int)gridDim.y;
   if (tid < 16) lut[tid] = c_lut_bf[tid];
 
   f32x16 acc[TM][TN];
@@ -374,51 +405,126 @@ __global__ __launch_bounds__(kThreads, 2) void k_nf4_bf16(Bf16GemmArgs g, int ti
   };
 
   // ---- segment 1: activations x dequantized weight ---------------------------
-  const bool a_vec = (g.lda % 8 == 0) && ((((uintptr_t)g.A) & 15) == 0);
-  const int kind = g.w.kind;
-  ActTile<XF> at;
-  typename std::conditional<WF == ROWK, WTileRow<BN>, WTileCol<BN>>::type wt;
-  const int64_t steps = (g.K + kBK - 1) / kBK;
-  auto stage = [&](uint16_t *D) {
-    at.store(D, D + A_ELEMS);
-    wt.store(D + 2 * A_ELEMS, D + 2 * A_ELEMS + B_ELEMS, lut, kind);
+  using WT = typename std::conditional<WF == ROWK, WTileRow<C, KIND>, WTileCol<C, KIND>>::type;
+  struct Regs {  // one step's loads: KS sub-tiles
+    ActTile<XF, C> a[KS];
+    WT w[KS];
   };
-  if (steps > 0) {
-    at.load(g.A, g.lda, m0, g.M, 0, g.K, a_vec);
-    wt.load(g.w, n0, 0);
-    __syncthreads();  // codebook
-    stage(smem);
-    __syncthreads();
-    for (int64_t t = 0; t < steps; ++t) {
-      const bool more = t + 1 < steps;
-      if (more) {
-        at.load(g.A, g.lda, m0, g.M, (t + 1) * kBK, g.K, a_vec);
-        wt.load(g.w, n0, (t + 1) * kBK);
+  // Steps of KS x 32: the forward walks K; the input gradient walks the
+  // segments one after the other, each from its first row.
+  constexpr int64_t SK = KS * kBK;
+  int64_t steps = 0;
+  if (WF == ROWK) {
+    steps = (g.K + SK - 1) / SK;
+  } else {
+    for (int i = 0; i < g.nseg; ++i) steps += (g.seg[i].len + SK - 1) / SK;
+  }
+  const int64_t t0 = steps * z / nz, t1 = steps * (z + 1) / nz;
+  auto stage = [&](uint16_t *D, const Regs &R) {
+#pragma unroll
+    for (int u = 0; u < KS; ++u) {
+      uint16_t *E = D + u * SUB;
+      R.a[u].store(E, E + A_ELEMS);
+      R.w[u].store(E + 2 * A_ELEMS, E + 2 * A_ELEMS + B_ELEMS, lut);
+    }
+  };
+  auto load = [&](Regs &R, int64_t t) {
+    if constexpr (WF == ROWK) {
+#pragma unroll
+      for (int u = 0; u < KS; ++u) {
+        const int64_t k = (t * KS + u) * kBK;
+        R.a[u].load(g.A, g.lda, m0, g.M, k, g.K);
+        R.w[u].load(g.seg[sg].w, n0, k);
       }
-      const uint16_t *S = smem + (t & 1) * STAGE;
-      mma(S, S + A_ELEMS, S + 2 * A_ELEMS, S + 2 * A_ELEMS + B_ELEMS, XF == 1);
-      if (more) stage(smem + ((t + 1) & 1) * STAGE);
+    } else {
+      int i = 0;
+      int64_t tl = t;
+      for (; i + 1 < g.nseg; ++i) {
+        const int64_t st = (g.seg[i].len + SK - 1) / SK;
+        if (tl < st) break;
+        tl -= st;
+      }
+      const Bf16Seg &q = g.seg[i];
+#pragma unroll
+      for (int u = 0; u < KS; ++u) {
+        const int64_t k = (tl * KS + u) * kBK;
+        R.a[u].load(q.A, q.lda, m0, g.M, k, q.len);
+        R.w[u].load(q.w, n0, k);
+      }
+    }
+  };
+  auto mma_stage = [&](const uint16_t *S) {
+#pragma unroll
+    for (int u = 0; u < KS; ++u) {
+      const uint16_t *E = S + u * SUB;
+      mma(E, E + A_ELEMS, E + 2 * A_ELEMS, E + 2 * A_ELEMS + B_ELEMS, XF == 1);
+    }
+  };
+  Regs ra;
+  if constexpr (C::PF == 1) {
+    if (t1 > t0) {
+      load(ra, t0);
+      __syncthreads();  // codebook
+      stage(smem, ra);
       __syncthreads();
+      for (int64_t t = t0; t < t1; ++t) {
+        const bool more = t + 1 < t1;
+        if (more) load(ra, t + 1);
+        mma_stage(smem + ((t - t0) & 1) * STAGE);
+        if (more) stage(smem + ((t + 1 - t0) & 1) * STAGE, ra);
+        __syncthreads();
+      }
+    }
+  } else {
+    // Two register sets: at the top of step t the LDS stage of t is full, the
+    // loads of step t + 1 are in flight in one set and step t + 2's go out
+    // into the other, so each load has two steps of MFMAs to arrive.  The
+    // loop runs two steps per turn to keep the sets in fixed registers.
+    Regs rb;
+    uint16_t *S0 = smem, *S1 = smem + STAGE;
+    if (t1 > t0) {
+      load(ra, t0);
+      if (t0 + 1 < t1) load(rb, t0 + 1);
+      __syncthreads();  // codebook
+      stage(S0, ra);
+      __syncthreads();
+      for (int64_t t = t0; t < t1; t += 2) {
+        if (t + 2 < t1) load(ra, t + 2);
+        mma_stage(S0);
+        if (t + 1 < t1) stage(S1, rb);
+        __syncthreads();
+        if (t + 1 >= t1) break;
+        if (t + 3 < t1) load(rb, t + 3);
+        mma_stage(S1);
+        if (t + 2 < t1) stage(S0, ra);
+        __syncthreads();
+      }
     }
   }
 
-  // ---- segment 2: the LoRA term, three MFMAs per tile ------------------------
-  if (g.K2 > 0) {
+  // ---- the LoRA terms, three MFMAs per tile ----------------------------------
+  if (z == 0) {
     uint16_t *Ah = smem, *Al = smem + A_ELEMS;
     uint16_t *Bh = smem + 2 * A_ELEMS, *Bl = smem + 2 * A_ELEMS + B_ELEMS;
-    for (int64_t k0 = 0; k0 < g.K2; k0 += kBK) {
-      stage_f32_rowk<kBM>(g.A2, g.lda2, m0, g.M, k0, g.K2, 1.0f, Ah, Al);
-      if (g.b2form == ROWK)
-        stage_f32_rowk<BN>(g.B2, g.ldb2, n0, g.N, k0, g.K2, g.b2scale, Bh, Bl);
-      else
-        stage_f32_krow<BN>(g.B2, g.ldb2, n0, g.N, k0, g.K2, g.b2scale, Bh, Bl);
-      __syncthreads();
-      mma(Ah, Al, Bh, Bl, true);
-      __syncthreads();
+    const int i0 = WF == ROWK ? sg : 0, i1 = WF == ROWK ? sg + 1 : g.nseg;
+    for (int i = i0; i < i1; ++i) {
+      const Bf16Seg &q = g.seg[i];
+      for (int64_t k0 = 0; k0 < q.K2; k0 += kBK) {
+        stage_f32_rowk<BM, C::T>(q.A2, q.lda2, m0, g.M, k0, q.K2, 1.0f, Ah, Al);
+        if (WF == ROWK)
+          stage_f32_rowk<BN, C::T>(q.B2, q.ldb2, n0, n_end, k0, q.K2, q.b2scale, Bh, Bl);
+        else
+          stage_f32_krow<BN, C::T>(q.B2, q.ldb2, n0, n_end, k0, q.K2, q.b2scale, Bh, Bl);
+        __syncthreads();
+        mma(Ah, Al, Bh, Bl, true);
+        __syncthreads();
+      }
     }
   }
 
   // ---- epilogue ---------------------------------------------------------------
+  float *Cz = (WF == ROWK ? g.seg[sg].C : g.C) + (nz > 1 ? (int64_t)z * g.split_stride : 0);
+  const int64_t ldc = WF == ROWK ? g.seg[sg].ldc : g.ldc;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -427,14 +533,14 @@ __global__ __launch_bounds__(kThreads, 2) void k_nf4_bf16(Bf16GemmArgs g, int ti
       for (int v = 0; v < 16; ++v) {
         const int64_t m = m0 + wm0 + 32 * i + 8 * (v / 4) + 4 * h + (v % 4);
         const int64_t n = n0 + wn0 + 32 * j + l32;
-        if (m < g.M && n < g.N) g.C[m * g.ldc + n] = g.alpha * acc[i][j][v];
+        if (m < g.M && n < n_end) Cz[m * ldc + n] = g.alpha * acc[i][j][v];
       }
 }
 
-template <int BN, int WF, int XF>
-hipError_t run_bf16(const Bf16GemmArgs &g, hipStream_t s) {
-  auto k = k_nf4_bf16<BN, WF, XF>;
-  constexpr uint32_t lds = (uint32_t)(2 * (2 * kBM + 2 * BN) * kBK * 2 + 16 * 4);
+template <class C, int WF, int XF, int KIND>
+hipError_t run_bf16(const Bf16GemmArgs &g0, int splits, float *partial, hipStream_t s) {
+  auto k = k_nf4_bf16<C, WF, XF, KIND>;
+  constexpr uint32_t lds = (uint32_t)(2 * C::KS * (2 * C::BM + 2 * C::BN) * kBK * 2 + 16 * 4);
   static bool attr = false;  // per instantiation
   if (!attr) {
     const hipError_t e =
@@ -442,34 +548,123 @@ hipError_t run_bf16(const Bf16GemmArgs &g, hipStream_t s) {
     if (e != hipSuccess) return e;
     attr = true;
   }
-  const int tiles_n = (int)((g.N + BN - 1) / BN);
-  const int tiles_m = (int)((g.M + kBM - 1) / kBM);
-  return qh_launch(k, dim3((unsigned)(tiles_n * tiles_m)), dim3(kThreads), lds, s, g, tiles_n);
+  Bf16GemmArgs g = g0;
+  int tiles_n = 0;
+  if (WF == ROWK) {
+    for (int i = 0; i < g.nseg; ++i) {
+      g.seg[i].tile0 = tiles_n;
+      tiles_n += (int)((g.seg[i].len + C::BN - 1) / C::BN);
+    }
+  } else {
+    tiles_n = (int)((g.N + C::BN - 1) / C::BN);
+  }
+  if (splits > 1) {
+    if (WF == ROWK) {  // one segment (checked by the caller)
+      g.seg[0].C = partial;
+      g.seg[0].ldc = g.seg[0].len;
+    } else {
+      g.C = partial;
+      g.ldc = g.N;
+    }
+    g.split_stride = g.M * g.N;
+  }
+  const int tiles_m = (int)((g.M + C::BM - 1) / C::BM);
+  hipError_t e = qh_launch(k, dim3((unsigned)(tiles_n * tiles_m), (unsigned)splits),
+                           dim3(C::T), lds, s, g, tiles_n);
+  if (e != hipSuccess || splits <= 1) return e;
+  return WF == ROWK
+             ? launch_reduce_splits(partial, splits, g.M, g.N, g0.seg[0].C, g0.seg[0].ldc, s)
+             : launch_reduce_splits(partial, splits, g.M, g.N, g0.C, g0.ldc, s);
 }
 
-template <int WF, int XF>
-hipError_t pick_bn(const Bf16GemmArgs &g, hipStream_t s) {
-  // 256 x 256 tiles when they leave no GPU-wide wave of blocks mostly empty
-  // (one block per CU: 256 CUs), else 256 x 128
+// Block shape and reduction splits by problem size.
+//  large:  256 x 256 or 256 x 128 tiles, 8 waves, for problems with at least
+//          256 tiles of 256 x 256 (MFMA-bound: C3, C5);
+//  medium: 128 x 128 tiles, 8 waves, two 32-wide sub-steps per barrier and
+//          loads two steps ahead, for 160 or more tiles of 128 x 128, or
+//          long reductions (24+ steps) over 32+ such tiles;
+//  small:  64 x 64 tiles, 4 waves, the same pipelining.
+// The medium and small blocks' step loops are latency-bound (about 0.7 us
+// per step at C4's shapes), so long reductions are split until the GPU
+// holds about one block per CU (four small ones for reductions of 24+
+// steps), each split keeping at least 6 steps; at most 8 splits and 64 MB of
+// partial sums.
+enum Tier { kLarge, kMedium, kSmall };
+struct Plan {
+  Tier tier;
+  int splits;
+};
+Plan plan_for(int64_t M, int64_t N, int64_t K) {
+  const int64_t steps = (K + kBK - 1) / kBK;
+  if (M >= 256 && N >= 256 && (M / 256) * (N / 256) >= 256) return Plan{kLarge, 1};
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  int64_t tiles, target;
+  Tier tier;
+  if (t128 >= 160 || (steps >= 24 && t128 >= 32)) {
+    tier = kMedium, tiles = t128, target = 256;
+  } else {
+    tier = kSmall, tiles = ((M + 63) / 64) * ((N + 63) / 64), target = steps >= 24 ? 1024 : 256;
+  }
+  int64_t sp = (target + tiles / 2) / (tiles ? tiles : 1);
+  if (sp > 8) sp = 8;
+  if (sp > steps / 6) sp = steps / 6;
+  while (sp > 1 && (size_t)(sp * M * N * 4) > ((size_t)64 << 20)) --sp;
+  return Plan{tier, sp < 1 ? 1 : (int)sp};
+}
+
+template <int WF, int XF, int KIND>
+hipError_t pick(const Bf16GemmArgs &g, int splits, float *partial, hipStream_t s) {
+  const Plan pl = plan_for(g.M, g.N, g.K);
+  if (pl.tier == kSmall) return run_bf16<CfgS, WF, XF, KIND>(g, splits, partial, s);
+  if (pl.tier == kMedium) return run_bf16<CfgM, WF, XF, KIND>(g, splits, partial, s);
   const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
   const int64_t waves = (t256 + 255) / 256;
   const bool wide = t256 >= 192 && (double)t256 / (double)(waves * 256) >= 0.75;
-  return wide ? run_bf16<256, WF, XF>(g, s) : run_bf16<128, WF, XF>(g, s);
+  return wide ? run_bf16<CfgL256, WF, XF, KIND>(g, 1, nullptr, s)
+              : run_bf16<CfgL128, WF, XF, KIND>(g, 1, nullptr, s);
+}
+
+template <int WF, int XF>
+hipError_t pick_kind(const Bf16GemmArgs &g, int splits, float *partial, hipStream_t s) {
+  return g.seg[0].w.kind == 0 ? pick<WF, XF, 0>(g, splits, partial, s)
+                              : pick<WF, XF, 1>(g, splits, partial, s);
 }
 
 }  // namespace
 
-// The bf16-MFMA path needs whole 64-element blocks per W row and enough
-// output tiles to fill the GPU (smaller problems stay on the fp32 tile
-// engine).
-bool bf16_gemm_ok(const DevQW &w, int64_t M, int64_t N) {
-  return w.bs == 64 && w.cols % 64 == 0 && M >= 256 && N >= 256 && (M / 256) * (N / 128) >= 128;
+// The bf16-MFMA path needs whole 64-element blocks per W row, and activation
+// rows it can read as 16-byte vectors (8 elements).
+bool bf16_gemm_ok(const DevQW &w, const void *a, int64_t lda, int64_t K) {
+  return w.bs == 64 && w.cols % 64 == 0 && lda % 8 == 0 && K % 8 == 0 &&
+         (((uintptr_t)a) & 15) == 0;
 }
 
-hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, int a_f32, hipStream_t s) {
+int bf16_gemm_splits(int64_t M, int64_t N, int64_t K) { return plan_for(M, N, K).splits; }
+
+hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, int a_f32, int splits,
+                            float *partial, hipStream_t s) {
   if (g.M == 0 || g.N == 0) return hipSuccess;
-  if (w_form == ROWK) return a_f32 ? pick_bn<ROWK, 1>(g, s) : pick_bn<ROWK, 0>(g, s);
-  return a_f32 ? pick_bn<KROW, 1>(g, s) : pick_bn<KROW, 0>(g, s);
+  if (splits < 1 || (splits > 1 && !partial) || g.nseg < 1 || g.nseg > kMaxBf16Segs ||
+      (splits > 1 && w_form == ROWK && g.nseg != 1))
+    return hipErrorInvalidValue;
+  // activation rows are read as 16-byte vectors of 8 elements: row strides
+  // and lengths multiples of 8, rows 16-byte aligned
+  auto vec_ok = [](const void *a, int64_t lda, int64_t k) {
+    return lda % 8 == 0 && k % 8 == 0 && (((uintptr_t)a) & 15) == 0;
+  };
+  int64_t n_sum = 0;
+  for (int i = 0; i < g.nseg; ++i) {
+    const Bf16Seg &q = g.seg[i];
+    if (q.w.kind != g.seg[0].w.kind) return hipErrorInvalidValue;
+    if (w_form == KROW && !vec_ok(q.A, q.lda, q.len)) return hipErrorInvalidValue;
+    n_sum += q.len;
+  }
+  if (w_form == ROWK && (!vec_ok(g.A, g.lda, g.K) || n_sum != g.N)) return hipErrorInvalidValue;
+  if (w_form == KROW && n_sum != g.K) return hipErrorInvalidValue;
+  if (w_form == ROWK) return a_f32 ? pick_kind<ROWK, 1>(g, splits, partial, s)
+                                   : pick_kind<ROWK, 0>(g, splits, partial, s);
+  return a_f32 ? pick_kind<KROW, 1>(g, splits, partial, s)
+               : pick_kind<KROW, 0>(g, splits, partial, s);
 }
 
 }  // namespace qh

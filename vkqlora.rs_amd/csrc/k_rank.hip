@@ -32,12 +32,17 @@ constexpr int kRankUnroll = 4;  // chunks of 16 k loaded before their MFMAs
 
 __device__ __forceinline__ float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
 
-// NB blocks of 16 output columns (r <= 16 * NB)
+// NB blocks of 16 output columns (r <= 16 * NB); job blockIdx.y of `jobs`.
 template <int QF, int PE, int NB>
-__global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
-    const void *__restrict__ P, int64_t ldp, const float *__restrict__ Q, int64_t ldq,
-    float *__restrict__ out, int64_t ldo, int64_t M, int64_t K, int r, float alpha) {
+__global__ __launch_bounds__(kRankThreads) void k_rank_gemm(RankJobs jobs, int64_t M) {
   __shared__ float red[kRankWaves][kRankRows][16 * NB + 1];
+  const RankJob &jb = jobs.j[blockIdx.y];
+  const void *__restrict__ P = jb.p;
+  const float *__restrict__ Q = jb.q;
+  float *__restrict__ out = jb.out;
+  const int64_t ldp = jb.ldp, ldq = jb.ldq, ldo = jb.ldo, K = jb.k;
+  const int r = jb.r;
+  const float alpha = jb.alpha;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int64_t m0 = (int64_t)blockIdx.x * kRankRows;
@@ -137,16 +142,22 @@ __global__ __launch_bounds__(kRankThreads) void k_rank_gemm(
 // The LoRA-rank GEMMs that reduce over the tokens (qlora.rs:147, 151):
 //   grad_B = s * dY^T . T1   (N x r)      grad_A = Ds^T . X   (r x K)
 // out(c, j) = alpha * sum_m Big[m][c] * Small[m][j], Big (M x C) row-major in
-// fp32 or bf16, Small (M x r) fp32; stored at out[c * ldo + j] (OT = 0) or
-// out[j * ldo + c] (OT = 1).  A workgroup owns 16 columns c and all r, its
+// fp32 or bf16, Small (M x r) fp32; stored at out[c * ldo + j] (out_t = 0) or
+// out[j * ldo + c] (out_t = 1).  A workgroup owns 16 columns c and all r, its
 // 8 waves split the tokens; lane quarter g takes tokens 16t + 4g + e, so a
 // lane's four A values are four rows of one column, coalesced across the
 // quarter's 16 lanes.
-template <int OT, int PE, int NB>
-__global__ __launch_bounds__(kRankThreads) void k_rank_tgemm(
-    const void *__restrict__ Big, int64_t ldb, const float *__restrict__ Small, int64_t lds,
-    float *__restrict__ out, int64_t ldo, int64_t M, int64_t C, int r, float alpha) {
+template <int PE, int NB>
+__global__ __launch_bounds__(kRankThreads) void k_rank_tgemm(RankJobs jobs, int64_t M) {
   __shared__ float red[kRankWaves][16][16 * NB + 1];
+  const RankJob &jb = jobs.j[blockIdx.y];
+  const void *__restrict__ Big = jb.p;
+  const float *__restrict__ Small = jb.q;
+  float *__restrict__ out = jb.out;
+  const int64_t ldb = jb.ldp, lds = jb.ldq, ldo = jb.ldo, C = jb.k;
+  const int r = jb.r, OT = jb.out_t;
+  const float alpha = jb.alpha;
+  if ((int64_t)blockIdx.x * 16 >= C) return;  // a shorter job of the launch
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int64_t c0 = (int64_t)blockIdx.x * 16;
@@ -212,15 +223,15 @@ __global__ __launch_bounds__(kRankThreads) void k_rank_tgemm(
 // every kRankUnroll chunks and the tile engine's split-K has more waves.
 bool rank_gemm_ok(int64_t K, int64_t r) { return r >= 1 && r <= 64 && K >= 1 && K <= 2048; }
 
-hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float *Q, int q_kmajor,
-                            int64_t ldq, float *out, int64_t ldo, int64_t M, int64_t K, int64_t r,
-                            float alpha, hipStream_t s) {
-  if (M == 0 || r == 0) return hipSuccess;
-  const dim3 grid((unsigned)((M + kRankRows - 1) / kRankRows)), block(kRankThreads);
-  const int ri = (int)r;
-#define QH_RANK(QF, PE, NB)                                                                    \
-  return qh_launch(k_rank_gemm<QF, PE, NB>, grid, block, 0, s, P, ldp, Q, ldq, out, ldo, M, K, \
-                   ri, alpha)
+hipError_t launch_rank_gemms(const RankJobs &jobs, int p_bf16, int q_kmajor, int64_t M,
+                             hipStream_t s) {
+  if (M == 0 || jobs.count == 0) return hipSuccess;
+  int rmax = 0;
+  for (int i = 0; i < jobs.count; ++i) rmax = jobs.j[i].r > rmax ? jobs.j[i].r : rmax;
+  if (rmax == 0) return hipSuccess;
+  const dim3 grid((unsigned)((M + kRankRows - 1) / kRankRows), (unsigned)jobs.count);
+  const dim3 block(kRankThreads);
+#define QH_RANK(QF, PE, NB) return qh_launch(k_rank_gemm<QF, PE, NB>, grid, block, 0, s, jobs, M)
 #define QH_RANK_NB(NB)                       \
   if (q_kmajor) {                            \
     if (p_bf16) QH_RANK(1, E_BF16, NB);      \
@@ -228,15 +239,24 @@ hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float 
   }                                          \
   if (p_bf16) QH_RANK(0, E_BF16, NB);        \
   QH_RANK(0, E_F32, NB);
-  if (r <= 16) {
+  if (rmax <= 16) {
     QH_RANK_NB(1)
   }
-  if (r <= 32) {
+  if (rmax <= 32) {
     QH_RANK_NB(2)
   }
   QH_RANK_NB(4)
 #undef QH_RANK_NB
 #undef QH_RANK
+}
+
+hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float *Q, int q_kmajor,
+                            int64_t ldq, float *out, int64_t ldo, int64_t M, int64_t K, int64_t r,
+                            float alpha, hipStream_t s) {
+  RankJobs jobs{};
+  jobs.count = 1;
+  jobs.j[0] = RankJob{P, ldp, Q, ldq, out, ldo, K, (int)r, 0, alpha};
+  return launch_rank_gemms(jobs, p_bf16, q_kmajor, M, s);
 }
 
 }  // namespace qh
@@ -248,31 +268,38 @@ namespace qh {
 // 4096 (C3's: 42-70 against 32 us), where each wave walks twice the tokens.
 bool rank_tgemm_ok(int64_t M, int64_t r) { return r >= 1 && r <= 64 && M >= 1 && M <= 2048; }
 
-hipError_t launch_rank_tgemm(const void *Big, int big_bf16, int64_t ldb, const float *Small,
-                             int64_t lds, float *out, int64_t ldo, int out_t, int64_t M,
-                             int64_t C, int64_t r, float alpha, hipStream_t s) {
-  if (C == 0 || r == 0) return hipSuccess;
-  const dim3 grid((unsigned)((C + 15) / 16)), block(kRankThreads);
-  const int ri = (int)r;
-#define QH_RT(OT, PE, NB)                                                                     \
-  return qh_launch(k_rank_tgemm<OT, PE, NB>, grid, block, 0, s, Big, ldb, Small, lds, out, \
-                   ldo, M, C, ri, alpha)
-#define QH_RT_NB(NB)                    \
-  if (out_t) {                          \
-    if (big_bf16) QH_RT(1, E_BF16, NB); \
-    QH_RT(1, E_F32, NB);                \
-  }                                     \
-  if (big_bf16) QH_RT(0, E_BF16, NB);   \
-  QH_RT(0, E_F32, NB);
-  if (r <= 16) {
+hipError_t launch_rank_tgemms(const RankJobs &jobs, int big_bf16, int64_t M, hipStream_t s) {
+  if (jobs.count == 0) return hipSuccess;
+  int rmax = 0;
+  int64_t cmax = 0;
+  for (int i = 0; i < jobs.count; ++i) {
+    rmax = jobs.j[i].r > rmax ? jobs.j[i].r : rmax;
+    cmax = jobs.j[i].k > cmax ? jobs.j[i].k : cmax;
+  }
+  if (rmax == 0 || cmax == 0) return hipSuccess;
+  const dim3 grid((unsigned)((cmax + 15) / 16), (unsigned)jobs.count), block(kRankThreads);
+#define QH_RT(PE, NB) return qh_launch(k_rank_tgemm<PE, NB>, grid, block, 0, s, jobs, M)
+#define QH_RT_NB(NB)                 \
+  if (big_bf16) QH_RT(E_BF16, NB);   \
+  QH_RT(E_F32, NB);
+  if (rmax <= 16) {
     QH_RT_NB(1)
   }
-  if (r <= 32) {
+  if (rmax <= 32) {
     QH_RT_NB(2)
   }
   QH_RT_NB(4)
 #undef QH_RT_NB
 #undef QH_RT
+}
+
+hipError_t launch_rank_tgemm(const void *Big, int big_bf16, int64_t ldb, const float *Small,
+                             int64_t lds, float *out, int64_t ldo, int out_t, int64_t M,
+                             int64_t C, int64_t r, float alpha, hipStream_t s) {
+  RankJobs jobs{};
+  jobs.count = 1;
+  jobs.j[0] = RankJob{Big, ldb, Small, lds, out, ldo, C, (int)r, out_t, alpha};
+  return launch_rank_tgemms(jobs, big_bf16, M, s);
 }
 
 }  // namespace qh

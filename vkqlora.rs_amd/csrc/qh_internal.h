@@ -78,28 +78,49 @@ struct GemmArgs {
   int64_t split_stride;
 };
 
-// ---- k_gemm_bf16.hip: the large NF4 GEMMs on bf16 MFMA ----
-// C (M x N) = alpha * (A . Wop + A2 . B2), A row-major (M x K, lda), bf16 or
-// (a_f32) fp32 split into bf16 hi and lo parts.
-// w_form ROWK: Wop[k][n] = W[n][k] (forward, W is N x K); KROW: Wop[k][n] =
-// W[k][n] (input gradient, W is K x N).  Segment 2 (K2 > 0): fp32 A2 (M x
-// K2, row-major, lda2) and B2, scaled by b2scale, in form b2form (ROWK:
-// B2[k][n] = p[n * ldb2 + k]; KROW: p[k * ldb2 + n]).
-struct Bf16GemmArgs {
-  int64_t M, N, K;
-  const void *A;
-  int64_t lda;
+// ---- k_gemm_bf16.hip: the NF4 GEMMs on bf16 MFMA ----
+// Up to kMaxBf16Segs weights, each with its LoRA term, in one launch.
+//  w_form ROWK (forward): every segment s reads the shared activations A
+//   (M x K, row stride lda) and writes its own output
+//   C_s (M x len_s) = alpha * (A . W_s^T + A2_s . B2_s),  W_s: len_s x K.
+//  w_form KROW (input gradient): one output C (M x N) sums all segments,
+//   C = alpha * sum_s (A_s . W_s + A2_s . B2_s),  A_s: M x len_s (row stride
+//   lda_s), W_s: len_s x N; K = sum of len_s.
+// A / A_s are bf16 or (a_f32) fp32 split into bf16 hi and lo parts.  The
+// LoRA term: fp32 A2_s (M x K2_s, row-major, lda2) times B2_s scaled by
+// b2scale, B2_s[k][n] = p[n * ldb2 + k] (ROWK) or p[k * ldb2 + n] (KROW).
+constexpr int kMaxBf16Segs = 4;
+struct Bf16Seg {
   DevQW w;
+  const void *A;  // KROW: this segment's activations
+  int64_t lda;
   const float *A2, *B2;
   int64_t lda2, ldb2, K2;
   float b2scale;
-  int b2form;
-  float *C;
+  float *C;  // ROWK: this segment's output
+  int64_t ldc;
+  int64_t len;    // ROWK: output columns; KROW: reduction length
+  int64_t tile0;  // ROWK: first output tile (set by the launcher)
+};
+struct Bf16GemmArgs {
+  int64_t M, N, K;  // N: all output columns, K: the whole reduction
+  const void *A;    // ROWK: the shared activations
+  int64_t lda;
+  float *C;  // KROW: the output
   int64_t ldc;
   float alpha;
+  int64_t split_stride;  // set by the launcher when the reduction is split
+  int nseg;
+  Bf16Seg seg[kMaxBf16Segs];
 };
-bool bf16_gemm_ok(const DevQW &w, int64_t M, int64_t N);
-hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, int a_f32, hipStream_t s);
+// True when the bf16-MFMA kernels take this weight (64-element blocks that
+// never straddle a row) with activations `a` (row stride lda, K columns read).
+bool bf16_gemm_ok(const DevQW &w, const void *a, int64_t lda, int64_t K);
+// Reduction splits the bf16 kernels use for (M x N) outputs over K: > 1
+// needs splits * M * N floats of partial sums.
+int bf16_gemm_splits(int64_t M, int64_t N, int64_t K);
+hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, int a_f32, int splits,
+                            float *partial, hipStream_t s);
 
 // ---- k_quant.hip ----
 hipError_t launch_quantize(const float *w, int64_t n, int64_t bs, int dq,
@@ -114,6 +135,10 @@ hipError_t launch_dequantize(const DevQW &w, float *out, hipStream_t s);
 // True when the tile engine runs (M x N) on 128x128 tiles (else 64x64).
 bool gemm_uses_t128(int64_t M, int64_t N);
 hipError_t launch_gemm(const GemmArgs &args, float *partial, hipStream_t s);
+// C (M x N, row stride ldc) = the sum of `splits` partial (M x N) matrices
+// stored back to back in `part`, added in split order.
+hipError_t launch_reduce_splits(const float *part, int splits, int64_t M, int64_t N, float *C,
+                                int64_t ldc, hipStream_t s);
 // Tile-engine eligibility of a quantized B operand: block_size 64 and
 // whole blocks per row of the reduction form.
 bool nf4_fast_ok(const DevQW &w);
@@ -235,6 +260,32 @@ hipError_t launch_softmax_ce(const float *logits, const uint32_t *targets, int64
 // LoRA-rank GEMMs with an (M x r) output, r <= 64, K <= 2048 (k_rank.hip):
 // out[m][j] = alpha * sum_k P[m][k] Q(j, k); P row-major (ldp) in fp32 or
 // bf16; Q(j, k) = q[j * ldq + k] (q_kmajor = 0) or q[k * ldq + j] (1).
+// A list of independent rank GEMMs for one launch (blockIdx.y = job).
+// k_rank_gemm job: out (M x r, row stride ldo) = alpha * P (M x k, stride
+// ldp) . Q(j, k) with Q = A (r x k, stride ldq) or, q_kmajor, B (k x r).
+// k_rank_tgemm job: out(c, j) = alpha * sum_m P[m][c] * Q[m][j] for c < k
+// (the job's column count), P (M x k) and Q (M x r, stride ldq), stored at
+// out[c * ldo + j] or, out_t, out[j * ldo + c].
+struct RankJob {
+  const void *p;
+  int64_t ldp;
+  const float *q;
+  int64_t ldq;
+  float *out;
+  int64_t ldo;
+  int64_t k;
+  int r;
+  int out_t;
+  float alpha;
+};
+constexpr int kMaxRankJobs = 6;
+struct RankJobs {
+  RankJob j[kMaxRankJobs];
+  int count;
+};
+hipError_t launch_rank_gemms(const RankJobs &jobs, int p_bf16, int q_kmajor, int64_t M,
+                             hipStream_t s);
+hipError_t launch_rank_tgemms(const RankJobs &jobs, int big_bf16, int64_t M, hipStream_t s);
 bool rank_gemm_ok(int64_t K, int64_t r);
 hipError_t launch_rank_gemm(const void *P, int p_bf16, int64_t ldp, const float *Q, int q_kmajor,
                             int64_t ldq, float *out, int64_t ldo, int64_t M, int64_t K, int64_t r,

@@ -534,7 +534,10 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
                     nullptr, r, 1.0f);
     gt1.splits = t1_rank ? 1 : choose_splits(M, r, K);
   }
-  const int y_splits = base_splits(M, N, K);
+  // NF4 weights in whole 64-element row blocks run on bf16 MFMA (the weight
+  // as hi / lo bf16 parts); others on the fp32 tile engine
+  const bool bf16 = fast && qh::bf16_gemm_ok(W, x, K, K);
+  const int y_splits = bf16 ? qh::bf16_gemm_splits(M, N, K) : base_splits(M, N, K);
   Carve c;
   size_t i_t1 = c.add(lora && !t1_out ? (size_t)M * r * 4 : 0);
   size_t i_w32 = c.add(fast ? 0 : (size_t)W.n * 4);
@@ -560,19 +563,20 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     timed(ctx, "dequantize", s, [&] { return qh::launch_dequantize(W, w32, s); });
     B = op(w32, K, qh::ROWK, qh::E_F32);
   }
-  if (fast && qh::bf16_gemm_ok(W, M, N)) {
+  if (bf16) {
     // bf16 MFMA against the weight's hi / lo bf16 parts (X exact when bf16,
     // split into hi / lo when fp32), the LoRA term T1 . (s B)^T in the same
     // kernel
     qh::Bf16GemmArgs b{};
-    b.M = M, b.N = N, b.K = K, b.A = x, b.lda = K, b.w = W;
-    if (lora) {
-      b.A2 = t1, b.lda2 = r, b.B2 = l->b, b.ldb2 = r, b.b2scale = sc, b.b2form = qh::ROWK;
-      b.K2 = r;
-    }
-    b.C = y, b.ldc = N, b.alpha = 1.0f;
+    b.M = M, b.N = N, b.K = K, b.A = x, b.lda = K, b.alpha = 1.0f, b.nseg = 1;
+    qh::Bf16Seg &q = b.seg[0];
+    q.w = W, q.len = N, q.C = y, q.ldc = N;
+    if (lora) q.A2 = t1, q.lda2 = r, q.B2 = l->b, q.ldb2 = r, q.b2scale = sc, q.K2 = r;
     timed(ctx, "forward_gemm_bf16", s,
-          [&] { return qh::launch_gemm_bf16(b, qh::ROWK, xe == qh::E_F32, s); });
+          [&] {
+            return qh::launch_gemm_bf16(b, qh::ROWK, xe == qh::E_F32, y_splits,
+                                        (float *)p[i_p2], s);
+          });
     return;
   }
   gm = gemm_args(M, N, K, op(x, K, qh::ROWK, xe), B, y, N, 1.0f);
@@ -644,7 +648,8 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   size_t i_p2 = c.add(lora ? partial_floats(gds) * 4 : 0);
   size_t i_p3 = c.add(lora ? partial_floats(ggb) * 4 : 0);
   size_t i_p4 = c.add(lora ? partial_floats(gga) * 4 : 0);
-  const int gx_splits = base_splits(M, K, N);
+  const bool bf16 = fast && qh::bf16_gemm_ok(W, dy, N, N);
+  const int gx_splits = bf16 ? qh::bf16_gemm_splits(M, K, N) : base_splits(M, K, N);
   size_t i_p5 = c.add(gx_splits > 1 ? (size_t)gx_splits * M * K * 4 : 0);
   if (plan_bytes) {
     *plan_bytes = c.total();
@@ -694,17 +699,18 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
       timed(ctx, "grad_a_gemm", s, [&] { return qh::launch_gemm(gga, (float *)p[i_p4], s); });
     }
   }
-  if (fast && qh::bf16_gemm_ok(W, M, K)) {
+  if (bf16) {
     // grad_x = dY . W + Ds . A on bf16 MFMA (dY exact when bf16, split when fp32)
     qh::Bf16GemmArgs b{};
-    b.M = M, b.N = K, b.K = N, b.A = dy, b.lda = N, b.w = W;
-    if (lora) {
-      b.A2 = ds, b.lda2 = r, b.B2 = l->a, b.ldb2 = K, b.b2scale = 1.0f, b.b2form = qh::KROW;
-      b.K2 = r;
-    }
-    b.C = gx, b.ldc = K, b.alpha = 1.0f;
+    b.M = M, b.N = K, b.K = N, b.C = gx, b.ldc = K, b.alpha = 1.0f, b.nseg = 1;
+    qh::Bf16Seg &q = b.seg[0];
+    q.w = W, q.A = dy, q.lda = N, q.len = N;
+    if (lora) q.A2 = ds, q.lda2 = r, q.B2 = l->a, q.ldb2 = K, q.b2scale = 1.0f, q.K2 = r;
     timed(ctx, "grad_x_gemm_bf16", s,
-          [&] { return qh::launch_gemm_bf16(b, qh::KROW, ae == qh::E_F32, s); });
+          [&] {
+            return qh::launch_gemm_bf16(b, qh::KROW, ae == qh::E_F32, gx_splits,
+                                        (float *)p[i_p5], s);
+          });
     return;
   }
   Operand B;
@@ -724,6 +730,153 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   }
   gm.splits = gx_splits;
   timed(ctx, "grad_x_gemm", s, [&] { return qh::launch_gemm(gm, (float *)p[i_p5], s); });
+}
+
+// ---- projections that read the same activations -------------------------
+// q / k / v of one normed input, or gate / up: their T1s in one rank
+// launch and their base GEMMs in one segmented bf16-MFMA launch (forward);
+// Ds, then grad_A and grad_B, in one rank launch each and the input gradient
+// summed over the group in one segmented launch (backward).  Taken when
+// every member fits those kernels; otherwise the members run one by one.
+constexpr size_t kMaxShared = 3;  // members: 2 rank jobs each in one launch
+
+bool shared_ok(size_t count, const DevQW *W, const qh_lora *const *l, const void *x,
+               const void *const *dy, int64_t M) {
+  if (count < 2 || count > kMaxShared || count > (size_t)qh::kMaxBf16Segs) return false;
+  const int64_t K = W[0].cols;
+  for (size_t i = 0; i < count; ++i) {
+    if (W[i].cols != K || W[i].rows == 0 || W[i].kind != W[0].kind) return false;
+    if (!qh::nf4_fast_ok(W[i]) || !qh::bf16_gemm_ok(W[i], x, K, K)) return false;
+    if (dy && !qh::bf16_gemm_ok(W[i], dy[i], W[i].rows, W[i].rows)) return false;
+    const qh_lora *li = l[i];
+    if (li) {
+      const int64_t r = (int64_t)li->r;
+      if (!qh::rank_gemm_ok(K, r) || !qh::rank_gemm_ok(W[i].rows, r) ||
+          !qh::rank_tgemm_ok(M, r))
+        return false;
+    }
+  }
+  return M > 16 && K > 0;  // decode-sized batches take the GEMV kernels
+}
+
+void forward_shared_dev(qh_ctx *ctx, size_t count, const DevQW *W, const qh_lora *const *l,
+                        const void *x, int xdt, size_t batch, float *const *y,
+                        float *const *t1_out, hipStream_t s) {
+  const int64_t M = (int64_t)batch, K = W[0].cols;
+  if (!shared_ok(count, W, l, x, nullptr, M)) {
+    for (size_t i = 0; i < count; ++i)
+      forward_dev(ctx, W[i], l[i], x, xdt, batch, y[i], t1_out ? t1_out[i] : nullptr, s);
+    return;
+  }
+  const int xe = xdt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
+  Carve c;
+  size_t it[kMaxShared];
+  for (size_t i = 0; i < count; ++i)
+    it[i] = c.add(l[i] && !(t1_out && t1_out[i]) ? (size_t)M * l[i]->r * 4 : 0);
+  auto p = c.bind(ctx->scratch);
+  float *t1[kMaxShared];
+  qh::RankJobs jt{};
+  for (size_t i = 0; i < count; ++i) {
+    t1[i] = nullptr;
+    if (!l[i]) continue;
+    t1[i] = t1_out && t1_out[i] ? t1_out[i] : (float *)p[it[i]];
+    jt.j[jt.count++] = qh::RankJob{x, K, l[i]->a, K, t1[i], (int64_t)l[i]->r, K,
+                                   (int)l[i]->r, 0, 1.0f};
+  }
+  if (jt.count)
+    timed(ctx, "t1_gemm", s,
+          [&] { return qh::launch_rank_gemms(jt, xe == qh::E_BF16, 0, M, s); });
+  qh::Bf16GemmArgs b{};
+  b.M = M, b.K = K, b.A = x, b.lda = K, b.alpha = 1.0f, b.nseg = (int)count;
+  for (size_t i = 0; i < count; ++i) {
+    qh::Bf16Seg &q = b.seg[i];
+    const int64_t N = W[i].rows;
+    q.w = W[i], q.len = N, q.C = y[i], q.ldc = N;
+    if (l[i]) {
+      const int64_t r = (int64_t)l[i]->r;
+      q.A2 = t1[i], q.lda2 = r, q.B2 = l[i]->b, q.ldb2 = r, q.K2 = r;
+      q.b2scale = l[i]->alpha / (float)l[i]->r;  // lora.rs:64-66
+    }
+    b.N += N;
+  }
+  timed(ctx, "forward_gemm_bf16", s,
+        [&] { return qh::launch_gemm_bf16(b, qh::ROWK, xe == qh::E_F32, 1, nullptr, s); });
+}
+
+// gx = sum over the members of their input gradients (summed in the GEMM's
+// accumulators: the same value as adding the members' gradients, rounded
+// differently).
+void backward_shared_dev(qh_ctx *ctx, size_t count, const DevQW *W, const qh_lora *const *l,
+                         const void *x, const void *const *dy, int adt, size_t batch,
+                         const float *const *t1_in, float *gx, float *const *ga,
+                         float *const *gb, hipStream_t s) {
+  const int64_t M = (int64_t)batch, K = W[0].cols;
+  if (!shared_ok(count, W, l, x, dy, M)) {
+    float *tmp = count > 1 ? (float *)ctx->block_tmp[1].ensure((size_t)M * K * 4) : nullptr;
+    for (size_t i = 0; i < count; ++i) {
+      backward_dev(ctx, W[i], l[i], x, dy[i], adt, batch, t1_in ? t1_in[i] : nullptr,
+                   i == 0 ? gx : tmp, ga[i], gb[i], s);
+      if (i > 0)
+        timed(ctx, "residual_add", s,
+              [&] { return qh::launch_axpy_inplace(gx, tmp, (int64_t)(M * K), s); });
+    }
+    return;
+  }
+  const int ae = adt == QH_BF16 ? qh::E_BF16 : qh::E_F32;
+  const int ab = ae == qh::E_BF16;
+  int64_t nsum = 0;
+  for (size_t i = 0; i < count; ++i) nsum += W[i].rows;
+  const int splits = qh::bf16_gemm_splits(M, K, nsum);
+  Carve c;
+  size_t it[kMaxShared], id[kMaxShared];
+  for (size_t i = 0; i < count; ++i) {
+    const size_t mr = l[i] ? (size_t)M * l[i]->r * 4 : 0;
+    it[i] = c.add(l[i] && !(t1_in && t1_in[i]) ? mr : 0);
+    id[i] = c.add(mr);
+  }
+  const size_t ip = c.add(splits > 1 ? (size_t)splits * M * K * 4 : 0);
+  auto p = c.bind(ctx->scratch);
+  const float *t1[kMaxShared];
+  float *ds[kMaxShared];
+  qh::RankJobs jt{}, jd{}, jg{};
+  for (size_t i = 0; i < count; ++i) {
+    t1[i] = nullptr, ds[i] = nullptr;
+    if (!l[i]) continue;
+    const int64_t N = W[i].rows, r = (int64_t)l[i]->r;
+    const float sc = l[i]->alpha / (float)l[i]->r;
+    if (t1_in && t1_in[i]) {
+      t1[i] = t1_in[i];
+    } else {
+      t1[i] = (float *)p[it[i]];
+      jt.j[jt.count++] = qh::RankJob{x, K, l[i]->a, K, (float *)p[it[i]], r, K, (int)r, 0, 1.0f};
+    }
+    ds[i] = (float *)p[id[i]];
+    // Ds = s dY . B (qlora.rs:143, 149)
+    jd.j[jd.count++] = qh::RankJob{dy[i], N, l[i]->b, r, ds[i], r, N, (int)r, 0, sc};
+    // grad_B = s dY^T . T1 (N x r), grad_A = Ds^T . X (r x K) (qlora.rs:147, 151)
+    jg.j[jg.count++] = qh::RankJob{dy[i], N, t1[i], r, gb[i], r, N, (int)r, 0, sc};
+    jg.j[jg.count++] = qh::RankJob{x, K, ds[i], r, ga[i], K, K, (int)r, 1, 1.0f};
+  }
+  if (jt.count)
+    timed(ctx, "t1_gemm", s, [&] { return qh::launch_rank_gemms(jt, ab, 0, M, s); });
+  if (jd.count) {
+    timed(ctx, "ds_gemm", s, [&] { return qh::launch_rank_gemms(jd, ab, 1, M, s); });
+    timed(ctx, "grad_ab_gemm", s, [&] { return qh::launch_rank_tgemms(jg, ab, M, s); });
+  }
+  qh::Bf16GemmArgs b{};
+  b.M = M, b.N = K, b.K = nsum, b.C = gx, b.ldc = K, b.alpha = 1.0f, b.nseg = (int)count;
+  for (size_t i = 0; i < count; ++i) {
+    qh::Bf16Seg &q = b.seg[i];
+    const int64_t N = W[i].rows;
+    q.w = W[i], q.A = dy[i], q.lda = N, q.len = N;
+    if (l[i]) {
+      const int64_t r = (int64_t)l[i]->r;
+      q.A2 = ds[i], q.lda2 = r, q.B2 = l[i]->a, q.ldb2 = K, q.b2scale = 1.0f, q.K2 = r;
+    }
+  }
+  timed(ctx, "grad_x_gemm_bf16", s, [&] {
+    return qh::launch_gemm_bf16(b, qh::KROW, ae == qh::E_F32, splits, (float *)p[ip], s);
+  });
 }
 
 // Plain GEMMs (gpu_matmul*): C = A.B, A^T.B, A.B^T.
@@ -1167,6 +1320,13 @@ qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w, const qh_lora *
   });
 }
 
+// Layer-indexed errors: "<kind>: layer i: <text>".
+static qh_status layer_error(qh_status st, size_t i) {
+  const size_t pos = g_err.find(": ");
+  if (pos != std::string::npos) g_err.insert(pos + 2, fmt("layer %zu: ", i));
+  return st;
+}
+
 qh_status qh_qlora_forward_group_dev(qh_ctx *ctx, size_t count, const qh_qweight *ws,
                                      const qh_lora *const *loras, const void *const *d_xs,
                                      int x_dtype, size_t batch, float *const *d_ys,
@@ -1184,12 +1344,7 @@ qh_status qh_qlora_forward_group_dev(qh_ctx *ctx, size_t count, const qh_qweight
     if (st == QH_OK) st = need_buf(d_xs[i], batch * w->cols, "x");
     if (st == QH_OK) st = need_buf(d_ys[i], batch * w->rows, "y");
     if (st == QH_OK) st = need_buf(w->codes, w->rows * w->cols, "the weight's codes");
-    if (st != QH_OK) {
-      // name the layer after the message's kind: "<kind>: layer i: <text>"
-      const size_t pos = g_err.find(": ");
-      if (pos != std::string::npos) g_err.insert(pos + 2, fmt("layer %zu: ", i));
-      return st;
-    }
+    if (st != QH_OK) return layer_error(st, i);
   }
   return guarded(ctx, [&] {
     hipStream_t s = pick_stream(ctx, stream);
@@ -1219,6 +1374,85 @@ qh_status qh_qlora_forward_group_dev(qh_ctx *ctx, size_t count, const qh_qweight
       }
       forward_dev(ctx, W1, l1, d_xs[i], x_dtype, batch, d_ys[i], t1o1, s);
     }
+    return QH_OK;
+  });
+}
+
+constexpr size_t kMaxSharedApi = 8;
+
+qh_status qh_qlora_forward_shared_dev(qh_ctx *ctx, size_t count, const qh_qweight *ws,
+                                      const qh_lora *const *loras, const void *d_x,
+                                      int x_dtype, size_t batch, float *const *d_ys,
+                                      float *const *d_t1s, void *stream) {
+  if (count == 0) return QH_OK;
+  if (count > kMaxSharedApi) return fail(QH_ERR_INVALID_CONFIG, "more than 8 layers");
+  if (!ws || !d_ys) return fail(QH_ERR_SHAPE_MISMATCH, "ws and d_ys must be given");
+  if (x_dtype != QH_F32 && x_dtype != QH_BF16)
+    return fail(QH_ERR_INVALID_CONFIG, "x_dtype must be QH_F32 or QH_BF16");
+  for (size_t i = 0; i < count; ++i) {
+    const qh_qweight *w = &ws[i];
+    qh_status st = validate_weight(w);
+    if (st == QH_OK && w->cols != ws[0].cols)
+      st = fail(QH_ERR_SHAPE_MISMATCH, fmt("in_dim %zu differs from layer 0's %zu", w->cols,
+                                           ws[0].cols));
+    if (st == QH_OK) st = validate_lora(loras ? loras[i] : nullptr, w->cols, w->rows);
+    if (st == QH_OK) st = need_buf(d_x, batch * w->cols, "x");
+    if (st == QH_OK) st = need_buf(d_ys[i], batch * w->rows, "y");
+    if (st == QH_OK) st = need_buf(w->codes, w->rows * w->cols, "the weight's codes");
+    if (st != QH_OK) return layer_error(st, i);
+  }
+  return guarded(ctx, [&] {
+    DevQW W[kMaxSharedApi];
+    const qh_lora *L[kMaxSharedApi];
+    for (size_t i = 0; i < count; ++i) {
+      W[i] = make_devqw(ws[i]);
+      L[i] = loras ? loras[i] : nullptr;
+    }
+    forward_shared_dev(ctx, count, W, L, d_x, x_dtype, batch, d_ys, d_t1s,
+                       pick_stream(ctx, stream));
+    return QH_OK;
+  });
+}
+
+static qh_status validate_backward_dev(const qh_qweight *w, const qh_lora *lora,
+                                       const void *d_x, const void *d_dy, int act_dtype,
+                                       size_t batch, float *d_grad_x, float *d_grad_a,
+                                       float *d_grad_b);
+
+qh_status qh_qlora_backward_shared_dev(qh_ctx *ctx, size_t count, const qh_qweight *ws,
+                                       const qh_lora *const *loras, const void *d_x,
+                                       const void *const *d_dys, int act_dtype, size_t batch,
+                                       const float *const *d_t1s, float *d_grad_x,
+                                       float *const *d_grad_as, float *const *d_grad_bs,
+                                       void *stream) {
+  if (count == 0) return QH_OK;
+  if (count > kMaxSharedApi) return fail(QH_ERR_INVALID_CONFIG, "more than 8 layers");
+  if (!ws || !d_dys) return fail(QH_ERR_SHAPE_MISMATCH, "ws and d_dys must be given");
+  for (size_t i = 0; i < count; ++i) {
+    const qh_lora *l = loras ? loras[i] : nullptr;
+    qh_status st = QH_OK;
+    if (ws[i].cols != ws[0].cols)
+      st = fail(QH_ERR_SHAPE_MISMATCH, fmt("in_dim %zu differs from layer 0's %zu", ws[i].cols,
+                                           ws[0].cols));
+    if (st == QH_OK && l && (!d_grad_as || !d_grad_bs))
+      st = fail(QH_ERR_SHAPE_MISMATCH, "an adapter's gradient buffer is NULL");
+    if (st == QH_OK)
+      st = validate_backward_dev(&ws[i], l, d_x, d_dys[i], act_dtype, batch, d_grad_x,
+                                 l ? d_grad_as[i] : nullptr, l ? d_grad_bs[i] : nullptr);
+    if (st != QH_OK) return layer_error(st, i);
+  }
+  return guarded(ctx, [&] {
+    DevQW W[kMaxSharedApi];
+    const qh_lora *L[kMaxSharedApi];
+    float *GA[kMaxSharedApi], *GB[kMaxSharedApi];
+    for (size_t i = 0; i < count; ++i) {
+      W[i] = make_devqw(ws[i]);
+      L[i] = loras ? loras[i] : nullptr;
+      GA[i] = L[i] ? d_grad_as[i] : nullptr;
+      GB[i] = L[i] ? d_grad_bs[i] : nullptr;
+    }
+    backward_shared_dev(ctx, count, W, L, d_x, d_dys, act_dtype, batch, d_t1s, d_grad_x, GA,
+                        GB, pick_stream(ctx, stream));
     return QH_OK;
   });
 }
@@ -1763,10 +1997,13 @@ qh_status qh_mlp_forward_dev(qh_ctx *ctx, const qh_mlp_block *b, float *d_x, siz
     timed(ctx, "rmsnorm", s, [&] {
       return qh::launch_rmsnorm(d_x, b->norm_w, c->xn, (int64_t)seq, (int)h, b->eps, s);
     });
-    forward_dev(ctx, make_devqw(b->gate), b->gate_lora, c->xn, QH_F32, seq, c->gate,
-                b->gate_lora ? c->t1_gate : nullptr, s);
-    forward_dev(ctx, make_devqw(b->up), b->up_lora, c->xn, QH_F32, seq, c->up,
-                b->up_lora ? c->t1_up : nullptr, s);
+    {
+      const DevQW W[2] = {make_devqw(b->gate), make_devqw(b->up)};
+      const qh_lora *L[2] = {b->gate_lora, b->up_lora};
+      float *Y[2] = {c->gate, c->up};
+      float *T[2] = {b->gate_lora ? c->t1_gate : nullptr, b->up_lora ? c->t1_up : nullptr};
+      forward_shared_dev(ctx, 2, W, L, c->xn, QH_F32, seq, Y, T, s);
+    }
     timed(ctx, "swiglu", s, [&] {
       return qh::launch_swiglu(c->gate, c->up, c->act, (int64_t)(seq * f), s);
     });
@@ -1805,16 +2042,16 @@ qh_status qh_mlp_backward_dev(qh_ctx *ctx, const qh_mlp_block *b, const qh_mlp_c
     timed(ctx, "swiglu_backward", s, [&] {
       return qh::launch_swiglu_bwd(c->gate, c->up, d_act, c->gate, c->up, (int64_t)(seq * f), s);
     });
-    float *dxn_u = (float *)ctx->block_tmp[1].ensure(seq * h * 4);
-    backward_dev(ctx, make_devqw(b->gate), b->gate_lora, c->xn, c->gate, QH_F32, seq,
-                 b->gate_lora ? c->t1_gate : nullptr, d_dx_in,
-                 b->gate_lora ? d_grad_a[0] : nullptr, b->gate_lora ? d_grad_b[0] : nullptr, s);
-    backward_dev(ctx, make_devqw(b->up), b->up_lora, c->xn, c->up, QH_F32, seq,
-                 b->up_lora ? c->t1_up : nullptr, dxn_u,
-                 b->up_lora ? d_grad_a[1] : nullptr, b->up_lora ? d_grad_b[1] : nullptr, s);
-    timed(ctx, "residual_add", s, [&] {
-      return qh::launch_axpy_inplace(d_dx_in, dxn_u, (int64_t)(seq * h), s);
-    });
+    {
+      // dxn = dxn_gate + dxn_up (llama.rs:563-567)
+      const DevQW W[2] = {make_devqw(b->gate), make_devqw(b->up)};
+      const qh_lora *L[2] = {b->gate_lora, b->up_lora};
+      const void *DY[2] = {c->gate, c->up};
+      const float *T[2] = {b->gate_lora ? c->t1_gate : nullptr, b->up_lora ? c->t1_up : nullptr};
+      float *GA[2] = {b->gate_lora ? d_grad_a[0] : nullptr, b->up_lora ? d_grad_a[1] : nullptr};
+      float *GB[2] = {b->gate_lora ? d_grad_b[0] : nullptr, b->up_lora ? d_grad_b[1] : nullptr};
+      backward_shared_dev(ctx, 2, W, L, c->xn, DY, QH_F32, seq, T, d_dx_in, GA, GB, s);
+    }
     // dx_mid = rmsnorm_backward(x_mid, w, dxn).dx + dx_out (dw is discarded,
     // llama.rs:568)
     timed(ctx, "rmsnorm_backward", s, [&] {
@@ -1874,12 +2111,12 @@ qh_status qh_attn_qkv_forward_dev(qh_ctx *ctx, const qh_attn_block *b, const flo
     timed(ctx, "rmsnorm", s, [&] {
       return qh::launch_rmsnorm(d_x, b->norm_w, c->xn, (int64_t)seq, (int)h, b->eps, s);
     });
-    forward_dev(ctx, make_devqw(b->q), b->q_lora, c->xn, QH_F32, seq, d_q,
-                b->q_lora ? c->t1_q : nullptr, s);
-    forward_dev(ctx, make_devqw(b->k), b->k_lora, c->xn, QH_F32, seq, d_k,
-                b->k_lora ? c->t1_k : nullptr, s);
-    forward_dev(ctx, make_devqw(b->v), b->v_lora, c->xn, QH_F32, seq, d_v,
-                b->v_lora ? c->t1_v : nullptr, s);
+    const DevQW W[3] = {make_devqw(b->q), make_devqw(b->k), make_devqw(b->v)};
+    const qh_lora *L[3] = {b->q_lora, b->k_lora, b->v_lora};
+    float *Y[3] = {d_q, d_k, d_v};
+    float *T[3] = {b->q_lora ? c->t1_q : nullptr, b->k_lora ? c->t1_k : nullptr,
+                   b->v_lora ? c->t1_v : nullptr};
+    forward_shared_dev(ctx, 3, W, L, c->xn, QH_F32, seq, Y, T, s);
     return QH_OK;
   });
 }
@@ -1948,22 +2185,17 @@ qh_status qh_attn_qkv_backward_dev(qh_ctx *ctx, const qh_attn_block *b, const qh
     const size_t h = b->hidden;
     // llama.rs:580-601: dxn = (dxn_q + dxn_k) + dxn_v, then the norm's dx and
     // the residual's straight path
-    float *tmp = (float *)ctx->block_tmp[1].ensure(seq * h * 4);
-    backward_dev(ctx, make_devqw(b->q), b->q_lora, c->xn, d_dq, QH_F32, seq,
-                 b->q_lora ? c->t1_q : nullptr, d_dx_in, b->q_lora ? d_grad_a[0] : nullptr,
-                 b->q_lora ? d_grad_b[0] : nullptr, s);
-    backward_dev(ctx, make_devqw(b->k), b->k_lora, c->xn, d_dk, QH_F32, seq,
-                 b->k_lora ? c->t1_k : nullptr, tmp, b->k_lora ? d_grad_a[1] : nullptr,
-                 b->k_lora ? d_grad_b[1] : nullptr, s);
-    timed(ctx, "residual_add", s, [&] {
-      return qh::launch_axpy_inplace(d_dx_in, tmp, (int64_t)(seq * h), s);
-    });
-    backward_dev(ctx, make_devqw(b->v), b->v_lora, c->xn, d_dv, QH_F32, seq,
-                 b->v_lora ? c->t1_v : nullptr, tmp, b->v_lora ? d_grad_a[2] : nullptr,
-                 b->v_lora ? d_grad_b[2] : nullptr, s);
-    timed(ctx, "residual_add", s, [&] {
-      return qh::launch_axpy_inplace(d_dx_in, tmp, (int64_t)(seq * h), s);
-    });
+    const DevQW W[3] = {make_devqw(b->q), make_devqw(b->k), make_devqw(b->v)};
+    const qh_lora *L[3] = {b->q_lora, b->k_lora, b->v_lora};
+    const void *DY[3] = {d_dq, d_dk, d_dv};
+    const float *T[3] = {b->q_lora ? c->t1_q : nullptr, b->k_lora ? c->t1_k : nullptr,
+                         b->v_lora ? c->t1_v : nullptr};
+    float *GA[3], *GB[3];
+    for (int i = 0; i < 3; ++i) {
+      GA[i] = L[i] ? d_grad_a[i] : nullptr;
+      GB[i] = L[i] ? d_grad_b[i] : nullptr;
+    }
+    backward_shared_dev(ctx, 3, W, L, c->xn, DY, QH_F32, seq, T, d_dx_in, GA, GB, s);
     timed(ctx, "rmsnorm_backward", s, [&] {
       return qh::launch_rmsnorm_bwd(c->x_in, b->norm_w, d_dx_in, d_dx_in, nullptr, nullptr,
                                     (int64_t)seq, (int)h, b->eps, s);

@@ -40,7 +40,7 @@ EXPORTED = [
     "qh_adam8bit_step_dev", "qh_adam8bit_state_bytes", "qh_adam8bit_get_state",
     "qh_quantize_nf4_dev", "qh_dequantize_dev", "qh_matmul_dev",
     "qh_qlora_forward_dev", "qh_qlora_backward_dev", "qh_qlora_backward_dev_noalloc",
-    "qh_qlora_forward_group_dev",
+    "qh_qlora_forward_group_dev", "qh_qlora_forward_shared_dev", "qh_qlora_backward_shared_dev",
     "qh_rmsnorm", "qh_rmsnorm_dev", "qh_rmsnorm_backward", "qh_rmsnorm_backward_dev",
     "qh_swiglu", "qh_swiglu_dev", "qh_swiglu_backward", "qh_swiglu_backward_dev",
     "qh_softmax_cross_entropy", "qh_softmax_cross_entropy_dev",
@@ -179,6 +179,13 @@ def load() -> C.CDLL:
         L.qh_qlora_forward_group_dev.argtypes = [vp, sz, C.POINTER(QWeight),
                                                  C.POINTER(C.POINTER(Lora)), C.POINTER(vp),
                                                  i32, sz, C.POINTER(vp), C.POINTER(vp), vp]
+        L.qh_qlora_forward_shared_dev.argtypes = [vp, sz, C.POINTER(QWeight),
+                                                  C.POINTER(C.POINTER(Lora)), vp, i32, sz,
+                                                  C.POINTER(vp), C.POINTER(vp), vp]
+        L.qh_qlora_backward_shared_dev.argtypes = [vp, sz, C.POINTER(QWeight),
+                                                   C.POINTER(C.POINTER(Lora)), vp,
+                                                   C.POINTER(vp), i32, sz, C.POINTER(vp), vp,
+                                                   C.POINTER(vp), C.POINTER(vp), vp]
         f32 = C.c_float
         L.qh_rmsnorm.argtypes = [vp, vp, sz, vp, sz, f32, vp]
         L.qh_rmsnorm_dev.argtypes = [vp, vp, vp, sz, sz, f32, vp, vp]

@@ -189,6 +189,52 @@ def backward(w: DeviceWeight, lora, x: torch.Tensor, dy: torch.Tensor, batch: in
         _dt(x), batch, _p(t1), _p(gx), _p(ga), _p(gb), C.c_void_p(_stream())))
 
 
+def _layer_arrays(layers):
+    n = len(layers)
+    ws = (QWeight * n)(*[w if isinstance(w, QWeight) else w.struct() for w, _ in layers])
+    loras = (C.POINTER(Lora) * n)(*[C.pointer(l) if l is not None else C.POINTER(Lora)()
+                                    for _, l in layers])
+    return n, ws, loras
+
+
+def _ptrs(ts):
+    return (C.c_void_p * len(ts))(*[t.data_ptr() if t is not None else None for t in ts])
+
+
+def forward_shared(layers, x: torch.Tensor, batch: int, ys, t1s=None, ctx=None) -> None:
+    """The forward of layers that read the same activations x
+    (qh_qlora_forward_shared_dev): ``layers`` holds (weight, lora) per
+    layer (weight a DeviceWeight or QWeight view, lora a ``Lora`` or None);
+    ``ys[i]`` / ``t1s[i]`` receive layer i's Y and T1."""
+    ctx = ctx or default_context()
+    n, ws, loras = _layer_arrays(layers)
+    if n == 0:
+        return
+    t1p = _ptrs(t1s if t1s is not None else [None] * n)
+    check(ctx.lib.qh_qlora_forward_shared_dev(ctx.h, n, ws, loras, _p(x), _dt(x), batch,
+                                              _ptrs(ys), t1p, C.c_void_p(_stream())))
+
+
+def backward_shared(layers, x: torch.Tensor, dys, batch: int, gx: torch.Tensor,
+                    gas=None, gbs=None, t1s=None, ctx=None) -> None:
+    """The backward of layers that read the same activations x
+    (qh_qlora_backward_shared_dev): gx receives the sum of the layers' input
+    gradients, gas[i] / gbs[i] layer i's grad_A / grad_B (None without an
+    adapter), t1s[i] the forward's T1 (or None)."""
+    ctx = ctx or default_context()
+    n, ws, loras = _layer_arrays(layers)
+    if n == 0:
+        return
+    if any(d.dtype != x.dtype for d in dys):
+        raise TypeError("x and every dy must share a dtype")
+    none = [None] * n
+    check(ctx.lib.qh_qlora_backward_shared_dev(
+        ctx.h, n, ws, loras, _p(x), _ptrs(dys), _dt(x), batch,
+        _ptrs(t1s if t1s is not None else none), _p(gx),
+        _ptrs(gas if gas is not None else none), _ptrs(gbs if gbs is not None else none),
+        C.c_void_p(_stream())))
+
+
 # ---- the glue of a decoder block (qlora-model/src/llama.rs) ------------------
 def _f32c(t: torch.Tensor, what: str) -> torch.Tensor:
     if t.dtype != torch.float32 or not t.is_contiguous():
