@@ -51,9 +51,9 @@ constexpr int kBK = 32;          // reduction per step = one LDS row
 // Block shape: T threads (T / 64 waves in a 2 x T/128 grid), BM x BN outputs;
 // a step reduces KS x 32 (KS LDS sub-tiles between two barriers) and its
 // global loads are issued PF steps before its MFMAs.
-template <int T_, int BM_, int BN_, int PF_ = 1, int KS_ = 1>
+template <int T_, int BM_, int BN_, int PF_ = 1, int KS_ = 1, int IL_ = 0>
 struct Cfg {
-  static constexpr int T = T_, BM = BM_, BN = BN_, PF = PF_, KS = KS_;
+  static constexpr int T = T_, BM = BM_, BN = BN_, PF = PF_, KS = KS_, IL = IL_;
   static_assert(PF == 1 || PF == 2, "prefetch depth");
   static_assert(KS == 1 || KS == 2, "sub-tiles per step");
   static constexpr int WGN = T / 128;              // wave grid: 2 x WGN
@@ -63,8 +63,13 @@ struct Cfg {
   static_assert(BN <= T && BM % (T / 4) == 0, "staging maps");
 };
 using CfgL256 = Cfg<512, 256, 256>;
+// The forward's 256 x 256 tiles interleave each step's MFMAs with the next
+// step's loads, decode and LDS writes (6 VALU instructions per MFMA): 7-8 %
+// faster at C3.  The input gradient and 256 x 128 tiles measured slower so.
+using CfgL256F = Cfg<512, 256, 256, 1, 1, 6>;
 using CfgL128 = Cfg<512, 256, 128>;
 using CfgM = Cfg<512, 128, 128, 2, 2>;
+using CfgM1 = Cfg<512, 128, 128, 2, 1>;  // half the LDS: two blocks per CU
 using CfgS = Cfg<256, 64, 64, 2, 2>;
 
 __constant__ float c_lut_bf[17] = QH_NF4_LUT17_INIT;  // the codebook (quant.rs:27-44)
@@ -469,9 +474,28 @@ __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_
       __syncthreads();
       for (int64_t t = t0; t < t1; ++t) {
         const bool more = t + 1 < t1;
-        if (more) load(ra, t + 1);
-        mma_stage(smem + ((t - t0) & 1) * STAGE);
-        if (more) stage(smem + ((t + 1 - t0) & 1) * STAGE, ra);
+        if constexpr (C::IL) {
+          // One straight-line step (the last one loads and stages its own
+          // step again, into the stage nobody reads), so that the scheduler
+          // can interleave the next step's loads, decode and LDS writes with
+          // this step's MFMAs: one MFMA, then a share of the other work.
+          load(ra, more ? t + 1 : t);
+          mma_stage(smem + ((t - t0) & 1) * STAGE);
+          stage(smem + ((t + 1 - t0) & 1) * STAGE, ra);
+          constexpr int NMF = KS * 2 * TM * TN * (XF == 1 ? 3 : 2);
+#pragma unroll
+          for (int q = 0; q < NMF; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, C::IL, 0);  // VALU
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+          }
+        } else {
+          if (more) load(ra, t + 1);
+          mma_stage(smem + ((t - t0) & 1) * STAGE);
+          if (more) stage(smem + ((t + 1 - t0) & 1) * STAGE, ra);
+        }
         __syncthreads();
       }
     }
@@ -580,9 +604,10 @@ hipError_t run_bf16(const Bf16GemmArgs &g0, int splits, float *partial, hipStrea
 // Block shape and reduction splits by problem size.
 //  large:  256 x 256 or 256 x 128 tiles, 8 waves, for problems with at least
 //          256 tiles of 256 x 256 (MFMA-bound: C3, C5);
-//  medium: 128 x 128 tiles, 8 waves, two 32-wide sub-steps per barrier and
-//          loads two steps ahead, for 160 or more tiles of 128 x 128, or
-//          long reductions (24+ steps) over 32+ such tiles;
+//  medium: 128 x 128 tiles, 8 waves, loads two steps ahead, two 32-wide
+//          sub-steps per barrier (one when there are more tiles than CUs,
+//          so that two blocks share a CU), for 160 or more tiles of
+//          128 x 128, or long reductions (24+ steps) over 32+ such tiles;
 //  small:  64 x 64 tiles, 4 waves, the same pipelining.
 // The medium and small blocks' step loops are latency-bound (about 0.7 us
 // per step at C4's shapes), so long reductions are split until the GPU
@@ -616,11 +641,17 @@ template <int WF, int XF, int KIND>
 hipError_t pick(const Bf16GemmArgs &g, int splits, float *partial, hipStream_t s) {
   const Plan pl = plan_for(g.M, g.N, g.K);
   if (pl.tier == kSmall) return run_bf16<CfgS, WF, XF, KIND>(g, splits, partial, s);
-  if (pl.tier == kMedium) return run_bf16<CfgM, WF, XF, KIND>(g, splits, partial, s);
+  if (pl.tier == kMedium) {
+    // more tiles than CUs: one sub-tile per barrier, so two blocks fit a CU
+    if (((g.M + 127) / 128) * ((g.N + 127) / 128) > 256)
+      return run_bf16<CfgM1, WF, XF, KIND>(g, splits, partial, s);
+    return run_bf16<CfgM, WF, XF, KIND>(g, splits, partial, s);
+  }
   const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
   const int64_t waves = (t256 + 255) / 256;
   const bool wide = t256 >= 192 && (double)t256 / (double)(waves * 256) >= 0.75;
-  return wide ? run_bf16<CfgL256, WF, XF, KIND>(g, 1, nullptr, s)
+  using L256 = typename std::conditional<WF == ROWK, CfgL256F, CfgL256>::type;
+  return wide ? run_bf16<L256, WF, XF, KIND>(g, 1, nullptr, s)
               : run_bf16<CfgL128, WF, XF, KIND>(g, 1, nullptr, s);
 }
 
