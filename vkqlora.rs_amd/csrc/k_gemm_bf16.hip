@@ -51,9 +51,9 @@ constexpr int kBK = 32;          // reduction per step = one LDS row
 // Block shape: T threads (T / 64 waves in a 2 x T/128 grid), BM x BN outputs;
 // a step reduces KS x 32 (KS LDS sub-tiles between two barriers) and its
 // global loads are issued PF steps before its MFMAs.
-template <int T_, int BM_, int BN_, int PF_ = 1, int KS_ = 1, int IL_ = 0>
+template <int T_, int BM_, int BN_, int PF_ = 1, int KS_ = 1>
 struct Cfg {
-  static constexpr int T = T_, BM = BM_, BN = BN_, PF = PF_, KS = KS_, IL = IL_;
+  static constexpr int T = T_, BM = BM_, BN = BN_, PF = PF_, KS = KS_;
   static_assert(PF == 1 || PF == 2, "prefetch depth");
   static_assert(KS == 1 || KS == 2, "sub-tiles per step");
   static constexpr int WGN = T / 128;              // wave grid: 2 x WGN
@@ -63,10 +63,6 @@ struct Cfg {
   static_assert(BN <= T && BM % (T / 4) == 0, "staging maps");
 };
 using CfgL256 = Cfg<512, 256, 256>;
-// The forward's 256 x 256 tiles interleave each step's MFMAs with the next
-// step's loads, decode and LDS writes (6 VALU instructions per MFMA): 7-8 %
-// faster at C3.  The input gradient and 256 x 128 tiles measured slower so.
-using CfgL256F = Cfg<512, 256, 256, 1, 1, 6>;
 using CfgL128 = Cfg<512, 256, 128>;
 using CfgM = Cfg<512, 128, 128, 2, 2>;
 using CfgM1 = Cfg<512, 128, 128, 2, 1>;  // half the LDS: two blocks per CU
@@ -474,28 +470,9 @@ __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_
       __syncthreads();
       for (int64_t t = t0; t < t1; ++t) {
         const bool more = t + 1 < t1;
-        if constexpr (C::IL) {
-          // One straight-line step (the last one loads and stages its own
-          // step again, into the stage nobody reads), so that the scheduler
-          // can interleave the next step's loads, decode and LDS writes with
-          // this step's MFMAs: one MFMA, then a share of the other work.
-          load(ra, more ? t + 1 : t);
-          mma_stage(smem + ((t - t0) & 1) * STAGE);
-          stage(smem + ((t + 1 - t0) & 1) * STAGE, ra);
-          constexpr int NMF = KS * 2 * TM * TN * (XF == 1 ? 3 : 2);
-#pragma unroll
-          for (int q = 0; q < NMF; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            __builtin_amdgcn_sched_group_barrier(0x002, C::IL, 0);  // VALU
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
-          }
-        } else {
-          if (more) load(ra, t + 1);
-          mma_stage(smem + ((t - t0) & 1) * STAGE);
-          if (more) stage(smem + ((t + 1 - t0) & 1) * STAGE, ra);
-        }
+        if (more) load(ra, t + 1);
+        mma_stage(smem + ((t - t0) & 1) * STAGE);
+        if (more) stage(smem + ((t + 1 - t0) & 1) * STAGE, ra);
         __syncthreads();
       }
     }
@@ -650,8 +627,7 @@ hipError_t pick(const Bf16GemmArgs &g, int splits, float *partial, hipStream_t s
   const int64_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
   const int64_t waves = (t256 + 255) / 256;
   const bool wide = t256 >= 192 && (double)t256 / (double)(waves * 256) >= 0.75;
-  using L256 = typename std::conditional<WF == ROWK, CfgL256F, CfgL256>::type;
-  return wide ? run_bf16<L256, WF, XF, KIND>(g, 1, nullptr, s)
+  return wide ? run_bf16<CfgL256, WF, XF, KIND>(g, 1, nullptr, s)
               : run_bf16<CfgL128, WF, XF, KIND>(g, 1, nullptr, s);
 }
 
