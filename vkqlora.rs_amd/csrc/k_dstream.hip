@@ -6,7 +6,9 @@
 //           + (alpha/r) sum_j T1[m][j] B[n][j],      T1 = X A^T.
 //
 // Grid: at most one workgroup per CU (each needs more than half of a CU's
-// LDS), 8 waves per workgroup.
+// LDS), 8 waves per workgroup.  Two independent layers go in one launch as
+// 4-wave workgroups of at most half a CU's LDS, one of each layer per CU
+// (k_dstream2, below).
 //  * Workgroup c owns R consecutive 16-row tiles and the whole of K.  Line
 //    wave w owns the K-lines [KL w / 8, KL (w+1) / 8) (a K-line = 256
 //    elements = 128 code bytes per row) of all R tiles, so each X fragment
@@ -55,6 +57,7 @@ constexpr int kThreads = kLW * 64;
 constexpr int kCopies = 32;               // codebook table copies
 constexpr uint32_t kTabBytes = 256u * kCopies * 8u;  // 64 KiB at LDS offset 0
 constexpr int kMaxLines = 8;   // code lines a wave holds in registers
+constexpr int kMaxLinesHalf = 12;  // the same for the 4-wave workgroups of a layer pair
 constexpr int kT1Loads = 4;   // tagged T1 partials read per thread (P * M * r <= 2048)
 constexpr int kLinesAhead = 3; // K-lines of loads a wave keeps in flight
 constexpr int kMaxSlices = 128;  // T1 slices (producing workgroups)
@@ -308,17 +311,16 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
 // every launch.
 // t1w: kMaxSlices * 64 words, zero before the first launch (tag 0 is never
 // current).
-// Dynamic LDS (byte offsets): [0, 64K) table | X fragments (KL M KiB, by
-// K-line) | lbs (16 R r16 floats) | red (kLW R 16 M floats) | t1s (64
-// floats, M r16 used) | flag, epoch | recomputed T1 slices (P MRp floats) |
-// per-wave T1 partial sums (kLW MRp floats).
+// Dynamic LDS (byte offsets): [0, 64K) table | X fragments (one K-line per
+// wave; after B2 the recomputed T1 slices, P MRp floats) | lbs (16 R r16
+// floats) | red (kLW R 16 M floats) | t1s (64 floats, M r16 used) | flag,
+// epoch | per-wave T1 partial sums (kLW MRp floats).
 // The weight's pointers, X and the shape lead the arguments: the first 16
 // argument dwords arrive preloaded in SGPRs (no kernel-argument load before
 // the first code line goes out).
-// One layer's share of workgroup c (of the layer's G workgroups).  The
-// codebook table is written when `build_table` is set; a workgroup that ran
-// another layer before keeps it (no layer writes LDS below kTabBytes).
-template <int XBF16, int KIND, int M, int R, int KLW>
+// One layer's share of workgroup c (of the layer's G workgroups), in a
+// workgroup of LW waves.
+template <int XBF16, int KIND, int M, int R, int KLW, int LW = kLW>
 __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
                                              const void *__restrict__ scales,
                                              const float *__restrict__ absmax,
@@ -328,10 +330,17 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
                                              uint64_t *__restrict__ t1w,
                                              uint64_t *__restrict__ epochs,
                                              float *__restrict__ t1_out, float *__restrict__ y,
-                                             StreamArgs sa, const int c, const int G,
-                                             const bool build_table) {
-  static_assert(R * KLW <= kMaxLines, "code lines per wave");
+                                             StreamArgs sa, const int c, const int G) {
   static_assert(M == 1 || M == 2 || M == 4 || M == 8, "batch rows");
+  // LW waves of NT threads.  The K split, the partial sums and the T1 sums
+  // follow the kLW-wave workgroup whatever LW is: wave w plays the kLW-wave
+  // workgroup's waves VPW w ... VPW w + VPW - 1 (its K-line slices one after
+  // the other, each into its own accumulators), so a layer gives the same
+  // bits in a 4-wave workgroup as in an 8-wave one.
+  static_assert(LW == kLW || (LW == kLW / 2 && M <= 2), "waves per workgroup");
+  constexpr int NT = LW * 64, VPW = kLW / LW;
+  constexpr int PKL = VPW * KLW;  // K-line slots per wave
+  static_assert(R * PKL <= (LW == kLW ? kMaxLines : kMaxLinesHalf), "code lines per wave");
   constexpr int M2 = 2 * M;
   // T1 is computed in this launch for batches of 1 and 2 and read from
   // sa.t1ext for 4 and 8 (their slices would not fit a producer lane)
@@ -350,7 +359,19 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   const int64_t KB = K >> 6;
   const int KL = (int)(K / kLine);
   const int64_t n0 = (int64_t)c * R * 16;
-  const int kl0 = KL * wave / kLW, nkl = KL * (wave + 1) / kLW - kl0;
+  // slice j of this wave: K-lines [kl0v[j], kl0v[j] + nklv[j]), slots [KLW j, KLW j + KLW)
+  int kl0v[VPW], nklv[VPW];
+#pragma unroll
+  for (int j = 0; j < VPW; ++j) {
+    kl0v[j] = KL * (VPW * wave + j) / kLW;
+    nklv[j] = KL * (VPW * wave + j + 1) / kLW - kl0v[j];
+  }
+  // slot kk's K-line (a slice's spare slots repeat its last line, weighted 0)
+  auto slot_line = [&](int kk) {
+    const int j = kk / KLW, q = kk % KLW;
+    return kl0v[j] + (q < nklv[j] ? q : nklv[j] - 1);
+  };
+  const int klf = kl0v[0], kll = kl0v[VPW - 1] + nklv[VPW - 1] - 1;  // first, last line
   const int nl = lane & 15, g = lane >> 4;
   int64_t nrow[R];
   const uint8_t *crow[R];
@@ -367,10 +388,10 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   // out before anything else is computed (only its addresses precede it).
   const int us = lane >> 3, up = (lane >> 2) & 1, ug = lane & 3;
   const int koff = step_koff(us, ug) + 4 * up;
-  float4 xv[KLW][M];
-  LineRegs L[KLW][R];
+  float4 xv[PKL][M];
+  LineRegs L[PKL][R];
   auto issue_line = [&](int kk) {
-    const int kl = kl0 + (kk < nkl ? kk : nkl - 1);
+    const int kl = slot_line(kk);
 #pragma unroll
     for (int m = 0; m < M; ++m)
       xv[kk][m] = load_x4<XBF16>(x, (int64_t)(m < sa.mact ? m : sa.mact - 1) * K +
@@ -380,7 +401,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   };
   // lines in flight: each holds M float4 of X per lane besides its codes
   constexpr int kAhead = M >= 8 ? 2 : kLinesAhead;
-  constexpr int DL = KLW < kAhead ? KLW : kAhead;
+  constexpr int DL = PKL < kAhead ? PKL : kAhead;
   // K-lines issued before the table is built: two for one tile (8 loads),
   // one for wider tiles (more loads stall issue behind a full queue).
   constexpr int DE = R == 1 && DL > 1 ? 2 : 1;
@@ -393,8 +414,8 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   if (KIND == 1) {
 #pragma unroll
     for (int t = 0; t < R; ++t) {
-      am0[t] = w.absmax[(nrow[t] * KB + 4 * kl0) >> 8];
-      am1[t] = w.absmax[(nrow[t] * KB + 4 * (kl0 + nkl - 1)) >> 8];
+      am0[t] = w.absmax[(nrow[t] * KB + 4 * klf) >> 8];
+      am1[t] = w.absmax[(nrow[t] * KB + 4 * kll) >> 8];
     }
   }
   uint64_t ev = 0;  // the epoch counter word (epoch = ev / 16)
@@ -404,14 +425,16 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   const int MR = M * r, P = sa.P, r16 = sa.r16;
   // B rows and T1 have rows of r16 floats, zero past r
   const uint32_t o_x = kTabBytes;  // one K-line of X fragments per wave
-  const uint32_t o_lb = o_x + (uint32_t)kLW * kFragLine;
+  const uint32_t o_lb = o_x + (uint32_t)LW * kFragLine;
   const uint32_t o_red = o_lb + (uint32_t)(16 * R * (r > 0 ? r16 : 1)) * 4;
   const uint32_t o_t1 = o_red + kLW * R * 16 * M * 4;
   const uint32_t o_flag = o_t1 + kT1Floats * 4;  // set when a T1 slice never arrived
   const uint32_t o_ep = o_flag + 4;       // epoch + 1 (0: not yet known)
-  const uint32_t o_tp = o_flag + 16;      // recomputed T1 slices [cc][o]
   const int mrl = sa.mrl, MRp = 1 << mrl;
-  const uint32_t o_wp = o_tp + (uint32_t)(P * MRp) * 4;  // per-wave T1 partials
+  const uint32_t o_wp = o_flag + 16;  // per-wave T1 partials [kLW][MRp]
+  // recomputed T1 slices [cc][o]: written after B2 only, when the X
+  // fragments are dead (P MRp floats fit there: host-checked)
+  const uint32_t o_tp = o_x;
 
   // ---- the codebook table, from constants: no memory round trip --------
   // Built before most loads are issued: a wave issuing more loads than the
@@ -421,7 +444,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   // Lh[q] | Ll[q] << 16, lo = 4 (wave & 3) + lane / 16 and hi = wave / 4 +
   // 2 i (uniform in the wave).  nib goes into lane q of a register from
   // immediates (indexed selects would become a constant-memory load).
-  if (build_table) {
+  {
     constexpr Tables kTab = make_tables();
     int nv = 0;
 #pragma unroll
@@ -430,16 +453,19 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
     const uint32_t nlo =
         (uint32_t)__builtin_amdgcn_ds_bpermute((4 * (wave & 3) + (lane >> 4)) * 4, nv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = (tid >> 4) + 32 * i;
-      const uint32_t nhi = (uint32_t)__builtin_amdgcn_readlane(nv, (wave >> 2) + 2 * i);
+    for (int i = 0; i < 4096 / NT; ++i) {
+      const int e = (tid >> 4) + (NT / 16) * i;
+      const uint32_t nhi = (uint32_t)__builtin_amdgcn_readlane(nv, (wave >> 2) + (NT / 256) * i);
       const uint32_t ph = (nlo & 0xffffu) | (nhi << 16), pl = (nlo >> 16) | (nhi & 0xffff0000u);
       *LDS_AT(lds_u4, (uint32_t)e * 256u + (uint32_t)(tid & 15) * 16u) = v4u{ph, pl, ph, pl};
     }
   }
-  // Wave 0 of workgroup c < P produces slice c.  Thread t reads the tagged
-  // partials of output so = t % MRp, slices sslot + (kThreads / MRp) q.
-  const int so = tid & (MRp - 1), sslot = tid >> mrl;
+  // Wave 0 of workgroup c < P produces slice c.  Thread t of the kLW-wave
+  // workgroup reads the tagged partials of output so = t % MRp, slices
+  // t / MRp + (kThreads / MRp) q; here thread (wave, lane) plays threads
+  // 64 (VPW wave + j) + lane, j < VPW (MRp <= 64: the same so).
+  const int so = lane & (MRp - 1);
+  auto sslot = [&](int j) { return (64 * (VPW * wave + j) + lane) >> mrl; };
   if (tid == 0) {
     *LDS_AT(lds_f, o_flag) = 0.0f;
     *LDS_AT(lds_f, o_ep) = 0.0f;
@@ -447,7 +473,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   if (r > 0) {
     // zero padding of lbs, t1s and the slice partials
     const v4u z4 = {0u, 0u, 0u, 0u};
-    for (int i = tid; i < 4 * R * r16; i += kThreads) *LDS_AT(lds_u4, o_lb + (uint32_t)i * 16) = z4;
+    for (int i = tid; i < 4 * R * r16; i += NT) *LDS_AT(lds_u4, o_lb + (uint32_t)i * 16) = z4;
     if (tid < kT1Floats / 4) *LDS_AT(lds_u4, o_t1 + (uint32_t)tid * 16) = z4;
   }
   lds_barrier();  // B1: the table is in LDS
@@ -460,14 +486,15 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   __builtin_amdgcn_sched_barrier(0);
   // The epilogue's operands: LoRA B rows of the workgroup's tiles (16 R r
   // <= 2 R * 512 floats) and the tagged T1 partials.
-  float lbv[2 * R];
-  uint64_t tpv[kT1Loads];  // tagged partials (slice sslot + (kThreads / MRp) q, output so)
-  int tpi[kT1Loads];       // their word indices (cc MR + so), -1: none
-#pragma unroll
-  for (int q = 0; q < kT1Loads; ++q) {
-    const int cc = sslot + (kThreads >> mrl) * q;
-    tpi[q] = so < MR && cc < P ? cc * MR + so : -1;
-  }
+  constexpr int NLB = 2 * R * VPW;  // B-row floats per thread (16 R r <= 1024 R)
+  float lbv[NLB];
+  uint64_t tpv[VPW][kT1Loads];  // tagged partials (slice sslot(j) + (kThreads / MRp) q, output so)
+  // their word indices (cc MR + so), -1: none (recomputed where used: no
+  // registers held through the stream)
+  auto tpi = [&](int j, int q) {
+    const int cc = sslot(j) + (kThreads >> mrl) * q;
+    return so < MR && cc < P ? cc * MR + so : -1;
+  };
   float t1v = 0.0f;        // batches of 4 and 8: T1 element tid (m, j)
   int t1e = -1;            // its place in LDS (m r16 + j), -1: none
   // T1 element o = lane of wave 0, (m, j) = (o / r, o % r), at m r16 + j
@@ -480,28 +507,49 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
     const int m = div_small(tid, sa.inv_r);
     t1e = m * r16 + (tid - m * r);
   }
-  // element offsets into B (N r < 2^31) and into lbs (-1: none), computed once
-  int lbi[2 * R], lbo[2 * R];
-#pragma unroll
-  for (int q = 0; q < 2 * R; ++q) {
+  // element offsets into B (N r < 2^31) and into lbs (-1: none): computed
+  // once in 8-wave workgroups, where they are used (no registers held
+  // through the stream) in 4-wave ones
+  auto lb_index = [&](int q, int &bi, int &bo) {
     const int rr = r > 0 ? r : 1;
-    const int idx = tid + 512 * q;
+    const int idx = tid + NT * q;
     const int ic = idx < 16 * R * rr ? idx : 16 * R * rr - 1;
     const int tr = div_small(ic, sa.inv_r), j = ic - tr * rr;
     int64_t row = n0 + tr;
     row = row < N ? row : N - 1;
-    lbi[q] = r > 0 ? (int)(row * rr + j) : 0;
-    lbo[q] = idx < 16 * R * rr ? tr * r16 + j : -1;
+    bi = r > 0 ? (int)(row * rr + j) : 0;
+    bo = idx < 16 * R * rr ? tr * r16 + j : -1;
+  };
+  constexpr bool kLbPre = VPW == 1;
+  int lbi[kLbPre ? NLB : 1], lbo[kLbPre ? NLB : 1];
+  if constexpr (kLbPre) {
+#pragma unroll
+    for (int q = 0; q < NLB; ++q) lb_index(q, lbi[q], lbo[q]);
   }
+  auto lb_src = [&](int q) {
+    if constexpr (kLbPre) return lbi[q];
+    int bi, bo;
+    lb_index(q, bi, bo);
+    return bi;
+  };
+  auto lb_dst = [&](int q) {
+    if constexpr (kLbPre) return lbo[q];
+    int bi, bo;
+    lb_index(q, bi, bo);
+    return bo;
+  };
   // Branch-free, so later waits count these loads exactly; with no adapter
   // they read valid words that go unused.
   const float *lbp = r > 0 ? lb : (const float *)t1w;
   auto issue_tail = [&]() {
 #pragma unroll
-    for (int q = 0; q < 2 * R; ++q) lbv[q] = lbp[lbi[q]];
+    for (int q = 0; q < NLB; ++q) lbv[q] = lbp[lb_src(q)];
     if (kT1In) {
 #pragma unroll
-      for (int q = 0; q < kT1Loads; ++q) tpv[q] = ld_dev64(t1w + (tpi[q] >= 0 ? tpi[q] : 0));
+      for (int j = 0; j < VPW; ++j)
+#pragma unroll
+        for (int q = 0; q < kT1Loads; ++q)
+          tpv[j][q] = ld_dev64(t1w + (tpi(j, q) >= 0 ? tpi(j, q) : 0));
     } else {
       // rows past mact read row mact - 1's (their outputs are not stored)
       const int mr = sa.mact * (r > 0 ? r : 1);
@@ -551,12 +599,12 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   // slices: a thread adds its slices in q order, the lanes of one output
   // add by xor butterfly (bits log2 MRp .. 5), and after the barrier wave 0
   // adds the 8 wave partials in a fixed tree.
-  auto t1_reduce = [&](const float (&v)[kT1Loads]) {
+  auto t1_reduce = [&](const float (&v)[kT1Loads], int j) {
     float p = v[0];
 #pragma unroll
     for (int q = 1; q < kT1Loads; ++q) p += v[q];
     for (int off = 32; off >= MRp; off >>= 1) p += __shfl_xor(p, off);
-    if (lane < MRp) *LDS_AT(lds_f, o_wp + (uint32_t)(wave * MRp + lane) * 4) = p;
+    if (lane < MRp) *LDS_AT(lds_f, o_wp + (uint32_t)((VPW * wave + j) * MRp + lane) * 4) = p;
   };
 
   // ---- the weight stream ----------------------------------------------
@@ -568,16 +616,29 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   {
     const uint32_t lo8 = (uint32_t)(lane & 31) * 8u;
     const int xo = (nl < M2 ? nl : M2 - 1) * 4 + g;
-    floatx4 acc[R];
+    floatx4 acc[R];  // the current K-line slice's sums
 #pragma unroll
     for (int t = 0; t < R; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Batches of 1-2: lane (nl, g) holds D rows 4g..4g+3 of column nl, y_m =
+    // D[m] + D[M+m]; slice j's sums go to LDS when it ends (red is read
+    // after B2 only) and the next slice starts from zero.
+    auto store_slice = [&](int j) {
+      if (g == 0) {
+#pragma unroll
+        for (int t = 0; t < R; ++t)
+#pragma unroll
+          for (int m = 0; m < M; ++m)
+            *LDS_AT(lds_f, o_red + (uint32_t)((((VPW * wave + j) * R + t) * M + m) * 16 + nl) * 4) =
+                acc[t][m] + acc[t][M + m];
+      }
+    };
     // Software pipeline over the wave's 8 KLW MFMA steps: the LDS operands
     // of step i + D are requested before step i's MFMAs.  A line's X
     // fragments are written and its code bytes regrouped when its first
     // step is fetched (a wave's LDS operations complete in order).
     // (the X of wider batches takes the registers of a deeper pipeline)
-    constexpr int D = R == 1 && M <= 2 ? 4 : 2;
-    constexpr int NS = KLW * 8;
+    constexpr int D = R == 1 && M <= 2 ? 4 : (LW < kLW && R >= 3 ? 1 : 2);
+    constexpr int NS = PKL * 8;
     // one line's regrouped code dwords: a line's are dead once its last
     // step is fetched, before the next line's are regrouped
     uint32_t sw[R][8];
@@ -591,11 +652,11 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int kk = i / 8, s = i % 8;
-      if (s == 0 && kk + DL < KLW) issue_line(kk + DL);
+      if (s == 0 && kk + DL < PKL) issue_line(kk + DL);
       // The epilogue's operands go out when the last line starts: the
       // producers have published by then.  (Issued earlier, right behind
       // the last line's loads, they measured no faster.)
-      if (i == (KLW - 1) * 8) issue_tail();
+      if (i == (PKL - 1) * 8) issue_tail();
       const int f = i + D;
       if (f < NS) {
         const int fk = f / 8, fs = f % 8;
@@ -612,8 +673,8 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
       }
       mfma_step<R>(ops[i % (D + 1)], d);
       if (s & 1) {  // block j = s / 2 of line kk is complete
-        const int j = s >> 1, kl = kl0 + (kk < nkl ? kk : nkl - 1);
-        const float valid = kk < nkl ? 1.0f : 0.0f;
+        const int j = s >> 1, kl = slot_line(kk), vj = kk / KLW;
+        const float valid = kk % KLW < nklv[vj] ? 1.0f : 0.0f;
 #pragma unroll
         for (int t = 0; t < R; ++t) {
           float sc;
@@ -624,7 +685,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
           } else {
             // a 256-block absmax group spans 64 K-lines: a wave's lines see
             // at most two groups
-            const float amax = ((nrow[t] * KB + 4 * kl) >> 8) == ((nrow[t] * KB + 4 * kl0) >> 8)
+            const float amax = ((nrow[t] * KB + 4 * kl) >> 8) == ((nrow[t] * KB + 4 * klf) >> 8)
                                    ? am0[t]
                                    : am1[t];
             sc = (float)(int8_t)((L[kk][t].sf.x >> (8 * j)) & 255u) *
@@ -636,21 +697,19 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
           // here, not sunk past the loop into the lanes that store it
           asm volatile("" : "+v"(acc[t]));
         }
+        if constexpr (M <= 2)
+          if (s == 7 && kk % KLW == KLW - 1 && vj < VPW - 1) {
+            store_slice(vj);
+#pragma unroll
+            for (int t = 0; t < R; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+          }
       }
       // Keep the steps in order: hoisted early, a later line's regrouping
       // would wait for that line's bytes.
       __builtin_amdgcn_sched_barrier(0);
     }
-    // Lane (nl, g) holds D rows 4g..4g+3 of column nl: y_m = D[m] + D[M+m].
     if constexpr (M <= 2) {
-      if (g == 0) {
-#pragma unroll
-        for (int t = 0; t < R; ++t)
-#pragma unroll
-          for (int m = 0; m < M; ++m)
-            *LDS_AT(lds_f, o_red + (uint32_t)(((wave * R + t) * M + m) * 16 + nl) * 4) =
-                acc[t][m] + acc[t][M + m];
-      }
+      store_slice(VPW - 1);
     } else {
       // the lo rows M + 4g + v sit M / 4 lane groups further
       const int src = lane + 16 * (M / 4);
@@ -670,8 +729,8 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   }
   if (r > 0) {
 #pragma unroll
-    for (int q = 0; q < 2 * R; ++q)
-      if (lbo[q] >= 0) *LDS_AT(lds_f, o_lb + (uint32_t)lbo[q] * 4) = lbv[q];
+    for (int q = 0; q < NLB; ++q)
+      if (const int bo = lb_dst(q); bo >= 0) *LDS_AT(lds_f, o_lb + (uint32_t)bo * 4) = lbv[q];
   }
   if (!kT1In && t1e >= 0) *LDS_AT(lds_f, o_t1 + (uint32_t)t1e * 4) = t1v;
   if (kT1In && r > 0) {
@@ -686,21 +745,24 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
     }
     bool stale = want == 0 || sa.t1_fallback != 0;
     const int polls = sa.t1_fallback ? 0 : kTagPolls;
-    float tv[kT1Loads];
 #pragma unroll
-    for (int q = 0; q < kT1Loads; ++q) {
-      tv[q] = 0.0f;
-      if (tpi[q] >= 0) {
-        uint64_t v = tpv[q];
-        for (int it = 0; it < polls && (uint32_t)(v >> 32) != want; ++it) {
-          __builtin_amdgcn_s_sleep(4);
-          v = ld_dev64(t1w + tpi[q]);
+    for (int j = 0; j < VPW; ++j) {
+      float tv[kT1Loads];
+#pragma unroll
+      for (int q = 0; q < kT1Loads; ++q) {
+        tv[q] = 0.0f;
+        if (const int ti = tpi(j, q); ti >= 0) {
+          uint64_t v = tpv[j][q];
+          for (int it = 0; it < polls && (uint32_t)(v >> 32) != want; ++it) {
+            __builtin_amdgcn_s_sleep(4);
+            v = ld_dev64(t1w + ti);
+          }
+          stale |= (uint32_t)(v >> 32) != want;
+          tv[q] = __uint_as_float((uint32_t)v);
         }
-        stale |= (uint32_t)(v >> 32) != want;
-        tv[q] = __uint_as_float((uint32_t)v);
       }
+      t1_reduce(tv, j);
     }
-    t1_reduce(tv);
     if (stale) *LDS_AT(lds_f, o_flag) = 1.0f;
   }
   lds_barrier();  // B2: partial sums, B rows and T1 slice partials are in LDS
@@ -724,13 +786,17 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
         }
       }
       lds_barrier();
-      float tv[kT1Loads];
 #pragma unroll
-      for (int q = 0; q < kT1Loads; ++q) {
-        const int cc = sslot + (kThreads >> mrl) * q;
-        tv[q] = tpi[q] >= 0 ? *LDS_AT(const lds_f, o_tp + (uint32_t)(cc * MRp + so) * 4) : 0.0f;
+      for (int j = 0; j < VPW; ++j) {
+        float tv[kT1Loads];
+#pragma unroll
+        for (int q = 0; q < kT1Loads; ++q) {
+          const int cc = sslot(j) + (kThreads >> mrl) * q;
+          tv[q] = tpi(j, q) >= 0 ? *LDS_AT(const lds_f, o_tp + (uint32_t)(cc * MRp + so) * 4)
+                                 : 0.0f;
+        }
+        t1_reduce(tv, j);
       }
-      t1_reduce(tv);
       lds_barrier();
     }
     if (wave == 0 && lane < MR) {
@@ -798,8 +864,7 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
                                                       float *__restrict__ t1_out,
                                                       float *__restrict__ y, StreamArgs sa) {
   stream_layer<XBF16, KIND, M, R, KLW>(codes, scales, absmax, x, N, K, a, r, lb, s_lora, t1w,
-                                       epochs, t1_out, y, sa, (int)blockIdx.x, (int)gridDim.x,
-                                       true);
+                                       epochs, t1_out, y, sa, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // One layer of a two-layer launch: its arguments and its workgroup count.
@@ -819,21 +884,23 @@ struct StreamLayer {
   int G;
 };
 
-// Two independent layers (batch 1) in one launch: workgroup c runs its share
-// of the first layer, then of the second, without a kernel boundary between
-// them and with the codebook table written once.
+// Two independent layers (batch 1) side by side: workgroups [0, G1) run the
+// first layer and [G1, G1 + G2) the second, 4 waves each and at most half of
+// a CU's LDS, so that a CU streams one workgroup of each layer at once: one
+// ramp and one tail for both weight streams.  Each layer's bits are those of
+// its 8-wave launch (the 4-wave workgroup plays the 8-wave K split).
 template <int XBF16, int KIND, int R1, int KLW1, int R2, int KLW2>
-__global__ __launch_bounds__(kThreads) void k_dstream2(StreamLayer L1, StreamLayer L2) {
+__global__ __launch_bounds__(kThreads / 2, 2) void k_dstream2(StreamLayer L1, StreamLayer L2) {
   const int c = (int)blockIdx.x;
   if (c < L1.G)
-    stream_layer<XBF16, KIND, 1, R1, KLW1>(L1.codes, L1.scales, L1.absmax, L1.x, L1.N, L1.K,
-                                           L1.a, L1.r, L1.lb, L1.s_lora, L1.t1w, L1.epochs,
-                                           L1.t1_out, L1.y, L1.sa, c, L1.G, true);
-  __syncthreads();  // the first layer's LDS reads are done before the second's writes
-  if (c < L2.G)
-    stream_layer<XBF16, KIND, 1, R2, KLW2>(L2.codes, L2.scales, L2.absmax, L2.x, L2.N, L2.K,
-                                           L2.a, L2.r, L2.lb, L2.s_lora, L2.t1w, L2.epochs,
-                                           L2.t1_out, L2.y, L2.sa, c, L2.G, c >= L1.G);
+    stream_layer<XBF16, KIND, 1, R1, KLW1, kLW / 2>(L1.codes, L1.scales, L1.absmax, L1.x, L1.N,
+                                                    L1.K, L1.a, L1.r, L1.lb, L1.s_lora, L1.t1w,
+                                                    L1.epochs, L1.t1_out, L1.y, L1.sa, c, L1.G);
+  else
+    stream_layer<XBF16, KIND, 1, R2, KLW2, kLW / 2>(L2.codes, L2.scales, L2.absmax, L2.x, L2.N,
+                                                    L2.K, L2.a, L2.r, L2.lb, L2.s_lora, L2.t1w,
+                                                    L2.epochs, L2.t1_out, L2.y, L2.sa, c - L1.G,
+                                                    L2.G);
 }
 
 // ---- host side --------------------------------------------------------------
@@ -879,8 +946,10 @@ bool shape_compiled(int R, int KLW, int Mt) {
 // rows in chunks of 8, the last one padded).
 int stream_rows(int64_t M, int64_t mact) { return M <= 2 ? (int)M : (mact <= 4 ? 4 : 8); }
 
-// Plan of one launch of mact rows (<= 8) with template rows Mt.
-StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r) {
+// Plan of one launch of mact rows (<= 8) with template rows Mt, in
+// workgroups of LW waves (kLW, or kLW / 2 for the side-by-side layer pair:
+// then at most half of a CU's LDS).
+StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r, int LW = kLW) {
   StreamPlan p;
   const int cus = cu_count();
   const int64_t r16 = (r + 15) & ~(int64_t)15;
@@ -895,6 +964,7 @@ StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r) {
   const int64_t R = (T + cus - 1) / cus;
   const int64_t KLW = (KL + kLW - 1) / kLW;
   if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW, Mt)) return p;
+  if (LW != kLW && (LW != kLW / 2 || Mt > 2 || R * KLW * (kLW / LW) > kMaxLinesHalf)) return p;
   const int64_t G = (T + R - 1) / R;
   const int64_t M = Mt;
   int64_t MRp = 1;
@@ -907,13 +977,15 @@ StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r) {
     if (w.cols / 4 < P || (units + lpj - 1) / lpj > t1_units((int)R)) return p;
     if (MRp > 64 || P * MRp > (int64_t)kT1Loads * kThreads) return p;
   }
-  // recomputed slices (P MRp floats) and per-wave partials (kLW MRp floats)
-  const size_t t1_floats = t1in && r > 0 ? (size_t)(P + kLW) * MRp : 0;
+  // per-wave T1 partials (kLW MRp floats); the recomputed slices (P MRp
+  // floats) reuse the X fragments' space
   const size_t frag_line = (size_t)16 * 2 * M * 4 * (M == 1 ? 16 : 8);
-  const size_t lds = kTabBytes + (size_t)kLW * frag_line +
+  if (t1in && r > 0 && (size_t)P * MRp * 4 > (size_t)LW * frag_line) return p;
+  const size_t t1_floats = t1in && r > 0 ? (size_t)kLW * MRp : 0;
+  const size_t lds = kTabBytes + (size_t)LW * frag_line +
                      (size_t)16 * R * (r > 0 ? r16 : 1) * 4 + (size_t)kLW * R * 16 * M * 4 +
                      (size_t)(t1in ? 64 : 64 * M) * 4 + 16 + t1_floats * 4;
-  if (lds > kLdsLimit) return p;
+  if (lds > (LW == kLW ? kLdsLimit : kLdsLimit / 2)) return p;
   p.sa.P = (int)P;
   p.sa.mrl = 63 - __builtin_clzll((unsigned long long)MRp);
   p.sa.r16 = (int)r16;
@@ -1017,20 +1089,19 @@ hipError_t run_stream2(const StreamLayer &L1, const StreamLayer &L2, uint32_t ld
   if (!attr) {
     const hipError_t e = hipFuncSetAttribute((const void *)k,
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)kLdsLimit);
+                                             (int)kLdsLimit / 2);
     if (e != hipSuccess) return e;
     attr = true;
   }
-  const int G = std::max(L1.G, L2.G);
-  return qh_launch(k, dim3((unsigned)G), dim3(kThreads), lds, st, L1, L2);
+  return qh_launch(k, dim3((unsigned)(L1.G + L2.G)), dim3(kThreads / 2), lds, st, L1, L2);
 }
 
 template <int XBF16, int KIND>
 hipError_t dispatch_pair(const StreamPlan &p1, const StreamPlan &p2, const StreamLayer &L1,
                          const StreamLayer &L2, hipStream_t st) {
   const uint32_t lds = std::max(p1.lds, p2.lds);
-#define QH_PAIR_CASE(a, b, c, d)                                        \
-  if (p1.R == a && p1.KLW == b && p2.R == c && p2.KLW == d)             \
+#define QH_PAIR_CASE(a, b, c, d)                                          \
+  if (p1.R == a && p1.KLW == b && p2.R == c && p2.KLW == d)               \
     return run_stream2<XBF16, KIND, a, b, c, d>(L1, L2, lds, st);
   QH_STREAM_PAIRS(QH_PAIR_CASE)
 #undef QH_PAIR_CASE
@@ -1041,7 +1112,7 @@ hipError_t dispatch_pair(const StreamPlan &p1, const StreamPlan &p2, const Strea
 
 bool decode_stream2_ok(const DevQW &w1, int64_t r1, const DevQW &w2, int64_t r2) {
   if (w1.kind != w2.kind) return false;
-  const StreamPlan p1 = stream_plan(w1, 1, 1, r1), p2 = stream_plan(w2, 1, 1, r2);
+  const StreamPlan p1 = stream_plan(w1, 1, 1, r1, kLW / 2), p2 = stream_plan(w2, 1, 1, r2, kLW / 2);
   return p1.ok && p2.ok && pair_compiled(p1.R, p1.KLW, p2.R, p2.KLW);
 }
 
@@ -1052,7 +1123,7 @@ hipError_t launch_decode_stream2(const DevQW &w1, const void *x1, const float *a
                                  int x_bf16, unsigned *tickets, bool force_t1_recompute,
                                  hipStream_t st) {
   if (!decode_stream2_ok(w1, r1, w2, r2)) return hipErrorInvalidValue;
-  StreamPlan p1 = stream_plan(w1, 1, 1, r1), p2 = stream_plan(w2, 1, 1, r2);
+  StreamPlan p1 = stream_plan(w1, 1, 1, r1, kLW / 2), p2 = stream_plan(w2, 1, 1, r2, kLW / 2);
   p1.sa.t1_fallback = p2.sa.t1_fallback = force_t1_recompute ? 1 : 0;
   // the first layer uses the single-layer launches' counters and T1 words,
   // the second its own
