@@ -218,53 +218,49 @@ struct WTileRow {
   }
 };
 
-// ---- NF4 tile, input-gradient orientation: 32 W rows (reduction) x BN W
-// columns (outputs), written transposed (LDS row = W column).  Thread t holds
-// one code byte (W columns c0 + 2 (t % BPR), + 1) of the RPT W rows n0 + RPT
-// (t / BPR) ... + RPT, so consecutive lanes write LDS rows two apart.
+// ---- NF4 tile, input-gradient orientation: 32 W rows (the reduction) x BN
+// W columns (the outputs), row-major in LDS (row stride ldb_t(BN)), read
+// column-wise by the LDS transpose loads (mma below).  Thread t holds EPT
+// consecutive columns (t % TPR) * EPT of W row k0 + t / TPR: one code load
+// and one block scale, as in the forward.
+__host__ __device__ constexpr int ldb_t(int bn) { return bn + 32; }  // 64 bytes of padding
+
 template <class C, int KIND>
-struct WTileCol {
-  static constexpr int BPR = C::BN / 2;         // code bytes per W row
-  static constexpr int RG = C::T / BPR;         // row groups
-  static constexpr int RPT = kBK / RG;          // rows per thread: 8 or 4
-  static_assert(RPT == 8 || RPT == 4, "rows per thread");
-  uint8_t c[RPT];
-  ScaleRef sr[RPT];
-  __device__ __forceinline__ void load(const DevQW &w, int64_t c0, int64_t n0) {
-    const int64_t col = c0 + 2 * (threadIdx.x % BPR);
-    const int64_t row0 = n0 + RPT * (threadIdx.x / BPR);
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int64_t n = row0 + i;
-      const bool ok = n < w.rows && col < w.cols;
-      const int64_t e = ok ? n * w.cols + col : 0;
-      const uint8_t t = w.codes[e >> 1];
-      const ScaleRef r = load_scale<KIND>(w, e >> 6);
-      c[i] = ok ? t : (uint8_t)0;
-      sr[i] = ScaleRef{ok ? r.a : 0.0f, r.c};
-    }
+struct WTileKRow {
+  static constexpr int EPT = C::BN * kBK / C::T;  // columns per thread: 16 or 8
+  static constexpr int TPR = C::BN / EPT;          // threads per W row
+  static_assert(EPT == 16 || EPT == 8, "columns per thread");
+  static_assert(TPR * kBK == C::T, "one W row per TPR threads");
+  uint2 c;        // EPT / 2 code bytes
+  ScaleRef sr;
+  __device__ __forceinline__ void load(const DevQW &w, int64_t n0, int64_t k0) {
+    const int64_t n = k0 + threadIdx.x / TPR;                 // W row (reduction)
+    const int64_t col = n0 + (threadIdx.x % TPR) * EPT;       // W column (output)
+    const bool ok = n < w.rows && col < w.cols;               // cols % 64 == 0
+    const int64_t e = ok ? n * w.cols + col : 0;
+    uint2 t;
+    if (EPT == 16) t = *(const uint2 *)(w.codes + (e >> 1));
+    else t = make_uint2(*(const uint32_t *)(w.codes + (e >> 1)), 0u);
+    const ScaleRef r = load_scale<KIND>(w, e >> 6);
+    if (!ok) t = make_uint2(0, 0);
+    c = t;
+    sr = ScaleRef{ok ? r.a : 0.0f, r.c};
   }
   __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl, const float *lut) const {
-    const int cl = 2 * (threadIdx.x % BPR), rl = RPT * (threadIdx.x / BPR);
-    float s[RPT];
+    const int row = threadIdx.x / TPR, c0 = (threadIdx.x % TPR) * EPT;
+    const float s = decode_scale<KIND>(sr);
+    const uint32_t cw[2] = {c.x, c.y};
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = decode_scale<KIND>(sr[i]);
+    for (int q = 0; q < EPT / 8; ++q) {  // 8 columns = one code word
+      float f[8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {  // W column cl + j: RPT consecutive reduction rows
-      float f[RPT];
+      for (int e = 0; e < 8; ++e) f[e] = lut[(cw[q] >> (4 * e)) & 15u] * s;
+      uint32_t h[4], l[4];
 #pragma unroll
-      for (int i = 0; i < RPT; ++i) f[i] = lut[((uint32_t)c[i] >> (4 * j)) & 15u] * s[i];
-      uint32_t h[RPT / 2], l[RPT / 2];
-#pragma unroll
-      for (int e = 0; e < RPT / 2; ++e) split2(f[2 * e], f[2 * e + 1], h[e], l[e]);
-      const int o = sw(cl + j, rl >> 3) + (rl & 7);
-      if constexpr (RPT == 8) {
-        *(uint4 *)(Sh + o) = make_uint4(h[0], h[1], h[2], h[3]);
-        *(uint4 *)(Sl + o) = make_uint4(l[0], l[1], l[2], l[3]);
-      } else {
-        *(uint2 *)(Sh + o) = make_uint2(h[0], h[1]);
-        *(uint2 *)(Sl + o) = make_uint2(l[0], l[1]);
-      }
+      for (int e = 0; e < 4; ++e) split2(f[2 * e], f[2 * e + 1], h[e], l[e]);
+      const int o = row * ldb_t(C::BN) + c0 + 8 * q;
+      *(uint4 *)(Sh + o) = make_uint4(h[0], h[1], h[2], h[3]);
+      *(uint4 *)(Sl + o) = make_uint4(l[0], l[1], l[2], l[3]);
     }
   }
 };
@@ -295,8 +291,9 @@ __device__ __forceinline__ void stage_f32_rowk(const float *p, int64_t ld, int64
   }
 }
 
-// 32 x R of a row-major fp32 matrix read transposed (element (col, k) at
-// p[k * ld + col]): thread t of T owns reduction rows t / (R / 4) + KS v and
+// 32 x R of a row-major fp32 matrix (element (col, k) at p[k * ld + col]),
+// scaled, into the input gradient's row-major B layout (row k, column col,
+// row stride ldb_t(R)): thread t owns reduction rows t / (R / 4) + KS v and
 // columns 4 (t % (R / 4)) ... + 4.
 template <int R, int T>
 __device__ __forceinline__ void stage_f32_krow(const float *p, int64_t ld, int64_t c0, int64_t clim,
@@ -309,16 +306,18 @@ __device__ __forceinline__ void stage_f32_krow(const float *p, int64_t ld, int64
   for (int i = 0; i < kBK / KS; ++i) {
     const int kl = threadIdx.x / CG + KS * i;
     const int64_t k = k0 + kl;
+    float f[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t col = c0 + cl + j;
-      const float f = (k < klim && col < clim) ? p[k * ld + col] * scale : 0.0f;
-      const __bf16 h = (__bf16)f;
-      const __bf16 l = (__bf16)(f - (float)h);
-      const int o = sw(cl + j, kl >> 3) + (kl & 7);
-      Sh[o] = __builtin_bit_cast(uint16_t, h);
-      Sl[o] = __builtin_bit_cast(uint16_t, l);
+      f[j] = (k < klim && col < clim) ? p[k * ld + col] * scale : 0.0f;
     }
+    uint32_t h0, h1, l0, l1;
+    split2(f[0], f[1], h0, l0);
+    split2(f[2], f[3], h1, l1);
+    const int o = kl * ldb_t(R) + cl;
+    *(uint2 *)(Sh + o) = make_uint2(h0, h1);
+    *(uint2 *)(Sl + o) = make_uint2(l0, l1);
   }
 }
 
@@ -333,7 +332,9 @@ __device__ __forceinline__ void stage_f32_krow(const float *p, int64_t ld, int64
 template <class C, int WF, int XF, int KIND>
 __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_n) {
   constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN, KS = C::KS;
-  constexpr int A_ELEMS = BM * kBK, B_ELEMS = BN * kBK;
+  // B: the forward's W rows as 32-element LDS rows; the input gradient's
+  // 32 W rows row-major (ldb_t(BN) per row)
+  constexpr int A_ELEMS = BM * kBK, B_ELEMS = WF == ROWK ? BN * kBK : kBK * ldb_t(BN);
   constexpr int SUB = 2 * A_ELEMS + 2 * B_ELEMS;  // one 32-wide sub-tile
   constexpr int STAGE = KS * SUB;
   extern __shared__ __align__(16) uint16_t smem[];
@@ -368,6 +369,24 @@ __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  // Input gradient: the B operand of lane l (column l % 32 of the MFMA's
+  // 32, reduction rows 8 (l / 32) ... + 8) from the row-major W tile by two
+  // LDS transpose loads.  Within each 16 lanes, ds_read_b64_tr_b16 gives
+  // lane i element i % 4 of the 8-byte pieces read by lanes i / 4 + 4 q,
+  // q = 0..3: lane i reads columns c0 + 4 (i % 4) ... + 4 of row r0 + i / 4
+  // (+ 4 for the second load), and receives rows r0 ... r0 + 3 (+ 4) of
+  // column c0 + i.
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  auto tr_operand = [&](const uint16_t *B, int r0, int c0, int ln) {
+    const int i = ln & 15;
+    const uint16_t *p = B + (r0 + (i >> 2)) * ldb_t(BN) + c0 + 4 * (i & 3);
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)p);
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)(p + 4 * ldb_t(BN)));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  };
   // 2 x 16 of the reduction from one stage: ah.bh + ah.bl (+ al.bh when the
   // A operand has a lo part).
   auto mma = [&](const uint16_t *Ah, const uint16_t *Al, const uint16_t *Bh, const uint16_t *Bl,
@@ -382,8 +401,13 @@ __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        bh[j] = *(const bf16x8_t *)(Bh + sw(wn0 + 32 * j + l32, 2 * kk + h));
-        bl[j] = *(const bf16x8_t *)(Bl + sw(wn0 + 32 * j + l32, 2 * kk + h));
+        if constexpr (WF == ROWK) {
+          bh[j] = *(const bf16x8_t *)(Bh + sw(wn0 + 32 * j + l32, 2 * kk + h));
+          bl[j] = *(const bf16x8_t *)(Bl + sw(wn0 + 32 * j + l32, 2 * kk + h));
+        } else {
+          bh[j] = tr_operand(Bh, 16 * kk + 8 * h, wn0 + 32 * j + 16 * ((lane >> 4) & 1), lane);
+          bl[j] = tr_operand(Bl, 16 * kk + 8 * h, wn0 + 32 * j + 16 * ((lane >> 4) & 1), lane);
+        }
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -406,7 +430,7 @@ __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_
   };
 
   // ---- segment 1: activations x dequantized weight ---------------------------
-  using WT = typename std::conditional<WF == ROWK, WTileRow<C, KIND>, WTileCol<C, KIND>>::type;
+  using WT = typename std::conditional<WF == ROWK, WTileRow<C, KIND>, WTileKRow<C, KIND>>::type;
   struct Regs {  // one step's loads: KS sub-tiles
     ActTile<XF, C> a[KS];
     WT w[KS];
@@ -541,7 +565,8 @@ __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_
 template <class C, int WF, int XF, int KIND>
 hipError_t run_bf16(const Bf16GemmArgs &g0, int splits, float *partial, hipStream_t s) {
   auto k = k_nf4_bf16<C, WF, XF, KIND>;
-  constexpr uint32_t lds = (uint32_t)(2 * C::KS * (2 * C::BM + 2 * C::BN) * kBK * 2 + 16 * 4);
+  constexpr int b_elems = WF == ROWK ? C::BN * kBK : kBK * ldb_t(C::BN);
+  constexpr uint32_t lds = (uint32_t)(2 * C::KS * (2 * C::BM * kBK + 2 * b_elems) * 2 + 16 * 4);
   static bool attr = false;  // per instantiation
   if (!attr) {
     const hipError_t e =
