@@ -51,19 +51,20 @@ constexpr int kBK = 32;          // reduction per step = one LDS row
 // Block shape: T threads (T / 64 waves in a 2 x T/128 grid), BM x BN outputs;
 // a step reduces KS x 32 (KS LDS sub-tiles between two barriers) and its
 // global loads are issued PF steps before its MFMAs.
-template <int T_, int BM_, int BN_, int PF_ = 1, int KS_ = 1>
+template <int T_, int BM_, int BN_, int PF_ = 1, int KS_ = 1, int PP_ = 0>
 struct Cfg {
-  static constexpr int T = T_, BM = BM_, BN = BN_, PF = PF_, KS = KS_;
+  static constexpr int T = T_, BM = BM_, BN = BN_, PF = PF_, KS = KS_, PP = PP_;
   static_assert(PF == 1 || PF == 2, "prefetch depth");
   static_assert(KS == 1 || KS == 2, "sub-tiles per step");
+  static_assert(!PP || (PF == 1 && KS == 1 && T == 512), "ping-pong blocks");
   static constexpr int WGN = T / 128;              // wave grid: 2 x WGN
   static constexpr int WTM = BM / 2, WTN = BN / WGN;  // one wave's outputs
   static constexpr int TM = WTM / 32, TN = WTN / 32;  // 32 x 32 MFMA tiles per wave
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(BN <= T && BM % (T / 4) == 0, "staging maps");
 };
-using CfgL256 = Cfg<512, 256, 256>;
-using CfgL128 = Cfg<512, 256, 128>;
+using CfgL256 = Cfg<512, 256, 256, 1, 1, 1>;
+using CfgL128 = Cfg<512, 256, 128, 1, 1, 1>;
 using CfgM = Cfg<512, 128, 128, 2, 2>;
 using CfgM1 = Cfg<512, 128, 128, 2, 1>;  // half the LDS: two blocks per CU
 using CfgS = Cfg<256, 64, 64, 2, 2>;
@@ -113,6 +114,11 @@ __device__ __forceinline__ float decode_scale(ScaleRef r) {
 // ---- activation tile: BM rows x 32 of a row-major (rows x K) matrix ----------
 // Thread t owns rows t / 4 + (T / 4) v and granule t % 4 (elements 8 (t % 4)
 // ... + 8).  bf16 (XF = 0) is copied; fp32 (XF = 1) is split into hi and lo.
+// The tiles take thread t = threadIdx.x % C::T, so that a half-size C lets
+// each half of a block stage its own half of a tile.  Rows and elements past
+// the matrix are loaded from a valid address and zeroed when written to LDS,
+// not when loaded: nothing touches loaded data before its LDS write, so the
+// MFMAs issued in between never wait for those loads.
 template <int XF, class C>
 struct ActTile;
 
@@ -120,23 +126,28 @@ template <class C>
 struct ActTile<0, C> {
   static constexpr int P = C::BM / (C::T / 4);  // passes
   uint4 v[P];
+  uint32_t okm;  // bit i: pass i in range
   __device__ __forceinline__ void load(const void *pv, int64_t ld, int64_t m0, int64_t M,
                                        int64_t k0, int64_t K) {
     const uint16_t *p = (const uint16_t *)pv;
-    const int c = threadIdx.x & 3;
+    const int c = (threadIdx.x % C::T) & 3;
+    okm = 0;
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const int64_t row = m0 + (threadIdx.x >> 2) + (C::T / 4) * i, k = k0 + 8 * c;
+      const int64_t row = m0 + ((threadIdx.x % C::T) >> 2) + (C::T / 4) * i, k = k0 + 8 * c;
       const bool ok = row < M && k < K;
-      uint4 t = *(const uint4 *)(p + (ok ? row * ld + k : 0));
-      if (!ok) t = make_uint4(0, 0, 0, 0);
-      v[i] = t;
+      v[i] = *(const uint4 *)(p + (ok ? row * ld + k : 0));
+      okm |= (uint32_t)ok << i;
     }
   }
   __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *) const {
-    const int c = threadIdx.x & 3;
+    const int c = (threadIdx.x % C::T) & 3;
 #pragma unroll
-    for (int i = 0; i < P; ++i) *(uint4 *)(Sh + sw((threadIdx.x >> 2) + (C::T / 4) * i, c)) = v[i];
+    for (int i = 0; i < P; ++i) {
+      uint4 t = v[i];
+      if (!((okm >> i) & 1u)) t = make_uint4(0, 0, 0, 0);
+      *(uint4 *)(Sh + sw(((threadIdx.x % C::T) >> 2) + (C::T / 4) * i, c)) = t;
+    }
   }
 };
 
@@ -144,32 +155,35 @@ template <class C>
 struct ActTile<1, C> {
   static constexpr int P = C::BM / (C::T / 4);  // passes
   float4 v[P][2];
+  uint32_t okm;  // bit i: pass i in range
   __device__ __forceinline__ void load(const void *pv, int64_t ld, int64_t m0, int64_t M,
                                        int64_t k0, int64_t K) {
     const float *p = (const float *)pv;
-    const int c = threadIdx.x & 3;
-    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int c = (threadIdx.x % C::T) & 3;
+    okm = 0;
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const int64_t row = m0 + (threadIdx.x >> 2) + (C::T / 4) * i, k = k0 + 8 * c;
+      const int64_t row = m0 + ((threadIdx.x % C::T) >> 2) + (C::T / 4) * i, k = k0 + 8 * c;
       const bool ok = row < M && k < K;
       const float *q = p + (ok ? row * ld + k : 0);
-      float4 t0 = *(const float4 *)q, t1 = *(const float4 *)(q + 4);
-      if (!ok) t0 = z, t1 = z;  // (a select of whole vectors went to scratch)
-      v[i][0] = t0;
-      v[i][1] = t1;
+      v[i][0] = *(const float4 *)q;
+      v[i][1] = *(const float4 *)(q + 4);
+      okm |= (uint32_t)ok << i;
     }
   }
   __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl) const {
-    const int c = threadIdx.x & 3;
+    const int c = (threadIdx.x % C::T) & 3;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int i = 0; i < P; ++i) {
+      float4 t0 = v[i][0], t1 = v[i][1];
+      if (!((okm >> i) & 1u)) t0 = z, t1 = z;  // (a select of whole vectors went to scratch)
       uint32_t h[4], l[4];
-      split2(v[i][0].x, v[i][0].y, h[0], l[0]);
-      split2(v[i][0].z, v[i][0].w, h[1], l[1]);
-      split2(v[i][1].x, v[i][1].y, h[2], l[2]);
-      split2(v[i][1].z, v[i][1].w, h[3], l[3]);
-      const int o = sw((threadIdx.x >> 2) + (C::T / 4) * i, c);
+      split2(t0.x, t0.y, h[0], l[0]);
+      split2(t0.z, t0.w, h[1], l[1]);
+      split2(t1.x, t1.y, h[2], l[2]);
+      split2(t1.z, t1.w, h[3], l[3]);
+      const int o = sw(((threadIdx.x % C::T) >> 2) + (C::T / 4) * i, c);
       *(uint4 *)(Sh + o) = make_uint4(h[0], h[1], h[2], h[3]);
       *(uint4 *)(Sl + o) = make_uint4(l[0], l[1], l[2], l[3]);
     }
@@ -186,22 +200,20 @@ struct WTileRow {
   static_assert(TPR == 2 || TPR == 4, "threads per W row");
   uint2 c;        // EPT / 2 code bytes
   ScaleRef sr;
+  bool in;        // in range (else the elements are written as zeros)
   __device__ __forceinline__ void load(const DevQW &w, int64_t n0, int64_t k0) {
-    const int64_t n = n0 + threadIdx.x / TPR;
-    const int64_t k = k0 + (threadIdx.x % TPR) * EPT;
+    const int64_t n = n0 + (threadIdx.x % C::T) / TPR;
+    const int64_t k = k0 + ((threadIdx.x % C::T) % TPR) * EPT;
     const bool ok = n < w.rows && k < w.cols;
     const int64_t e = ok ? n * w.cols + k : 0;
-    uint2 t;
-    if (EPT == 16) t = *(const uint2 *)(w.codes + (e >> 1));
-    else t = make_uint2(*(const uint32_t *)(w.codes + (e >> 1)), 0u);
-    const ScaleRef r = load_scale<KIND>(w, e >> 6);
-    if (!ok) t = make_uint2(0, 0);
-    c = t;
-    sr = ScaleRef{ok ? r.a : 0.0f, r.c};
+    if (EPT == 16) c = *(const uint2 *)(w.codes + (e >> 1));
+    else c = make_uint2(*(const uint32_t *)(w.codes + (e >> 1)), 0u);
+    sr = load_scale<KIND>(w, e >> 6);
+    in = ok;
   }
   __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl, const float *lut) const {
-    const int row = threadIdx.x / TPR, g0 = (threadIdx.x % TPR) * (EPT / 8);
-    const float s = decode_scale<KIND>(sr);
+    const int row = (threadIdx.x % C::T) / TPR, g0 = ((threadIdx.x % C::T) % TPR) * (EPT / 8);
+    const float s = in ? decode_scale<KIND>(sr) : 0.0f;
     const uint32_t cw[2] = {c.x, c.y};
 #pragma unroll
     for (int q = 0; q < EPT / 8; ++q) {  // 8 elements = one code word = one granule
@@ -225,7 +237,7 @@ struct WTileRow {
 // and one block scale, as in the forward.
 __host__ __device__ constexpr int ldb_t(int bn) { return bn + 32; }  // 64 bytes of padding
 
-template <class C, int KIND>
+template <class C, int KIND, int LDB = ldb_t(C::BN)>
 struct WTileKRow {
   static constexpr int EPT = C::BN * kBK / C::T;  // columns per thread: 16 or 8
   static constexpr int TPR = C::BN / EPT;          // threads per W row
@@ -233,22 +245,20 @@ struct WTileKRow {
   static_assert(TPR * kBK == C::T, "one W row per TPR threads");
   uint2 c;        // EPT / 2 code bytes
   ScaleRef sr;
+  bool in;        // in range (else the elements are written as zeros)
   __device__ __forceinline__ void load(const DevQW &w, int64_t n0, int64_t k0) {
-    const int64_t n = k0 + threadIdx.x / TPR;                 // W row (reduction)
-    const int64_t col = n0 + (threadIdx.x % TPR) * EPT;       // W column (output)
+    const int64_t n = k0 + (threadIdx.x % C::T) / TPR;                 // W row (reduction)
+    const int64_t col = n0 + ((threadIdx.x % C::T) % TPR) * EPT;       // W column (output)
     const bool ok = n < w.rows && col < w.cols;               // cols % 64 == 0
     const int64_t e = ok ? n * w.cols + col : 0;
-    uint2 t;
-    if (EPT == 16) t = *(const uint2 *)(w.codes + (e >> 1));
-    else t = make_uint2(*(const uint32_t *)(w.codes + (e >> 1)), 0u);
-    const ScaleRef r = load_scale<KIND>(w, e >> 6);
-    if (!ok) t = make_uint2(0, 0);
-    c = t;
-    sr = ScaleRef{ok ? r.a : 0.0f, r.c};
+    if (EPT == 16) c = *(const uint2 *)(w.codes + (e >> 1));
+    else c = make_uint2(*(const uint32_t *)(w.codes + (e >> 1)), 0u);
+    sr = load_scale<KIND>(w, e >> 6);
+    in = ok;
   }
   __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl, const float *lut) const {
-    const int row = threadIdx.x / TPR, c0 = (threadIdx.x % TPR) * EPT;
-    const float s = decode_scale<KIND>(sr);
+    const int row = (threadIdx.x % C::T) / TPR, c0 = ((threadIdx.x % C::T) % TPR) * EPT;
+    const float s = in ? decode_scale<KIND>(sr) : 0.0f;
     const uint32_t cw[2] = {c.x, c.y};
 #pragma unroll
     for (int q = 0; q < EPT / 8; ++q) {  // 8 columns = one code word
@@ -258,7 +268,7 @@ struct WTileKRow {
       uint32_t h[4], l[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) split2(f[2 * e], f[2 * e + 1], h[e], l[e]);
-      const int o = row * ldb_t(C::BN) + c0 + 8 * q;
+      const int o = row * LDB + c0 + 8 * q;
       *(uint4 *)(Sh + o) = make_uint4(h[0], h[1], h[2], h[3]);
       *(uint4 *)(Sl + o) = make_uint4(l[0], l[1], l[2], l[3]);
     }
@@ -486,7 +496,85 @@ __global__ __launch_bounds__(C::T, 2) void k_nf4_bf16(Bf16GemmArgs g, int tiles_
     }
   };
   Regs ra;
-  if constexpr (C::PF == 1) {
+  if constexpr (C::PP) {
+    // Ping-pong: waves 0-3 (group 0) and 4-7 (group 1), one of each per SIMD,
+    // take turns: while group 0 runs step t's MFMAs, group 1 dequantizes and
+    // writes its half of step t + 1 (A rows BM/2 .., W rows or columns
+    // BN/2 ..); after a barrier the roles swap.  So a SIMD keeps one wave on
+    // the matrix core while the other does the VALU work.  Two barriers per
+    // step; step t + 1's LDS stage is complete (both halves) before either
+    // group reads it, and step t's is read by both before step t + 2's
+    // writes start.  A group's loads are issued one phase before it writes
+    // them, ahead of its MFMAs.
+    using HC = Cfg<C::T / 2, BM / 2, BN / 2>;
+    using HW = typename std::conditional<WF == ROWK, WTileRow<HC, KIND>,
+                                         WTileKRow<HC, KIND, ldb_t(BN)>>::type;
+    struct HRegs {
+      ActTile<XF, HC> a;
+      HW w;
+    };
+    const int grp = wave >= C::T / 128 ? 1 : 0;  // wave-uniform
+    auto hload = [&](HRegs &R, int64_t t, int hf) {
+      const int64_t k = t * kBK, ma = m0 + hf * (BM / 2), nb = n0 + hf * (BN / 2);
+      if constexpr (WF == ROWK) {
+        R.a.load(g.A, g.lda, ma, g.M, k, g.K);
+        R.w.load(g.seg[sg].w, nb, k);
+      } else {
+        int i = 0;
+        int64_t tl = t;
+        for (; i + 1 < g.nseg; ++i) {
+          const int64_t st = (g.seg[i].len + kBK - 1) / kBK;
+          if (tl < st) break;
+          tl -= st;
+        }
+        const Bf16Seg &q = g.seg[i];
+        R.a.load(q.A, q.lda, ma, g.M, tl * kBK, q.len);
+        R.w.load(q.w, nb, tl * kBK);
+      }
+    };
+    auto hstage = [&](uint16_t *D, const HRegs &R, int hf) {
+      const int ao = hf * (BM / 2) * kBK;
+      R.a.store(D + ao, D + A_ELEMS + ao);
+      const int bo = WF == ROWK ? hf * (BN / 2) * kBK : hf * (BN / 2);
+      R.w.store(D + 2 * A_ELEMS + bo, D + 2 * A_ELEMS + B_ELEMS + bo, lut);
+    };
+    // one copy of the loop per group, its half a constant
+    auto run = [&](auto G) {
+      constexpr int gp = decltype(G)::value;
+      HRegs r;
+      hload(r, t0, gp);
+      __syncthreads();  // codebook
+      hstage(smem, r, gp);
+      if (gp == 1 && t0 + 1 < t1) hload(r, t0 + 1, 1);
+      __syncthreads();
+      // Each step is two phases: group 0 loads its half of step t + 1 and
+      // runs step t's MFMAs while group 1 writes its half of step t + 1;
+      // then group 1 loads its half of step t + 2 and runs step t's MFMAs
+      // while group 0 writes its half of step t + 1.  (Each group's loop is
+      // straight-line code: with the roles chosen by a branch in one loop the
+      // compiler spilled the accumulators.)
+      for (int64_t t = t0; t < t1; ++t) {
+        uint16_t *cur = smem + ((t - t0) & 1) * STAGE, *nxt = smem + ((t + 1 - t0) & 1) * STAGE;
+        if constexpr (gp == 0) {
+          if (t + 1 < t1) hload(r, t + 1, 0);
+          mma_stage(cur);
+          __syncthreads();
+          if (t + 1 < t1) hstage(nxt, r, 0);
+          __syncthreads();
+        } else {
+          if (t + 1 < t1) hstage(nxt, r, 1);
+          __syncthreads();
+          if (t + 2 < t1) hload(r, t + 2, 1);
+          mma_stage(cur);
+          __syncthreads();
+        }
+      }
+    };
+    if (t1 > t0) {
+      if (grp == 0) run(std::integral_constant<int, 0>{});
+      else run(std::integral_constant<int, 1>{});
+    }
+  } else if constexpr (C::PF == 1) {
     if (t1 > t0) {
       load(ra, t0);
       __syncthreads();  // codebook
