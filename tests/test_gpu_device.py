@@ -46,7 +46,10 @@ def test_prefill_shape_parity(ctx, QD, act):
     (640, 320, 1, 40, torch.bfloat16),     # rank 1
     (256, 200, 16, 50, torch.float32),     # K not a multiple of 16 (fp32 weight path)
     (1536, 576, 8, 64, torch.float32),     # Ds over N = 1536
-    (256, 2560, 16, 40, torch.float32),    # T1 past K = 2048: the tile engine again
+    (256, 2560, 16, 40, torch.float32),    # T1 past K = 2048: the dense bf16 kernel
+    (320, 640, 24, 2104, torch.float32),   # grad_A / grad_B past 2048 tokens: dense kernel
+    (512, 384, 40, 2300, torch.bfloat16),  # the same with bf16 X and dY, ragged tiles
+    (192, 576, 33, 2050, torch.float32),   # r not a multiple of 8: the tile engine
 ])
 def test_rank_gemm_shapes_parity(ctx, QD, N, K, r, M, act):
     _say(f"rank-gemm shapes N={N} K={K} r={r} M={M} act={act}")

@@ -750,6 +750,260 @@ hipError_t pick_kind(const Bf16GemmArgs &g, int splits, float *partial, hipStrea
                               : pick<WF, XF, 1>(g, splits, partial, s);
 }
 
+// ---- dense GEMMs on bf16 MFMA: the LoRA-rank products ------------------------
+// C = alpha * sum_k A(m, k) B(n, k) with both operands dense fp32 (split into
+// bf16 hi + lo) or bf16, each stored either ROWK (row-major along k: staged
+// like the activations above) or KROW (k is the row: staged row-major with
+// the LDS row stride ldb_t and read by the transpose loads).  Products run
+// as ah.bh (+ ah.bl for an fp32 B, + al.bh for an fp32 A).  One output side
+// is a LoRA rank (<= 64): 128 x 64 or 64 x 128 tiles, 4 waves, reduction
+// split over blocks with partial sums summed in a fixed order.
+struct DenseArgs {
+  int64_t M, N, K;
+  const void *A;  // A(m, k) at A[m lda + k] (ROWK) or A[k lda + m] (KROW)
+  int64_t lda;
+  const void *B;  // B(n, k) at B[n ldb + k] (ROWK) or B[k ldb + n] (KROW)
+  int64_t ldb;
+  float *C;
+  int64_t ldc;
+  float alpha;
+  int64_t split_stride;
+};
+
+// 32 rows (k) x R columns of a row-major matrix S[k][col] (ld), fp32 (XE = 1,
+// split) or bf16, into the transposed LDS layout (row stride ldb_t(R)).
+// Thread t (of T) holds EPT consecutive columns of row t / TPR; columns are
+// taken in groups of 8 (clim % 8 == 0, 16-byte aligned rows), zeroed at the
+// LDS write when out of range.
+template <int XE, int T, int R>
+struct KTile {
+  static constexpr int EPT = R * kBK / T;  // 8 or 16
+  static constexpr int TPR = R / EPT;
+  static constexpr int NG = EPT / 8;       // groups of 8 columns
+  static_assert(EPT == 8 || EPT == 16, "columns per thread");
+  static_assert(TPR * kBK == T, "one row per TPR threads");
+  float4 f[XE ? 2 * NG : 1];
+  uint4 b[XE ? 1 : NG];
+  uint32_t okm;
+  __device__ __forceinline__ void load(const void *S, int64_t ld, int64_t k0, int64_t klim,
+                                       int64_t c0, int64_t clim) {
+    const int t = threadIdx.x % T;
+    const int64_t k = k0 + t / TPR, c = c0 + (t % TPR) * EPT;
+    okm = 0;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      const bool ok = k < klim && c + 8 * q < clim;
+      const int64_t e = ok ? k * ld + c + 8 * q : 0;
+      if constexpr (XE) {
+        f[2 * q] = *(const float4 *)((const float *)S + e);
+        f[2 * q + 1] = *(const float4 *)((const float *)S + e + 4);
+      } else {
+        b[q] = *(const uint4 *)((const uint16_t *)S + e);
+      }
+      okm |= (uint32_t)ok << q;
+    }
+  }
+  __device__ __forceinline__ void store(uint16_t *Sh, uint16_t *Sl) const {
+    const int t = threadIdx.x % T;
+    const int o0 = (t / TPR) * ldb_t(R) + (t % TPR) * EPT;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      const bool ok = (okm >> q) & 1u;
+      if constexpr (XE) {
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 u0 = f[2 * q], u1 = f[2 * q + 1];
+        if (!ok) u0 = z, u1 = z;
+        uint32_t h[4], l[4];
+        split2(u0.x, u0.y, h[0], l[0]);
+        split2(u0.z, u0.w, h[1], l[1]);
+        split2(u1.x, u1.y, h[2], l[2]);
+        split2(u1.z, u1.w, h[3], l[3]);
+        *(uint4 *)(Sh + o0 + 8 * q) = make_uint4(h[0], h[1], h[2], h[3]);
+        *(uint4 *)(Sl + o0 + 8 * q) = make_uint4(l[0], l[1], l[2], l[3]);
+      } else {
+        uint4 v = b[q];
+        if (!ok) v = make_uint4(0, 0, 0, 0);
+        *(uint4 *)(Sh + o0 + 8 * q) = v;
+      }
+    }
+  }
+};
+
+// Elements of one operand stage: ROWK R x 32, KROW 32 x ldb_t(R).
+__host__ __device__ constexpr int dense_elems(int form, int R) {
+  return form == ROWK ? R * kBK : kBK * ldb_t(R);
+}
+
+template <class C, int AF, int BF, int XA, int XB>
+__global__ __launch_bounds__(C::T, 2) void k_dense_bf16(DenseArgs g, int tiles_n) {
+  constexpr int TM = C::TM, TN = C::TN, BM = C::BM, BN = C::BN;
+  constexpr int AE = dense_elems(AF, BM), BE = dense_elems(BF, BN);
+  constexpr int STAGE = 2 * AE + 2 * BE;
+  extern __shared__ __align__(16) uint16_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const int wm0 = (wave / C::WGN) * C::WTM, wn0 = (wave % C::WGN) * C::WTN;
+  const int nb = (int)gridDim.x;
+  int tb = (int)blockIdx.x;
+  if (nb % 8 == 0) tb = (tb % 8) * (nb / 8) + tb / 8;
+  const int64_t m0 = (int64_t)(tb / tiles_n) * BM, n0 = (int64_t)(tb % tiles_n) * BN;
+  const int z = (int)blockIdx.y, nz = (int)gridDim.y;
+
+  // operand tiles in registers: ROWK through the activation tile, KROW
+  // through KTile
+  using CA = Cfg<C::T, BM, 64>;
+  using CB = Cfg<C::T, BN, 64>;
+  using TA = typename std::conditional<AF == ROWK, ActTile<XA, CA>, KTile<XA, C::T, BM>>::type;
+  using TB = typename std::conditional<BF == ROWK, ActTile<XB, CB>, KTile<XB, C::T, BN>>::type;
+  struct Regs {
+    TA a;
+    TB b;
+  };
+  const int64_t steps = (g.K + kBK - 1) / kBK;
+  const int64_t t0 = steps * z / nz, t1 = steps * (z + 1) / nz;
+  auto load = [&](Regs &R, int64_t t) {
+    const int64_t k = t * kBK;
+    if constexpr (AF == ROWK) R.a.load(g.A, g.lda, m0, g.M, k, g.K);
+    else R.a.load(g.A, g.lda, k, g.K, m0, g.M);
+    if constexpr (BF == ROWK) R.b.load(g.B, g.ldb, n0, g.N, k, g.K);
+    else R.b.load(g.B, g.ldb, k, g.K, n0, g.N);
+  };
+  auto stage = [&](uint16_t *D, const Regs &R) {
+    R.a.store(D, D + AE);
+    R.b.store(D + 2 * AE, D + 2 * AE + BE);
+  };
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  // transposed layout: rows r0 .. r0 + 8 of column c0 + lane % 16 (see mma
+  // in k_nf4_bf16)
+  auto tr_operand = [&](const uint16_t *B, int ld, int r0, int c0) {
+    const int i = lane & 15;
+    const uint16_t *p = B + (r0 + (i >> 2)) * ld + c0 + 4 * (i & 3);
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)p);
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s *)(p + 4 * ld));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  };
+  auto operand = [&](const uint16_t *S, int form, int ld, int row0, int kk) {
+    if (form == ROWK) return *(const bf16x8_t *)(S + sw(row0 + l32, 2 * kk + h));
+    return tr_operand(S, ld, 16 * kk + 8 * h, row0 + 16 * ((lane >> 4) & 1));
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  auto mma = [&](const uint16_t *D) {
+    const uint16_t *Ah = D, *Al = D + AE, *Bh = D + 2 * AE, *Bl = D + 2 * AE + BE;
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      bf16x8_t ah[TM], al[TM], bh[TN], bl[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        ah[i] = operand(Ah, AF, ldb_t(BM), wm0 + 32 * i, kk);
+        if (XA) al[i] = operand(Al, AF, ldb_t(BM), wm0 + 32 * i, kk);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        bh[j] = operand(Bh, BF, ldb_t(BN), wn0 + 32 * j, kk);
+        if (XB) bl[j] = operand(Bl, BF, ldb_t(BN), wn0 + 32 * j, kk);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+          if (XB)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+          if (XA)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  };
+  if (t1 > t0) {
+    Regs R;
+    load(R, t0);
+    stage(smem, R);
+    __syncthreads();
+    for (int64_t t = t0; t < t1; ++t) {
+      const bool more = t + 1 < t1;
+      if (more) load(R, t + 1);
+      mma(smem + ((t - t0) & 1) * STAGE);
+      if (more) stage(smem + ((t + 1 - t0) & 1) * STAGE, R);
+      __syncthreads();
+    }
+  }
+  float *Cz = g.C + (nz > 1 ? (int64_t)z * g.split_stride : 0);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm0 + 32 * i + 8 * (v / 4) + 4 * h + (v % 4);
+        const int64_t n = n0 + wn0 + 32 * j + l32;
+        if (m < g.M && n < g.N) Cz[m * g.ldc + n] = g.alpha * acc[i][j][v];
+      }
+}
+
+using CfgD1 = Cfg<256, 128, 64>;  // N is the rank
+using CfgD2 = Cfg<256, 64, 128>;  // M is the rank
+
+template <class C, int AF, int BF, int XA, int XB>
+hipError_t run_dense(const DenseArgs &g0, int splits, float *partial, hipStream_t s) {
+  auto k = k_dense_bf16<C, AF, BF, XA, XB>;
+  constexpr uint32_t lds =
+      (uint32_t)(2 * (2 * dense_elems(AF, C::BM) + 2 * dense_elems(BF, C::BN)) * 2);
+  static bool attr = false;  // per instantiation
+  if (!attr) {
+    const hipError_t e =
+        hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  DenseArgs g = g0;
+  if (splits > 1) {
+    g.C = partial;
+    g.ldc = g.N;
+    g.split_stride = g.M * g.N;
+  }
+  const int tiles_n = (int)((g.N + C::BN - 1) / C::BN);
+  const int tiles_m = (int)((g.M + C::BM - 1) / C::BM);
+  hipError_t e = qh_launch(k, dim3((unsigned)(tiles_n * tiles_m), (unsigned)splits),
+                           dim3(C::T), lds, s, g, tiles_n);
+  if (e != hipSuccess || splits <= 1) return e;
+  return launch_reduce_splits(partial, splits, g.M, g.N, g0.C, g0.ldc, s);
+}
+
+template <class C, int AF, int BF>
+hipError_t dense_types(const DenseArgs &g, int xa, int xb, int splits, float *partial,
+                       hipStream_t s) {
+  if (xa && xb) return run_dense<C, AF, BF, 1, 1>(g, splits, partial, s);
+  if (xa) return run_dense<C, AF, BF, 1, 0>(g, splits, partial, s);
+  if (xb) return run_dense<C, AF, BF, 0, 1>(g, splits, partial, s);
+  return run_dense<C, AF, BF, 0, 0>(g, splits, partial, s);
+}
+
+// Block shape: the rank side gets the 64-wide tile side.
+bool dense_rank_n(int64_t M, int64_t N) { return N <= 64 || M > 64; }
+
+int dense_splits_for(int64_t M, int64_t N, int64_t K) {
+  const bool rn = dense_rank_n(M, N);
+  const int64_t tiles = ((M + (rn ? 127 : 63)) / (rn ? 128 : 64)) *
+                        ((N + (rn ? 63 : 127)) / (rn ? 64 : 128));
+  const int64_t steps = (K + kBK - 1) / kBK;
+  int64_t sp = (768 + tiles - 1) / (tiles ? tiles : 1);
+  if (sp > 16) sp = 16;
+  if (sp > steps / 8) sp = steps / 8;
+  while (sp > 1 && (size_t)(sp * M * N * 4) > ((size_t)64 << 20)) --sp;
+  return sp < 1 ? 1 : (int)sp;
+}
+
 }  // namespace
 
 // The bf16-MFMA path needs whole 64-element blocks per W row, and activation
@@ -785,6 +1039,44 @@ hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, int a_f32, int sp
                                    : pick_kind<ROWK, 0>(g, splits, partial, s);
   return a_f32 ? pick_kind<KROW, 1>(g, splits, partial, s)
                : pick_kind<KROW, 0>(g, splits, partial, s);
+}
+
+// Dense products of the LoRA rank on bf16 MFMA: row strides and the
+// contiguous dimensions multiples of 8, operands 16-byte aligned, one side of
+// the output at most 64.
+bool dense_bf16_ok(int64_t M, int64_t N, int64_t K, int a_form, const void *a, int64_t lda,
+                   int b_form, const void *b, int64_t ldb) {
+  auto al = [](const void *p) { return (((uintptr_t)p) & 15) == 0; };
+  if (M < 1 || N < 1 || K < 1 || (M > 64 && N > 64)) return false;
+  if (!al(a) || !al(b) || lda % 8 != 0 || ldb % 8 != 0) return false;
+  // the contiguous dimension of each operand is read in groups of 8
+  if ((a_form == ROWK ? K : M) % 8 != 0 || (b_form == ROWK ? K : N) % 8 != 0) return false;
+  return true;
+}
+
+int dense_bf16_splits(int64_t M, int64_t N, int64_t K) { return dense_splits_for(M, N, K); }
+
+hipError_t launch_dense_bf16(const void *a, int a_form, int a_f32, int64_t lda, const void *b,
+                             int b_form, int b_f32, int64_t ldb, float *c, int64_t ldc,
+                             int64_t M, int64_t N, int64_t K, float alpha, float *partial,
+                             hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  if (!dense_bf16_ok(M, N, K, a_form, a, lda, b_form, b, ldb)) return hipErrorInvalidValue;
+  const int splits = dense_splits_for(M, N, K);
+  if (splits > 1 && !partial) return hipErrorInvalidValue;
+  DenseArgs g{M, N, K, a, lda, b, ldb, c, ldc, alpha, 0};
+  const bool rn = dense_rank_n(M, N);
+#define QH_DENSE(C_)                                                                       \
+  if (a_form == ROWK && b_form == ROWK) return dense_types<C_, ROWK, ROWK>(g, a_f32, b_f32, splits, partial, s); \
+  if (a_form == ROWK) return dense_types<C_, ROWK, KROW>(g, a_f32, b_f32, splits, partial, s);                  \
+  if (b_form == ROWK) return dense_types<C_, KROW, ROWK>(g, a_f32, b_f32, splits, partial, s);                  \
+  return dense_types<C_, KROW, KROW>(g, a_f32, b_f32, splits, partial, s);
+  if (rn) {
+    QH_DENSE(CfgD1)
+  } else {
+    QH_DENSE(CfgD2)
+  }
+#undef QH_DENSE
 }
 
 }  // namespace qh

@@ -121,6 +121,18 @@ bool bf16_gemm_ok(const DevQW &w, const void *a, int64_t lda, int64_t K);
 int bf16_gemm_splits(int64_t M, int64_t N, int64_t K);
 hipError_t launch_gemm_bf16(const Bf16GemmArgs &g, int w_form, int a_f32, int splits,
                             float *partial, hipStream_t s);
+// Dense C = alpha sum_k A(m, k) B(n, k) on bf16 MFMA (fp32 operands as hi +
+// lo parts), one output side at most 64 (the LoRA-rank products T1, Ds,
+// grad_A, grad_B); A(m, k) at a[m lda + k] (ROWK) or a[k lda + m] (KROW), B
+// the same with n.  Splits > 1 need dense_bf16_splits(M, N, K) * M * N floats
+// of partial sums.
+bool dense_bf16_ok(int64_t M, int64_t N, int64_t K, int a_form, const void *a, int64_t lda,
+                   int b_form, const void *b, int64_t ldb);
+int dense_bf16_splits(int64_t M, int64_t N, int64_t K);
+hipError_t launch_dense_bf16(const void *a, int a_form, int a_f32, int64_t lda, const void *b,
+                             int b_form, int b_f32, int64_t ldb, float *c, int64_t ldc,
+                             int64_t M, int64_t N, int64_t K, float alpha, float *partial,
+                             hipStream_t s);
 
 // ---- k_quant.hip ----
 hipError_t launch_quantize(const float *w, int64_t n, int64_t bs, int dq,

@@ -404,6 +404,36 @@ size_t partial_floats(const GemmArgs &g) {
   return g.splits > 1 ? (size_t)g.splits * g.M * g.N : 0;
 }
 
+// A LoRA-rank product (T1, Ds, grad_A, grad_B) on the dense bf16-MFMA
+// kernel: C = alpha sum_k A(m, k) B(n, k), taken where the rank kernels'
+// reduction limit (2048) is passed and the operands allow it.
+struct DenseOp {
+  const void *a;
+  int af, a32;
+  int64_t lda;
+  const void *b;
+  int bf, b32;
+  int64_t ldb;
+  float *c;
+  int64_t ldc, M, N, K;
+  float alpha;
+  bool ok() const { return qh::dense_bf16_ok(M, N, K, af, a, lda, bf, b, ldb); }
+  size_t partial_bytes() const {
+    const int sp = qh::dense_bf16_splits(M, N, K);
+    return sp > 1 ? (size_t)sp * M * N * 4 : 0;
+  }
+  hipError_t run(float *partial, hipStream_t s) const {
+    return qh::launch_dense_bf16(a, af, a32, lda, b, bf, b32, ldb, c, ldc, M, N, K, alpha,
+                                 partial, s);
+  }
+};
+
+// T1 = X . A^T (M x r): X(m, k) along k, A(j, k) along k.
+DenseOp dense_t1(const void *x, int xe, int64_t M, int64_t K, const qh_lora *l, float *t1) {
+  return DenseOp{x, qh::ROWK, xe == qh::E_F32, K, l->a, qh::ROWK, 1, K, t1, (int64_t)l->r,
+                 M, (int64_t)l->r, K, 1.0f};
+}
+
 // T1 = X . A^T (M x r) on its own (lora.rs:94-97), for the shapes where no
 // GEMM follows it.
 void t1_dev(qh_ctx *ctx, const void *x, int xe, int64_t M, int64_t K, const qh_lora *l,
@@ -413,6 +443,14 @@ void t1_dev(qh_ctx *ctx, const void *x, int xe, int64_t M, int64_t K, const qh_l
     timed(ctx, "t1_gemm", s, [&] {
       return qh::launch_rank_gemm(x, xe == qh::E_BF16, K, l->a, 0, K, t1, r, M, K, r, 1.0f, s);
     });
+    return;
+  }
+  const DenseOp dt = dense_t1(x, xe, M, K, l, t1);
+  if (dt.ok()) {
+    Carve c;
+    size_t ip = c.add(dt.partial_bytes());
+    auto p = c.bind(ctx->scratch);
+    timed(ctx, "t1_gemm", s, [&] { return dt.run((float *)p[ip], s); });
     return;
   }
   GemmArgs g = gemm_args(M, r, K, op(x, K, qh::ROWK, xe), op(l->a, K, qh::ROWK, qh::E_F32),
@@ -529,10 +567,14 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
 
   GemmArgs gt1{}, gm{};
   const bool t1_rank = lora && qh::rank_gemm_ok(K, r);
+  DenseOp dt1{};
+  bool t1_dense = false;
   if (lora) {
     gt1 = gemm_args(M, r, K, op(x, K, qh::ROWK, xe), op(l->a, K, qh::ROWK, qh::E_F32),
                     nullptr, r, 1.0f);
-    gt1.splits = t1_rank ? 1 : choose_splits(M, r, K);
+    dt1 = dense_t1(x, xe, M, K, l, nullptr);
+    t1_dense = !t1_rank && dt1.ok();
+    gt1.splits = t1_rank || t1_dense ? 1 : choose_splits(M, r, K);
   }
   // NF4 weights in whole 64-element row blocks run on bf16 MFMA (the weight
   // as hi / lo bf16 parts); others on the fp32 tile engine
@@ -541,7 +583,7 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   Carve c;
   size_t i_t1 = c.add(lora && !t1_out ? (size_t)M * r * 4 : 0);
   size_t i_w32 = c.add(fast ? 0 : (size_t)W.n * 4);
-  size_t i_p1 = c.add(lora ? partial_floats(gt1) * 4 : 0);
+  size_t i_p1 = c.add(!lora ? 0 : t1_dense ? dt1.partial_bytes() : partial_floats(gt1) * 4);
   size_t i_p2 = c.add(y_splits > 1 ? (size_t)y_splits * M * N * 4 : 0);
   auto p = c.bind(ctx->scratch);
   float *t1 = lora ? (t1_out ? t1_out : (float *)p[i_t1]) : nullptr;
@@ -550,6 +592,9 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
     timed(ctx, "t1_gemm", s, [&] {
       return qh::launch_rank_gemm(x, xe == qh::E_BF16, K, l->a, 0, K, t1, r, M, K, r, 1.0f, s);
     });
+  } else if (lora && t1_dense) {
+    dt1.c = t1;
+    timed(ctx, "t1_gemm", s, [&] { return dt1.run((float *)p[i_p1], s); });
   } else if (lora) {
     gt1.C = t1;
     timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(gt1, (float *)p[i_p1], s); });
@@ -623,31 +668,50 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   GemmArgs gt1{}, gds{}, ggb{}, gga{};
   const bool t1_rank = lora && qh::rank_gemm_ok(K, r);
   const bool ds_rank = lora && qh::rank_gemm_ok(N, r);
+  const bool g_rank = lora && qh::rank_tgemm_ok(M, r);
+  // the dense bf16 kernel where the rank kernels do not reach
+  const int a32 = ae == qh::E_F32;
+  DenseOp dt1{}, dds{}, dgb{}, dga{};
+  bool t1_dense = false, ds_dense = false, gb_dense = false, ga_dense = false;
+  if (lora) {
+    dt1 = dense_t1(x, ae, M, K, l, nullptr);
+    // Ds = s dY . B: dY(m, n) along n, B(j, n) = B[n][j] across n
+    dds = DenseOp{dy, qh::ROWK, a32, N, l->b, qh::KROW, 1, r, nullptr, r, M, r, N, sc};
+    // grad_B = s dY^T . T1: dY(n, m) = dY[m][n] and T1(j, m) = T1[m][j], across m
+    // (T1 is the caller's t1_in or aligned scratch: the check sees which)
+    dgb = DenseOp{dy, qh::KROW, a32, N, t1_in, qh::KROW, 1, r, gb, r, N, r, M, sc};
+    // grad_A = Ds^T . X: Ds(j, m) = Ds[m][j] and X(k, m) = X[m][k], across m
+    dga = DenseOp{nullptr, qh::KROW, 1, r, x, qh::KROW, a32, K, ga, K, r, K, M, 1.0f};
+    t1_dense = !t1_in && !t1_rank && dt1.ok();
+    ds_dense = !ds_rank && dds.ok();
+    gb_dense = !g_rank && dgb.ok();
+    ga_dense = !g_rank && dga.ok();
+  }
   if (lora) {
     gt1 = gemm_args(M, r, K, op(x, K, qh::ROWK, ae), op(l->a, K, qh::ROWK, qh::E_F32),
                     nullptr, r, 1.0f);
-    gt1.splits = t1_rank ? 1 : choose_splits(M, r, K);
+    gt1.splits = t1_rank || t1_dense ? 1 : choose_splits(M, r, K);
     // Ds = s * dY . B   (qlora.rs:143,149)
     gds = gemm_args(M, r, N, op(dy, N, qh::ROWK, ae), op(l->b, r, qh::KROW, qh::E_F32),
                     nullptr, r, sc);
-    gds.splits = ds_rank ? 1 : choose_splits(M, r, N);
+    gds.splits = ds_rank || ds_dense ? 1 : choose_splits(M, r, N);
     // grad_B = (s * dY)^T . T1  (qlora.rs:147)
     ggb = gemm_args(N, r, M, op(dy, N, qh::KROW, ae), op(nullptr, r, qh::KROW, qh::E_F32),
                     gb, r, sc);
-    ggb.splits = choose_splits(N, r, M);
+    ggb.splits = g_rank || gb_dense ? 1 : choose_splits(N, r, M);
     // grad_A = Ds^T . X  (qlora.rs:151)
     gga = gemm_args(r, K, M, op(nullptr, r, qh::KROW, qh::E_F32), op(x, K, qh::KROW, ae),
                     ga, K, 1.0f);
-    gga.splits = choose_splits(r, K, M);
+    gga.splits = g_rank || ga_dense ? 1 : choose_splits(r, K, M);
   }
   Carve c;
   size_t i_t1 = c.add(lora && !t1_in ? (size_t)M * r * 4 : 0);
   size_t i_ds = c.add(lora ? (size_t)M * r * 4 : 0);
   size_t i_w32 = c.add(fast ? 0 : (size_t)W.n * 4);
-  size_t i_p1 = c.add(lora ? partial_floats(gt1) * 4 : 0);
-  size_t i_p2 = c.add(lora ? partial_floats(gds) * 4 : 0);
-  size_t i_p3 = c.add(lora ? partial_floats(ggb) * 4 : 0);
-  size_t i_p4 = c.add(lora ? partial_floats(gga) * 4 : 0);
+  size_t i_p1 = c.add(!lora ? 0 : t1_dense ? dt1.partial_bytes() : partial_floats(gt1) * 4);
+  size_t i_p2 = c.add(!lora ? 0 : ds_dense ? dds.partial_bytes() : partial_floats(gds) * 4);
+  size_t i_p3 = c.add(!lora ? 0 : gb_dense ? dgb.partial_bytes() : partial_floats(ggb) * 4);
+  size_t i_p4 = c.add(!lora ? 0 : ga_dense ? dga.partial_bytes() : partial_floats(gga) * 4);
   const bool bf16 = fast && qh::bf16_gemm_ok(W, dy, N, N);
   const int gx_splits = bf16 ? qh::bf16_gemm_splits(M, K, N) : base_splits(M, K, N);
   size_t i_p5 = c.add(gx_splits > 1 ? (size_t)gx_splits * M * K * 4 : 0);
@@ -670,6 +734,10 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
                                     s);
       });
       t1 = t1w;
+    } else if (t1_dense) {
+      dt1.c = (float *)p[i_t1];
+      timed(ctx, "t1_gemm", s, [&] { return dt1.run((float *)p[i_p1], s); });
+      t1 = dt1.c;
     } else {
       gt1.C = (float *)p[i_t1];
       timed(ctx, "t1_gemm", s, [&] { return qh::launch_gemm(gt1, (float *)p[i_p1], s); });
@@ -680,11 +748,14 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
       timed(ctx, "ds_gemm", s, [&] {
         return qh::launch_rank_gemm(dy, ae == qh::E_BF16, N, l->b, 1, r, ds, r, M, N, r, sc, s);
       });
+    } else if (ds_dense) {
+      dds.c = ds;
+      timed(ctx, "ds_gemm", s, [&] { return dds.run((float *)p[i_p2], s); });
     } else {
       gds.C = ds;
       timed(ctx, "ds_gemm", s, [&] { return qh::launch_gemm(gds, (float *)p[i_p2], s); });
     }
-    if (qh::rank_tgemm_ok(M, r)) {
+    if (g_rank) {
       // grad_B (N x r) = s dY^T T1, grad_A (r x K) = Ds^T X
       timed(ctx, "grad_b_gemm", s, [&] {
         return qh::launch_rank_tgemm(dy, ae == qh::E_BF16, N, t1, r, gb, r, 0, M, N, r, sc, s);
@@ -693,10 +764,20 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
         return qh::launch_rank_tgemm(x, ae == qh::E_BF16, K, ds, r, ga, K, 1, M, K, r, 1.0f, s);
       });
     } else {
-      ggb.B.p = t1;
-      timed(ctx, "grad_b_gemm", s, [&] { return qh::launch_gemm(ggb, (float *)p[i_p3], s); });
-      gga.A.p = ds;
-      timed(ctx, "grad_a_gemm", s, [&] { return qh::launch_gemm(gga, (float *)p[i_p4], s); });
+      if (gb_dense) {
+        dgb.b = t1;
+        timed(ctx, "grad_b_gemm", s, [&] { return dgb.run((float *)p[i_p3], s); });
+      } else {
+        ggb.B.p = t1;
+        timed(ctx, "grad_b_gemm", s, [&] { return qh::launch_gemm(ggb, (float *)p[i_p3], s); });
+      }
+      if (ga_dense) {
+        dga.a = ds;
+        timed(ctx, "grad_a_gemm", s, [&] { return dga.run((float *)p[i_p4], s); });
+      } else {
+        gga.A.p = ds;
+        timed(ctx, "grad_a_gemm", s, [&] { return qh::launch_gemm(gga, (float *)p[i_p4], s); });
+      }
     }
   }
   if (bf16) {
