@@ -267,11 +267,12 @@ def test_noalloc_backward_checks_before_any_launch():
     f = L.qh_qlora_backward_dev_noalloc
     assert f(None, C.byref(w), C.byref(lora), bp, bp, 0, 8, None, bp, None, bp, None) == 1
     assert _err(L) == "shape mismatch: grad_a is NULL but holds 4096 elements"
-    # 300000 tokens at r = 64: T1 and Ds (2 x 76.8 MB) plus the split-K
-    # partials of grad_A and grad_B (2 x 32 splits x 64 x 64 floats)
+    # 300000 tokens at r = 64: T1 and Ds (2 x 76.8 MB) plus the split
+    # reduction partials of grad_A and grad_B on the dense bf16 kernel
+    # (2 x 16 splits x 64 x 64 floats)
     assert f(None, C.byref(w), C.byref(lora), bp, bp, 0, 300000, None, bp, bp, bp,
              None) == 2
-    assert _err(L) == ("invalid config: the call needs 154648576 bytes of scratch but the "
+    assert _err(L) == ("invalid config: the call needs 154124288 bytes of scratch but the "
                        f"allocation-free backward has {_lib.QH_NOALLOC_SCRATCH_BYTES}")
     # within the region: reaches the context check (a GPU error without one)
     assert f(None, C.byref(w), C.byref(lora), bp, bp, 0, 8, None, bp, bp, bp, None) == 3
