@@ -668,7 +668,9 @@ void backward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
   GemmArgs gt1{}, gds{}, ggb{}, gga{};
   const bool t1_rank = lora && qh::rank_gemm_ok(K, r);
   const bool ds_rank = lora && qh::rank_gemm_ok(N, r);
-  const bool g_rank = lora && qh::rank_tgemm_ok(M, r);
+  // (grad_A / grad_B of wide layers go to the dense kernel even within the
+  // rank kernel's token limit: measured faster from 8192 features up)
+  const bool g_rank = lora && qh::rank_tgemm_ok(M, r) && std::max(N, K) < 8192;
   // the dense bf16 kernel where the rank kernels do not reach
   const int a32 = ae == qh::E_F32;
   DenseOp dt1{}, dds{}, dgb{}, dga{};
