@@ -240,7 +240,7 @@ QH_API qh_status qh_qlora_forward_dev(qh_ctx *ctx, const qh_qweight *w,
  * adapter).  No counterpart in the reference, whose forward takes one layer
  * per call (qlora-wgpu/src/kernels.rs:262-296): at batch 1, consecutive
  * layers that the one-launch decode kernel serves run in pairs, one launch
- * per pair (no kernel boundary between them, one codebook table), as in a
+ * per pair (the two layers' workgroups side by side on every CU), as in a
  * decoder block's independent projections (q / k / v, gate / up) or two
  * layers of a decode step.  Arguments are validated for every layer before
  * any launch. */
