@@ -399,3 +399,39 @@ def test_two_layer_launch_recompute_and_fallbacks(ctx, QD):
     torch.cuda.synchronize()
     for y, r_ in zip(ys, yr):
         assert torch.equal(y, r_)
+
+
+@pytest.mark.parametrize("batch", [4, 16])
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_group_batches_share_one_t1_launch(ctx, QD, batch, act):
+    """At batches of 3-16 a group computes every stream layer's T1 in one
+    launch: y and T1 are the bits of per-layer calls, with and without the
+    caller's T1 buffers, and a layer without an adapter keeps its own path."""
+    _say(f"group T1 launch batch={batch} act={act}")
+    dev = torch.device("cuda:0")
+    shapes = [(11008, 4096, 16), (4096, 11008, 16), (4096, 4096, 8), (2048, 4096, 0)]
+    Ls = [_layer(QD, ctx, N, K, r, SEED ^ (0x91 + i), act) for i, (N, K, r) in enumerate(shapes)]
+    g = torch.Generator(device="cpu").manual_seed(SEED + batch)
+    for L in Ls:
+        L["tx"] = torch.randn(batch, L["K"], generator=g).to(dev).to(act)
+    ref = []
+    for L in Ls:
+        y = torch.empty(batch, L["N"], device=dev)
+        t1 = torch.empty(batch, max(L["r"], 1), device=dev)
+        QD.forward(L["W"], L["lora"], L["tx"], batch, y, t1=t1 if L["r"] else None, ctx=ctx)
+        ref.append((y, t1))
+    for with_t1 in (True, False):
+        outs = [(torch.full((batch, L["N"]), float("nan"), device=dev),
+                 torch.full((batch, max(L["r"], 1)), float("nan"), device=dev)) for L in Ls]
+        ctx.set_timing(True)
+        ctx.timing_report(reset=True)
+        QD.forward_group([(L["W"], L["lora"], L["tx"], y, t1 if (with_t1 and L["r"]) else None)
+                          for L, (y, t1) in zip(Ls, outs)], batch, ctx=ctx)
+        torch.cuda.synchronize()
+        rep = ctx.timing_report(reset=True)
+        ctx.set_timing(False)
+        assert rep["decode_stream_t1"][0] == 1, rep
+        for (y, t1), (yr, t1r), L in zip(outs, ref, Ls):
+            assert torch.equal(y, yr), (with_t1, L["N"], L["K"])
+            if with_t1 and L["r"]:
+                assert torch.equal(t1, t1r)

@@ -198,11 +198,11 @@ __global__ __launch_bounds__(256) void k_gemv(DevQW w, const void *__restrict__ 
 // one output; loads are issued in unconditional batches of 8 per thread
 // (clamped index, zero weight).  Needs K % 4 == 0 and 16-byte aligned rows.
 template <int XBF16>
-__global__ __launch_bounds__(256) void k_lora_t1(const void *__restrict__ x, int64_t K,
-                                                 const float *__restrict__ a, int r,
-                                                 float *__restrict__ t1) {
-  __shared__ float red[4];
-  const int j = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+__device__ __forceinline__ void lora_t1_out(const void *__restrict__ x, int64_t K,
+                                            const float *__restrict__ a, int r,
+                                            float *__restrict__ t1, const int j, const int m,
+                                            float *red) {
+  const int tid = threadIdx.x;
   const int64_t nk4 = K >> 2;
   const float4 *a4 = (const float4 *)(a + (int64_t)j * K);
   float s = 0.0f;
@@ -240,6 +240,24 @@ __global__ __launch_bounds__(256) void k_lora_t1(const void *__restrict__ x, int
   if (tid == 0) t1[m * r + j] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+template <int XBF16>
+__global__ __launch_bounds__(256) void k_lora_t1(const void *__restrict__ x, int64_t K,
+                                                 const float *__restrict__ a, int r,
+                                                 float *__restrict__ t1) {
+  __shared__ float red[4];
+  lora_t1_out<XBF16>(x, K, a, r, t1, (int)blockIdx.x, (int)blockIdx.y, red);
+}
+
+// Several layers' T1 in one launch (grid z = job, the same instructions per
+// output as k_lora_t1, so the same bits).
+template <int XBF16>
+__global__ __launch_bounds__(256) void k_lora_t1_jobs(T1Jobs jobs) {
+  __shared__ float red[4];
+  const T1Job &q = jobs.j[blockIdx.z];
+  if ((int)blockIdx.x >= q.r) return;  // block-uniform: before any barrier
+  lora_t1_out<XBF16>(q.x, q.K, q.a, q.r, q.t1, (int)blockIdx.x, (int)blockIdx.y, red);
+}
+
 template <int M, int XB>
 hipError_t run_gemv(const DevQW &w, const void *x, const float *t1, const float *lb,
                     int64_t r, float s, float *y, hipStream_t st) {
@@ -269,6 +287,17 @@ hipError_t launch_lora_t1(const void *x, int x_bf16, int64_t M, int64_t K, const
   const dim3 grid((unsigned)r, (unsigned)M);
   if (x_bf16) return qh_launch(k_lora_t1<1>, grid, dim3(256), 0, st, x, K, a, (int)r, t1);
   return qh_launch(k_lora_t1<0>, grid, dim3(256), 0, st, x, K, a, (int)r, t1);
+}
+
+hipError_t launch_lora_t1_jobs(const T1Jobs &jobs, int x_bf16, int64_t M, hipStream_t st) {
+  if (M == 0 || jobs.count == 0) return hipSuccess;
+  if (jobs.count > kMaxT1Jobs) return hipErrorInvalidValue;
+  int rmax = 0;
+  for (int i = 0; i < jobs.count; ++i) rmax = jobs.j[i].r > rmax ? jobs.j[i].r : rmax;
+  if (rmax == 0) return hipSuccess;
+  const dim3 grid((unsigned)rmax, (unsigned)M, (unsigned)jobs.count);
+  if (x_bf16) return qh_launch(k_lora_t1_jobs<1>, grid, dim3(256), 0, st, jobs);
+  return qh_launch(k_lora_t1_jobs<0>, grid, dim3(256), 0, st, jobs);
 }
 
 hipError_t launch_gemv(const DevQW &w, const void *x, int x_bf16, int64_t M,

@@ -164,6 +164,21 @@ bool gemv_ok(const DevQW &w, int64_t M);
 // T1 = X A^T for the GEMV path (K % 4 == 0, 16-byte aligned rows).
 hipError_t launch_lora_t1(const void *x, int x_bf16, int64_t M, int64_t K, const float *a,
                           int64_t r, float *t1, hipStream_t st);
+// The T1 of several layers with the same batch in one launch (per layer
+// x: M x K, a: r x K, t1: M x r; the bits of launch_lora_t1).
+constexpr int kMaxT1Jobs = 8;
+struct T1Job {
+  const void *x;
+  const float *a;
+  float *t1;
+  int64_t K;
+  int r;
+};
+struct T1Jobs {
+  T1Job j[kMaxT1Jobs];
+  int count;
+};
+hipError_t launch_lora_t1_jobs(const T1Jobs &jobs, int x_bf16, int64_t M, hipStream_t st);
 
 // ---- k_decode.hip ----
 // Decode path (batch <= 16): X split into MFMA fragments + T1 (prep), then

@@ -1433,7 +1433,54 @@ qh_status qh_qlora_forward_group_dev(qh_ctx *ctx, size_t count, const qh_qweight
     hipStream_t s = pick_stream(ctx, stream);
     const int xb = x_dtype == QH_BF16;
     const bool force = (ctx->test_flags & QH_TEST_FORCE_T1_RECOMPUTE) != 0;
+    std::vector<char> done(count, 0);
+    if (batch >= 3 && batch <= 16) {
+      // Batches of 3-16 on the one-launch decode kernel take T1 from a
+      // launch before theirs: the adapters' T1 of all such layers in one
+      // launch (the caller's T1 buffer where given, else scratch), then each
+      // layer's weight-stream launches.
+      const int64_t M = (int64_t)batch;
+      std::vector<size_t> idx;
+      for (size_t i = 0; i < count; ++i) {
+        const qh_lora *l = loras ? loras[i] : nullptr;
+        if (l && takes_stream(make_devqw(ws[i]), l, d_xs[i], M)) idx.push_back(i);
+      }
+      if (idx.size() >= 2) {
+        Carve c;
+        std::vector<size_t> slot(idx.size());
+        for (size_t q = 0; q < idx.size(); ++q)
+          slot[q] = c.add(d_t1s && d_t1s[idx[q]] ? 0 : (size_t)M * loras[idx[q]]->r * 4);
+        auto p = c.bind(ctx->scratch);
+        std::vector<float *> t1(idx.size());
+        for (size_t q = 0; q < idx.size(); ++q)
+          t1[q] = d_t1s && d_t1s[idx[q]] ? d_t1s[idx[q]] : (float *)p[slot[q]];
+        for (size_t q0 = 0; q0 < idx.size(); q0 += qh::kMaxT1Jobs) {
+          qh::T1Jobs jobs{};
+          jobs.count = (int)std::min<size_t>(qh::kMaxT1Jobs, idx.size() - q0);
+          for (int q = 0; q < jobs.count; ++q) {
+            const size_t i = idx[q0 + q];
+            jobs.j[q] = qh::T1Job{d_xs[i], loras[i]->a, t1[q0 + q], (int64_t)ws[i].cols,
+                                  (int)loras[i]->r};
+          }
+          timed(ctx, "decode_stream_t1", s,
+                [&] { return qh::launch_lora_t1_jobs(jobs, xb, M, s); });
+        }
+        for (size_t q = 0; q < idx.size(); ++q) {
+          const size_t i = idx[q];
+          const qh_lora *l = loras[i];
+          const DevQW W = make_devqw(ws[i]);
+          for (int64_t m0 = 0; m0 < M; m0 += qh::decode_stream_chunk(M))
+            timed(ctx, "decode_stream", s, [&] {
+              return qh::launch_decode_stream(W, d_xs[i], xb, M, m0, l->a, (int64_t)l->r, l->b,
+                                              l->alpha / (float)l->r, d_ys[i], t1[q],
+                                              ctx->tickets, force, s);
+            });
+          done[i] = 1;
+        }
+      }
+    }
     for (size_t i = 0; i < count; ++i) {
+      if (done[i]) continue;
       const qh_lora *l1 = loras ? loras[i] : nullptr;
       float *t1o1 = d_t1s ? d_t1s[i] : nullptr;
       const DevQW W1 = make_devqw(ws[i]);
