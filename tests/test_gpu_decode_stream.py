@@ -13,7 +13,9 @@ kernel launched just before and run one launch per 8 rows: their tests
 cover chunking, ragged rows, ranks 0-64, both scale stores and repeatability
 next to batch-1 calls.  The path a workgroup takes when published T1
 slices never arrive (it recomputes them) is forced from the host and must
-give the same bits.  Every call checks from the context's kernel timing
+give the same bits.  Batch 2 past the producer's register limit (long
+rows, larger ranks) runs like the wider batches: T1 first, then the 4-row
+template with 2 rows.  Every call checks from the context's kernel timing
 that k_dstream ran.
 """
 import numpy as np
@@ -73,10 +75,14 @@ def test_stream_parity(ctx, QD, N, K):
             _say(f"stream N={N} K={K} M={M} act={act}")
             xa = bf16_round(x) if act == torch.bfloat16 else x
             y, t1, rep = _forward(QD, ctx, W, lora, torch.from_numpy(xa).to(dev).to(act), M, N, r)
-            # batch 2 takes the one-launch kernel where its T1 slices fit a
-            # producer lane's registers, else the two-kernel path
-            if M == 1:
+            # batch 2 computes T1 in the launch where its slices fit a
+            # producer lane's registers, else in a launch just before (at
+            # 14336 rows that needs 4 tiles per workgroup of the 4-row
+            # template, not compiled: the two-kernel path runs)
+            if M == 1 or N != 14336:
                 assert "decode_stream" in rep, rep
+            else:
+                assert "decode_small" in rep, rep
             tol = TOL_F32 if act == torch.float32 else TOL_BF16
             yo = O.qlora_forward(wd, N, K, a, b, r, alpha, xa, M)
             e = nerr(y.cpu().numpy().ravel(), yo, K, xa, wd)
@@ -100,12 +106,13 @@ def test_stream_f32_scales_no_adapter(ctx, QD):
     assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
 
 
-@pytest.mark.parametrize("M,r,stream", [(1, 64, False), (2, 32, False), (2, 64, False),
+@pytest.mark.parametrize("M,r,stream", [(1, 64, False), (2, 32, True), (2, 64, True),
                                         (1, 1, True), (1, 5, True), (1, 16, True), (2, 8, True)])
 def test_stream_ranks(ctx, QD, M, r, stream):
     # small adapters run in one launch; where the T1 slices would not fit
-    # the producer's registers (batch * r of 64 and more at this shape) the
-    # two-kernel path runs, with the same result
+    # the producer's registers (batch * r of 64 and more at this shape)
+    # batch 2 takes T1 from a launch before its weight stream and batch 1
+    # the two-kernel path, with the same result
     N, K, alpha = 4096, 4096, 16.0
     g = O.Rng(SEED ^ (100 + 7 * r + M))
     w = g.normal(N * K, 0.02)
@@ -401,12 +408,13 @@ def test_two_layer_launch_recompute_and_fallbacks(ctx, QD):
         assert torch.equal(y, r_)
 
 
-@pytest.mark.parametrize("batch", [4, 16])
+@pytest.mark.parametrize("batch", [2, 4, 16])
 @pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
 def test_group_batches_share_one_t1_launch(ctx, QD, batch, act):
-    """At batches of 3-16 a group computes every stream layer's T1 in one
-    launch: y and T1 are the bits of per-layer calls, with and without the
-    caller's T1 buffers, and a layer without an adapter keeps its own path."""
+    """At batches of 3-16 (and 2, for the layers whose launch cannot
+    compute T1) a group computes those stream layers' T1 in one launch: y
+    and T1 are the bits of per-layer calls, with and without the caller's
+    T1 buffers, and the other layers keep their own path."""
     _say(f"group T1 launch batch={batch} act={act}")
     dev = torch.device("cuda:0")
     shapes = [(11008, 4096, 16), (4096, 11008, 16), (4096, 4096, 8), (2048, 4096, 0)]

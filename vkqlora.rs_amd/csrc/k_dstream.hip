@@ -117,36 +117,41 @@ __device__ __forceinline__ void regroup(const LineRegs &L, uint32_t (&sw)[8]) {
 
 // X fragments are stored with the (P_ab, P_ab, P_cd, P_cd) repetition the
 // interleaved B operand needs (16 bytes, read straight into the A operand)
-// for batch 1; wider batches store (P_ab, P_cd) and repeat the dwords in
-// registers.
+// for batch 1, units ordered (step, half, row, group).  Wider batches store
+// (P_ab, P_cd) and repeat the dwords in registers, units ordered (step,
+// row, group, half): one 16-byte read per step gives both K halves (two
+// 8-byte reads would be merged by the compiler into one instruction issued
+// behind the table lookups, whose wait then covers all of them).
 template <int M>
 struct FragOf {
   static constexpr bool kDup = M == 1;
   static constexpr uint32_t kUnit = kDup ? 16 : 8;  // bytes per (step, half, row, group)
   static constexpr uint32_t kLine = 16 * 2 * M * 4 * kUnit;
+  // byte offset of unit (step s, half p, A row ro, lane group g)
+  static __device__ __forceinline__ uint32_t off(int s, int p, int ro, int g) {
+    return kDup ? (uint32_t)((s * 2 + p) * 2 * M * 4 + ro * 4 + g) * kUnit
+                : (uint32_t)(((s * 2 * M * 4 + ro * 4 + g) * 2 + p)) * kUnit;
+  }
 };
 
 // LDS operands of one MFMA step (two K=32 halves p) for R tiles.
 template <int R>
 struct StepOps {
-  v4u xa[2];    // A operands
+  v4u xa[2];    // A operands (8-byte units: xa[0] holds both halves' units)
   v2u e[R][4];  // table entries: bytes 2p, 2p+1 of the step's dword
 };
 
+// xo = A row * 4 + lane group
 template <int M, int R>
 __device__ __forceinline__ void fetch_step(StepOps<R> &o, const uint32_t (&sw)[R][8], int s,
                                            uint32_t xf, int xo, uint32_t lo8) {
-  constexpr int M2 = 2 * M;
   typedef FragOf<M> F;
+  // 8-byte units: the dwords are repeated where the MFMA is issued, so the
+  // register copies do not wait for this read
+  if (!F::kDup) o.xa[0] = *LDS_AT(const lds_u4, xf + F::off(s, 0, xo >> 2, xo & 3));
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const uint32_t a = xf + (uint32_t)((s * 2 + p) * M2 * 4 + xo) * F::kUnit;
-    if (F::kDup) {
-      o.xa[p] = *LDS_AT(const lds_u4, a);
-    } else {
-      const v2u q = *LDS_AT(const lds_u2, a);
-      o.xa[p] = v4u{q.x, q.x, q.y, q.y};
-    }
+    if (F::kDup) o.xa[p] = *LDS_AT(const lds_u4, xf + F::off(s, p, xo >> 2, xo & 3));
 #pragma unroll
     for (int t = 0; t < R; ++t) {
       o.e[t][2 * p] = *LDS_AT(const lds_u2, tab_addr(sw[t][s], lo8, 2 * p));
@@ -155,11 +160,14 @@ __device__ __forceinline__ void fetch_step(StepOps<R> &o, const uint32_t (&sw)[R
   }
 }
 
-template <int R>
+template <int M, int R>
 __device__ __forceinline__ void mfma_step(const StepOps<R> &o, floatx4 (&d)[R]) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const bf16x8 av = __builtin_bit_cast(bf16x8, o.xa[p]);
+    const v4u q = o.xa[0];
+    const v4u a = FragOf<M>::kDup ? o.xa[p]
+                                  : (p == 0 ? v4u{q.x, q.x, q.y, q.y} : v4u{q.z, q.z, q.w, q.w});
+    const bf16x8 av = __builtin_bit_cast(bf16x8, a);
 #pragma unroll
     for (int t = 0; t < R; ++t) {
       const v2u e0 = o.e[t][2 * p], e1 = o.e[t][2 * p + 1];
@@ -271,8 +279,10 @@ __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// the lane's unit: step us, half up, lane group ug (rows m and M + m)
 template <int XBF16, int M>
-__device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base, int ug) {
+__device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t xf, int us, int up,
+                                            int ug) {
   typedef FragOf<M> F;
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -284,8 +294,8 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t base
       l23 = bf16_pair(xv[m].z - __uint_as_float(h23 << 16),
                       xv[m].w - __uint_as_float(h23 & 0xffff0000u));
     }
-    const uint32_t ah = base + (uint32_t)(m * 4 + ug) * F::kUnit;
-    const uint32_t al = base + (uint32_t)((M + m) * 4 + ug) * F::kUnit;
+    const uint32_t ah = xf + F::off(us, up, m, ug);
+    const uint32_t al = xf + F::off(us, up, M + m, ug);
     if (F::kDup) {
       *LDS_AT(lds_u4, ah) = v4u{h01, h01, h23, h23};
       *LDS_AT(lds_u4, al) = v4u{l01, l01, l23, l23};
@@ -612,7 +622,6 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   // fragments are written after every read of line kk - 1's (a wave's LDS
   // operations complete in order).
   auto xfrag = [&](int) { return o_x + (uint32_t)wave * kFragLine; };
-  const uint32_t xunit = (uint32_t)(us * 2 + up) * M2 * 4 * FragOf<M>::kUnit;
   {
     const uint32_t lo8 = (uint32_t)(lane & 31) * 8u;
     const int xo = (nl < M2 ? nl : M2 - 1) * 4 + g;
@@ -643,7 +652,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
     // step is fetched, before the next line's are regrouped
     uint32_t sw[R][8];
     StepOps<R> ops[D + 1];
-    write_frags<XBF16, M>(xv[0], xfrag(0) + xunit, ug);
+    write_frags<XBF16, M>(xv[0], xfrag(0), us, up, ug);
 #pragma unroll
     for (int t = 0; t < R; ++t) regroup(L[0][t], sw[t]);
 #pragma unroll
@@ -661,7 +670,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
       if (f < NS) {
         const int fk = f / 8, fs = f % 8;
         if (fs == 0) {
-          write_frags<XBF16, M>(xv[fk], xfrag(fk) + xunit, ug);
+          write_frags<XBF16, M>(xv[fk], xfrag(fk), us, up, ug);
 #pragma unroll
           for (int t = 0; t < R; ++t) regroup(L[fk][t], sw[t]);
         }
@@ -671,7 +680,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
 #pragma unroll
         for (int t = 0; t < R; ++t) d[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       }
-      mfma_step<R>(ops[i % (D + 1)], d);
+      mfma_step<M, R>(ops[i % (D + 1)], d);
       if (s & 1) {  // block j = s / 2 of line kk is complete
         const int j = s >> 1, kl = slot_line(kk), vj = kk / KLW;
         const float valid = kk % KLW < nklv[vj] ? 1.0f : 0.0f;
@@ -942,9 +951,9 @@ bool shape_compiled(int R, int KLW, int Mt) {
   return false;
 }
 
-// Template rows of a launch of mact rows (the wider templates take the
-// rows in chunks of 8, the last one padded).
-int stream_rows(int64_t M, int64_t mact) { return M <= 2 ? (int)M : (mact <= 4 ? 4 : 8); }
+// Template rows of a launch of mact rows that takes T1 from an earlier
+// launch (rows in chunks of 8, the last one padded).
+int stream_rows(int64_t mact) { return mact <= 4 ? 4 : 8; }
 
 // Plan of one launch of mact rows (<= 8) with template rows Mt, in
 // workgroups of LW waves (kLW, or kLW / 2 for the side-by-side layer pair:
@@ -1139,13 +1148,20 @@ hipError_t launch_decode_stream2(const DevQW &w1, const void *x1, const float *a
                       : dispatch_pair<0, 1>(p1, p2, L1, L2, st);
 }
 
+bool decode_stream_t1_in(const DevQW &w, int64_t M, int64_t r) {
+  return M >= 1 && M <= 2 && stream_plan(w, (int)M, (int)M, r).ok;
+}
+
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r) {
   if (M < 1 || M > kStreamMaxRows) return false;
-  if (M <= 2) return stream_plan(w, (int)M, (int)M, r).ok;
-  // every chunk of 8 rows (the last one possibly narrower) must fit
+  if (decode_stream_t1_in(w, M, r)) return true;
+  // batch 1 only with T1 in the launch; batch 2 and wider batches take T1
+  // from launch_decode_stream_t1, and every chunk of 8 rows (the last one
+  // possibly narrower) must fit
+  if (M == 1) return false;
   for (int64_t m0 = 0; m0 < M; m0 += 8) {
     const int mact = (int)std::min<int64_t>(8, M - m0);
-    if (!stream_plan(w, stream_rows(M, mact), mact, r).ok) return false;
+    if (!stream_plan(w, stream_rows(mact), mact, r).ok) return false;
   }
   return true;
 }
@@ -1161,7 +1177,7 @@ float *stream_t1(float *t1_out, unsigned *tickets) {
 hipError_t launch_decode_stream_t1(const DevQW &w, const void *x, int x_bf16, int64_t M,
                                    const float *a, int64_t r, float *t1_out, unsigned *tickets,
                                    hipStream_t st) {
-  if (M <= 2 || r == 0) return hipSuccess;  // batches of 1-2 compute T1 in the GEMV launch
+  if (r == 0 || decode_stream_t1_in(w, M, r)) return hipSuccess;  // T1 in the GEMV launch
   return launch_lora_t1(x, x_bf16, M, w.cols, a, r, stream_t1(t1_out, tickets), st);
 }
 
@@ -1174,7 +1190,7 @@ hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64
   uint64_t *epochs = (uint64_t *)(tickets + kStreamEpochWord);
   uint64_t *t1w = (uint64_t *)(tickets + kTicketWords);
   const int ri = (int)r;
-  if (M <= 2) {
+  if (decode_stream_t1_in(w, M, r)) {
     StreamPlan p = stream_plan(w, (int)M, (int)M, r);
     // Tests force the path a workgroup takes when published T1 slices never
     // arrive (it must give the same bits).
@@ -1182,10 +1198,11 @@ hipError_t launch_decode_stream(const DevQW &w, const void *x, int x_bf16, int64
     if (M == 1) return dispatch_rows<1>(x_bf16, w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st);
     return dispatch_rows<2>(x_bf16, w, x, a, ri, lb, s, t1w, epochs, t1_out, y, p, st);
   }
-  // Rows [m0, m0 + 8) of a wider batch, T1 from launch_decode_stream_t1.
+  // Rows [m0, m0 + 8) of a wider batch (or batch 2 whose T1 slices do not
+  // fit a producer lane), T1 from launch_decode_stream_t1.
   const int64_t N = w.rows, K = w.cols;
   const int mact = (int)std::min<int64_t>(8, M - m0);
-  const int Mt = stream_rows(M, mact);
+  const int Mt = stream_rows(mact);
   StreamPlan p = stream_plan(w, Mt, mact, r);
   p.sa.t1ext = r > 0 ? stream_t1(t1_out, tickets) + m0 * r : nullptr;
   const void *xm = x_bf16 ? (const void *)((const uint16_t *)x + m0 * K)

@@ -232,10 +232,14 @@ hipError_t launch_decode_stream2(const DevQW &w1, const void *x1, const float *a
                                  int x_bf16, unsigned *tickets, bool force_t1_recompute,
                                  hipStream_t st);
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r);
+// True when the weight-stream launch computes T1 itself (batches of 1-2
+// whose T1 slices fit a producer lane's registers).
+bool decode_stream_t1_in(const DevQW &w, int64_t M, int64_t r);
 // Rows per launch (M for batches of 1-2, else 8).
 int64_t decode_stream_chunk(int64_t M);
-// Batches of 3-16 rows: T1 = X A^T into t1_out (or the tickets' T1 words),
-// before the row launches; nothing for 1-2 rows.
+// Batches whose launch does not compute T1 (3-16 rows, and 2 rows past the
+// producer limit): T1 = X A^T into t1_out (or the tickets' T1 words),
+// before the row launches; nothing otherwise.
 hipError_t launch_decode_stream_t1(const DevQW &w, const void *x, int x_bf16, int64_t M,
                                    const float *a, int64_t r, float *t1_out, unsigned *tickets,
                                    hipStream_t st);

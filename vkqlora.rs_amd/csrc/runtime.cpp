@@ -520,7 +520,7 @@ void forward_dev(qh_ctx *ctx, const DevQW &W, const qh_lora *l, const void *x,
 
   if (decode && qh::decode_stream_ok(W, M, r)) {
     const int xb = xe == qh::E_BF16;
-    if (M > 2 && lora)
+    if (lora && !qh::decode_stream_t1_in(W, M, r))
       timed(ctx, "decode_stream_t1", s, [&] {
         return qh::launch_decode_stream_t1(W, x, xb, M, l->a, r, t1_out, ctx->tickets, s);
       });
@@ -1434,16 +1434,19 @@ qh_status qh_qlora_forward_group_dev(qh_ctx *ctx, size_t count, const qh_qweight
     const int xb = x_dtype == QH_BF16;
     const bool force = (ctx->test_flags & QH_TEST_FORCE_T1_RECOMPUTE) != 0;
     std::vector<char> done(count, 0);
-    if (batch >= 3 && batch <= 16) {
-      // Batches of 3-16 on the one-launch decode kernel take T1 from a
-      // launch before theirs: the adapters' T1 of all such layers in one
-      // launch (the caller's T1 buffer where given, else scratch), then each
-      // layer's weight-stream launches.
+    if (batch >= 2 && batch <= 16) {
+      // Batches on the one-launch decode kernel that take T1 from a launch
+      // before theirs (3-16 rows, and 2 rows past the in-launch limit): the
+      // adapters' T1 of all such layers in one launch (the caller's T1
+      // buffer where given, else scratch), then each layer's weight-stream
+      // launches.
       const int64_t M = (int64_t)batch;
       std::vector<size_t> idx;
       for (size_t i = 0; i < count; ++i) {
         const qh_lora *l = loras ? loras[i] : nullptr;
-        if (l && takes_stream(make_devqw(ws[i]), l, d_xs[i], M)) idx.push_back(i);
+        const DevQW W = make_devqw(ws[i]);
+        if (l && takes_stream(W, l, d_xs[i], M) && !qh::decode_stream_t1_in(W, M, (int64_t)l->r))
+          idx.push_back(i);
       }
       if (idx.size() >= 2) {
         Carve c;
