@@ -46,6 +46,7 @@
 // quant decode c*(absmax/127) is within 1 ulp of quant.rs:218's
 // fl(fl(c/127)*absmax) and only enters this sum, never a stored weight.
 #include <algorithm>
+#include <cstdint>
 
 #include "decode_common.h"
 
@@ -184,7 +185,6 @@ struct StreamArgs {
   int r16;     // r rounded up to a multiple of 16
   int lps;     // log2 of the lanes per A row in a slice
   float inv_r;  // 1 / r (1 when r = 0)
-  int mact;    // rows of X in this launch (<= M; the rest repeat the last)
   const float *t1ext;  // batches of 4 and 8: T1 (mact x r), computed before
   int t1_fallback;     // set by tests: every workgroup computes all T1 slices
 };
@@ -325,16 +325,18 @@ __device__ __forceinline__ void write_frags(const float4 (&xv)[M], uint32_t xf, 
 // wave; after B2 the recomputed T1 slices, P MRp floats) | lbs (16 R r16
 // floats) | red (kLW R 16 M floats) | t1s (64 floats, M r16 used) | flag,
 // epoch | per-wave T1 partial sums (kLW MRp floats).
-// The weight's pointers, X and the shape lead the arguments: the first 16
-// argument dwords arrive preloaded in SGPRs (no kernel-argument load before
-// the first code line goes out).
+// The weight's pointers, X, the shape and the row count lead the
+// arguments: the first 16 argument dwords arrive preloaded in SGPRs (no
+// kernel-argument load before the first code line goes out).
 // One layer's share of workgroup c (of the layer's G workgroups), in a
-// workgroup of LW waves.
+// workgroup of LW waves.  mact: rows of X in this launch (<= M, the rest
+// repeat the last; M itself when T1 is computed in the launch).
 template <int XBF16, int KIND, int M, int R, int KLW, int LW = kLW>
 __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
                                              const void *__restrict__ scales,
                                              const float *__restrict__ absmax,
                                              const void *__restrict__ x, int64_t N, int64_t K,
+                                             const int mact_arg,
                                              const float *__restrict__ a, int r,
                                              const float *__restrict__ lb, float s_lora,
                                              uint64_t *__restrict__ t1w,
@@ -356,6 +358,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   // sa.t1ext for 4 and 8 (their slices would not fit a producer lane)
   constexpr bool kT1In = M <= 2;
   constexpr int kT1Floats = kT1In ? 64 : 64 * M;  // T1 in LDS: M r16 <= this
+  const int mact = kT1In ? M : mact_arg;
   constexpr uint32_t kFragLine = FragOf<M>::kLine;  // bytes of X fragments per K-line
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar line indices
@@ -404,7 +407,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
     const int kl = slot_line(kk);
 #pragma unroll
     for (int m = 0; m < M; ++m)
-      xv[kk][m] = load_x4<XBF16>(x, (int64_t)(m < sa.mact ? m : sa.mact - 1) * K +
+      xv[kk][m] = load_x4<XBF16>(x, (int64_t)(m < mact ? m : mact - 1) * K +
                                         (int64_t)kl * kLine + koff);
 #pragma unroll
     for (int t = 0; t < R; ++t) load_line<KIND>(L[kk][t], w, nrow[t], KB, crow[t], kl, g);
@@ -421,11 +424,16 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
   // absmax (first used at line 0's first block scale) and, in wave 0, the
   // launch epoch
   float am0[R], am1[R];
+  // K-lines below klb[t] share line klf's absmax group (am0), the rest
+  // line kll's (am1): group(kl) = (n KB + 4 kl) >> 8
+  int klb[R];
   if (KIND == 1) {
 #pragma unroll
     for (int t = 0; t < R; ++t) {
-      am0[t] = w.absmax[(nrow[t] * KB + 4 * klf) >> 8];
+      const int64_t b0 = nrow[t] * KB + 4 * klf;
+      am0[t] = w.absmax[b0 >> 8];
       am1[t] = w.absmax[(nrow[t] * KB + 4 * kll) >> 8];
+      klb[t] = klf + (int)((((b0 >> 8) + 1) * 256 - b0 + 3) / 4);
     }
   }
   uint64_t ev = 0;  // the epoch counter word (epoch = ev / 16)
@@ -562,7 +570,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
           tpv[j][q] = ld_dev64(t1w + (tpi(j, q) >= 0 ? tpi(j, q) : 0));
     } else {
       // rows past mact read row mact - 1's (their outputs are not stored)
-      const int mr = sa.mact * (r > 0 ? r : 1);
+      const int mr = mact * (r > 0 ? r : 1);
       const float *tp = r > 0 ? sa.t1ext : lbp;
       t1v = tp[tid < mr ? tid : mr - 1];
     }
@@ -626,6 +634,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
     const uint32_t lo8 = (uint32_t)(lane & 31) * 8u;
     const int xo = (nl < M2 ? nl : M2 - 1) * 4 + g;
     floatx4 acc[R];  // the current K-line slice's sums
+    float lf[R];     // the current line's scale factor per tile
 #pragma unroll
     for (int t = 0; t < R; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     // Batches of 1-2: lane (nl, g) holds D rows 4g..4g+3 of column nl, y_m =
@@ -682,29 +691,35 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
       }
       mfma_step<M, R>(ops[i % (D + 1)], d);
       if (s & 1) {  // block j = s / 2 of line kk is complete
-        const int j = s >> 1, kl = slot_line(kk), vj = kk / KLW;
-        const float valid = kk % KLW < nklv[vj] ? 1.0f : 0.0f;
+        const int j = s >> 1, vj = kk / KLW;
+        if (j == 0) {
+          // the line's factor: 0 for a spare slot; KIND 1 also the absmax
+          // of the line's group / 127 (a 256-block group spans 64 K-lines:
+          // a wave's lines see at most two)
+          const float valid = kk % KLW < nklv[vj] ? 1.0f : 0.0f;
+          const int kl = slot_line(kk);
+#pragma unroll
+          for (int t = 0; t < R; ++t)
+            lf[t] = KIND == 0 ? valid : (kl < klb[t] ? am0[t] : am1[t]) * (1.0f / 127.0f) * valid;
+        }
 #pragma unroll
         for (int t = 0; t < R; ++t) {
           float sc;
           if (KIND == 0) {
             const LineRegs &Lr = L[kk][t];
             sc = __uint_as_float(j == 0 ? Lr.sf.x : j == 1 ? Lr.sf.y : j == 2 ? Lr.sf.z : Lr.sf.w) *
-                 valid;
+                 lf[t];
           } else {
-            // a 256-block absmax group spans 64 K-lines: a wave's lines see
-            // at most two groups
-            const float amax = ((nrow[t] * KB + 4 * kl) >> 8) == ((nrow[t] * KB + 4 * klf) >> 8)
-                                   ? am0[t]
-                                   : am1[t];
-            sc = (float)(int8_t)((L[kk][t].sf.x >> (8 * j)) & 255u) *
-                 (amax * (1.0f / 127.0f) * valid);
+            sc = (float)(int8_t)((L[kk][t].sf.x >> (8 * j)) & 255u) * lf[t];
           }
-          // only D rows < 2M carry output
+          // only D rows < 2M carry output; kept here, not sunk past the
+          // loop into the lanes that store them
 #pragma unroll
-          for (int v = 0; v < (M2 < 4 ? M2 : 4); ++v) acc[t][v] = fmaf(sc, d[t][v], acc[t][v]);
-          // here, not sunk past the loop into the lanes that store it
-          asm volatile("" : "+v"(acc[t]));
+          for (int v = 0; v < (M2 < 4 ? M2 : 4); ++v) {
+            float a = fmaf(sc, d[t][v], acc[t][v]);
+            asm volatile("" : "+v"(a));
+            acc[t][v] = a;
+          }
         }
         if constexpr (M <= 2)
           if (s == 7 && kk % KLW == KLW - 1 && vj < VPW - 1) {
@@ -856,7 +871,7 @@ __device__ __forceinline__ void stream_layer(const uint8_t *__restrict__ codes,
       }
       sum = fmaf(s_lora, (l[0] + l[1]) + (l[2] + l[3]), sum);
     }
-    if (n < N && m < sa.mact) y[(int64_t)m * N + n] = sum;
+    if (n < N && m < mact) y[(int64_t)m * N + n] = sum;
   }
 }
 
@@ -865,24 +880,23 @@ __global__ __launch_bounds__(kThreads) void k_dstream(const uint8_t *__restrict_
                                                       const void *__restrict__ scales,
                                                       const float *__restrict__ absmax,
                                                       const void *__restrict__ x, int64_t N,
-                                                      int64_t K, const float *__restrict__ a,
-                                                      int r,
+                                                      int64_t K, int mact,
+                                                      const float *__restrict__ a, int r,
                                                       const float *__restrict__ lb,
                                                       float s_lora, uint64_t *__restrict__ t1w,
                                                       uint64_t *__restrict__ epochs,
                                                       float *__restrict__ t1_out,
                                                       float *__restrict__ y, StreamArgs sa) {
-  stream_layer<XBF16, KIND, M, R, KLW>(codes, scales, absmax, x, N, K, a, r, lb, s_lora, t1w,
-                                       epochs, t1_out, y, sa, (int)blockIdx.x, (int)gridDim.x);
+  stream_layer<XBF16, KIND, M, R, KLW>(codes, scales, absmax, x, N, K, mact, a, r, lb, s_lora,
+                                       t1w, epochs, t1_out, y, sa, (int)blockIdx.x,
+                                       (int)gridDim.x);
 }
 
-// One layer of a two-layer launch: its arguments and its workgroup count.
-struct StreamLayer {
-  const uint8_t *codes;
-  const void *scales;
+// The arguments of one layer of a two-layer launch that its workgroups do
+// not need before their first code line (the kernel's leading scalar
+// arguments, preloaded in SGPRs, carry the rest).
+struct StreamTail {
   const float *absmax;
-  const void *x;
-  int64_t N, K;
   const float *a;
   int r;
   const float *lb;
@@ -890,7 +904,6 @@ struct StreamLayer {
   uint64_t *t1w, *epochs;  // the layer's own T1 words and launch counters
   float *t1_out, *y;
   StreamArgs sa;
-  int G;
 };
 
 // Two independent layers (batch 1) side by side: workgroups [0, G1) run the
@@ -898,23 +911,35 @@ struct StreamLayer {
 // a CU's LDS, so that a CU streams one workgroup of each layer at once: one
 // ramp and one tail for both weight streams.  Each layer's bits are those of
 // its 8-wave launch (the 4-wave workgroup plays the 8-wave K split).
+// The weights' pointers, X and the shapes (14 dwords: rows < 2^16 and
+// K-lines of the two layers packed in one dword each) lead the arguments
+// and arrive preloaded in SGPRs; the split point G1 = ceil(tiles / R1) is
+// the host plan's workgroup count of the first layer.
 template <int XBF16, int KIND, int R1, int KLW1, int R2, int KLW2>
-__global__ __launch_bounds__(kThreads / 2, 2) void k_dstream2(StreamLayer L1, StreamLayer L2) {
+__global__ __launch_bounds__(kThreads / 2, 2) void k_dstream2(
+    const uint8_t *__restrict__ codes1, const void *__restrict__ scales1,
+    const void *__restrict__ x1, const uint8_t *__restrict__ codes2,
+    const void *__restrict__ scales2, const void *__restrict__ x2, uint32_t rows12,
+    uint32_t klines12, StreamTail L1, StreamTail L2) {
   const int c = (int)blockIdx.x;
-  if (c < L1.G)
-    stream_layer<XBF16, KIND, 1, R1, KLW1, kLW / 2>(L1.codes, L1.scales, L1.absmax, L1.x, L1.N,
-                                                    L1.K, L1.a, L1.r, L1.lb, L1.s_lora, L1.t1w,
-                                                    L1.epochs, L1.t1_out, L1.y, L1.sa, c, L1.G);
+  const int N1 = (int)(rows12 & 0xffffu), N2 = (int)(rows12 >> 16);
+  const int K1 = (int)(klines12 & 0xffffu) * kLine, K2 = (int)(klines12 >> 16) * kLine;
+  const int G1 = (((N1 + 15) >> 4) + R1 - 1) / R1;
+  if (c < G1)
+    stream_layer<XBF16, KIND, 1, R1, KLW1, kLW / 2>(codes1, scales1, L1.absmax, x1, N1, K1, 1,
+                                                    L1.a, L1.r, L1.lb, L1.s_lora, L1.t1w,
+                                                    L1.epochs, L1.t1_out, L1.y, L1.sa, c, G1);
   else
-    stream_layer<XBF16, KIND, 1, R2, KLW2, kLW / 2>(L2.codes, L2.scales, L2.absmax, L2.x, L2.N,
-                                                    L2.K, L2.a, L2.r, L2.lb, L2.s_lora, L2.t1w,
-                                                    L2.epochs, L2.t1_out, L2.y, L2.sa, c - L1.G,
-                                                    L2.G);
+    stream_layer<XBF16, KIND, 1, R2, KLW2, kLW / 2>(codes2, scales2, L2.absmax, x2, N2, K2, 1,
+                                                    L2.a, L2.r, L2.lb, L2.s_lora, L2.t1w,
+                                                    L2.epochs, L2.t1_out, L2.y, L2.sa, c - G1,
+                                                    (int)gridDim.x - G1);
 }
 
 // ---- host side --------------------------------------------------------------
 struct StreamPlan {
   int R = 0, KLW = 0, G = 0;
+  int mact = 0;  // rows of X in the launch
   uint32_t lds = 0;
   StreamArgs sa{};
   bool ok = false;
@@ -964,6 +989,7 @@ StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r, int LW = kLW
   const int64_t r16 = (r + 15) & ~(int64_t)15;
   const bool t1in = Mt <= 2;
   if (cus <= 0 || mact < 1 || mact > Mt || r < 0 || r > 64 || (t1in && Mt * r16 > 64)) return p;
+  if (t1in && mact != Mt) return p;  // the kernel takes mact = M for these
   if (w.bs != 64 || w.cols % kLine != 0 || w.cols >= (int64_t)1 << 24) return p;
   if ((((uintptr_t)w.codes) & 15) != 0) return p;
   if (w.kind == 0 ? (((uintptr_t)w.scales) & 15) != 0 : (((uintptr_t)w.scale_codes) & 3) != 0)
@@ -1000,7 +1026,7 @@ StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r, int LW = kLW
   p.sa.r16 = (int)r16;
   p.sa.lps = r > 0 ? 63 - __builtin_clzll((unsigned long long)(64 / r)) : 0;
   p.sa.inv_r = r > 0 ? 1.0f / (float)r : 1.0f;
-  p.sa.mact = mact;
+  p.mact = mact;
   p.sa.t1ext = nullptr;
   p.sa.t1_fallback = 0;
   p.R = (int)R;
@@ -1026,7 +1052,7 @@ hipError_t run_stream(const DevQW &w, const void *x, const float *a, int r, cons
   }
   const void *sc = KIND == 0 ? (const void *)w.scales : (const void *)w.scale_codes;
   return qh_launch(k, dim3((unsigned)p.G), dim3(kThreads), p.lds, st, w.codes, sc, w.absmax, x,
-                   w.rows, w.cols, a, r, lb, s, t1w, epochs, t1_out, y, p.sa);
+                   w.rows, w.cols, p.mact, a, r, lb, s, t1w, epochs, t1_out, y, p.sa);
 }
 
 template <int XBF16, int KIND, int M>
@@ -1067,31 +1093,40 @@ bool pair_compiled(int R1, int KLW1, int R2, int KLW2) {
   return false;
 }
 
-StreamLayer layer_of(const DevQW &w, const void *x, const float *a, int64_t r, const float *lb,
-                     float s, uint64_t *t1w, uint64_t *epochs, float *t1_out, float *y,
-                     const StreamPlan &p) {
-  StreamLayer L;
+// One layer of a two-layer launch on the host side.
+struct PairLayer {
+  const uint8_t *codes;
+  const void *scales;
+  const void *x;
+  int N, K, G;
+  StreamTail t;
+};
+
+PairLayer layer_of(const DevQW &w, const void *x, const float *a, int64_t r, const float *lb,
+                   float s, uint64_t *t1w, uint64_t *epochs, float *t1_out, float *y,
+                   const StreamPlan &p) {
+  PairLayer L;
   L.codes = w.codes;
   L.scales = w.kind == 0 ? (const void *)w.scales : (const void *)w.scale_codes;
-  L.absmax = w.absmax;
   L.x = x;
-  L.N = w.rows;
-  L.K = w.cols;
-  L.a = a;
-  L.r = (int)r;
-  L.lb = lb;
-  L.s_lora = s;
-  L.t1w = t1w;
-  L.epochs = epochs;
-  L.t1_out = t1_out;
-  L.y = y;
-  L.sa = p.sa;
+  L.N = (int)w.rows;
+  L.K = (int)w.cols;
   L.G = p.G;
+  L.t.absmax = w.absmax;
+  L.t.a = a;
+  L.t.r = (int)r;
+  L.t.lb = lb;
+  L.t.s_lora = s;
+  L.t.t1w = t1w;
+  L.t.epochs = epochs;
+  L.t.t1_out = t1_out;
+  L.t.y = y;
+  L.t.sa = p.sa;
   return L;
 }
 
 template <int XBF16, int KIND, int R1, int KLW1, int R2, int KLW2>
-hipError_t run_stream2(const StreamLayer &L1, const StreamLayer &L2, uint32_t lds,
+hipError_t run_stream2(const PairLayer &L1, const PairLayer &L2, uint32_t lds,
                        hipStream_t st) {
   auto k = k_dstream2<XBF16, KIND, R1, KLW1, R2, KLW2>;
   static bool attr = false;  // per instantiation; the attribute is per function
@@ -1102,12 +1137,17 @@ hipError_t run_stream2(const StreamLayer &L1, const StreamLayer &L2, uint32_t ld
     if (e != hipSuccess) return e;
     attr = true;
   }
-  return qh_launch(k, dim3((unsigned)(L1.G + L2.G)), dim3(kThreads / 2), lds, st, L1, L2);
+  // the kernel derives the first layer's workgroup count from N1 and R1
+  if (L1.G != ((L1.N + 15) / 16 + R1 - 1) / R1) return hipErrorInvalidValue;
+  return qh_launch(k, dim3((unsigned)(L1.G + L2.G)), dim3(kThreads / 2), lds, st, L1.codes,
+                   L1.scales, L1.x, L2.codes, L2.scales, L2.x,
+                   (uint32_t)L1.N | (uint32_t)L2.N << 16,
+                   (uint32_t)(L1.K / kLine) | (uint32_t)(L2.K / kLine) << 16, L1.t, L2.t);
 }
 
 template <int XBF16, int KIND>
-hipError_t dispatch_pair(const StreamPlan &p1, const StreamPlan &p2, const StreamLayer &L1,
-                         const StreamLayer &L2, hipStream_t st) {
+hipError_t dispatch_pair(const StreamPlan &p1, const StreamPlan &p2, const PairLayer &L1,
+                         const PairLayer &L2, hipStream_t st) {
   const uint32_t lds = std::max(p1.lds, p2.lds);
 #define QH_PAIR_CASE(a, b, c, d)                                          \
   if (p1.R == a && p1.KLW == b && p2.R == c && p2.KLW == d)               \
@@ -1120,7 +1160,10 @@ hipError_t dispatch_pair(const StreamPlan &p1, const StreamPlan &p2, const Strea
 }  // namespace
 
 bool decode_stream2_ok(const DevQW &w1, int64_t r1, const DevQW &w2, int64_t r2) {
-  if (w1.kind != w2.kind) return false;
+  // rows and K-lines of both layers travel packed in 16 bits each
+  if (w1.kind != w2.kind || w1.rows > 0xffff || w2.rows > 0xffff || w1.cols / kLine > 0xffff ||
+      w2.cols / kLine > 0xffff)
+    return false;
   const StreamPlan p1 = stream_plan(w1, 1, 1, r1, kLW / 2), p2 = stream_plan(w2, 1, 1, r2, kLW / 2);
   return p1.ok && p2.ok && pair_compiled(p1.R, p1.KLW, p2.R, p2.KLW);
 }
@@ -1140,8 +1183,8 @@ hipError_t launch_decode_stream2(const DevQW &w1, const void *x1, const float *a
   uint64_t *w1t = (uint64_t *)(tickets + kTicketWords);
   uint64_t *e2 = (uint64_t *)(tickets + kStreamSlot2Word);
   uint64_t *w2t = (uint64_t *)(tickets + kStreamSlot2Word + 32);
-  const StreamLayer L1 = layer_of(w1, x1, a1, r1, lb1, s1, w1t, e1, t1_out1, y1, p1);
-  const StreamLayer L2 = layer_of(w2, x2, a2, r2, lb2, s2, w2t, e2, t1_out2, y2, p2);
+  const PairLayer L1 = layer_of(w1, x1, a1, r1, lb1, s1, w1t, e1, t1_out1, y1, p1);
+  const PairLayer L2 = layer_of(w2, x2, a2, r2, lb2, s2, w2t, e2, t1_out2, y2, p2);
   if (x_bf16) return w1.kind == 0 ? dispatch_pair<1, 0>(p1, p2, L1, L2, st)
                                   : dispatch_pair<1, 1>(p1, p2, L1, L2, st);
   return w1.kind == 0 ? dispatch_pair<0, 0>(p1, p2, L1, L2, st)
