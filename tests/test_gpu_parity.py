@@ -256,6 +256,52 @@ def test_adam_wave_kernel_block_sizes_ragged_and_misaligned(ctx, block_size, big
                 assert _same_bits(sg[key], so[key]), (misaligned, i, key)
 
 
+@pytest.mark.parametrize("block_size", [256, 1024])
+def test_adam_wave_kernel_special_values(ctx, block_size):
+    """Device path, bit-exact against the oracle on blocks whose variance is
+    zero (zero gradient and state), tiny (below 2^-96, subnormal squares)
+    or overflowing to inf (one step: the state then holds inf scales), next
+    to ordinary blocks: the wave kernel's cheaper root and reciprocals hand
+    such blocks to the library-math path, and both must give the
+    reference's bits."""
+    import ctypes as C
+    import torch
+    _say(f"adam special values block_size={block_size}")
+    n = block_size * 6
+    g = O.Rng(SEED ^ 0x5EC1A1)
+
+    def grads(huge):
+        gr = g.normal(n, 0.01)
+        b = block_size
+        gr[:b] = 0.0                                   # zero variance
+        gr[b:2 * b] = g.normal(b, 1e-30)               # var ~ 1e-63: below 2^-96
+        gr[2 * b:3 * b] = g.normal(b, 1e-44)           # subnormal gradients
+        gr[3 * b + 5] = 0.0                            # one zero in a normal block
+        if huge:
+            gr[4 * b:5 * b] = g.normal(b, 1e20)        # g * g overflows to inf
+        return gr.astype(np.float32)
+
+    for steps, huge in ((3, False), (1, True)):
+        p_np = g.normal(n, 0.05)
+        p_dev = torch.from_numpy(p_np).cuda()
+        og = QH.Adam8bit(lr=1e-3, block_size=block_size, ctx=ctx)
+        oo = O.Adam8bit(lr=1e-3, block_size=block_size)
+        for step in range(steps):
+            gr = grads(huge)
+            g_dev = torch.from_numpy(gr).cuda()
+            pp = (C.c_void_p * 1)(p_dev.data_ptr())
+            gp = (C.c_void_p * 1)(g_dev.data_ptr())
+            ll = (C.c_size_t * 1)(n)
+            st = QH._lib.AdamStats()
+            QH._lib.check(ctx.lib.qh_adam8bit_step_dev(og.h, pp, gp, ll, 1, C.byref(st), None))
+            oo.step([p_np], [gr])
+            torch.cuda.synchronize()
+            assert _same_bits(p_dev.cpu().numpy(), p_np), (huge, step)
+        sg, so = og.state(0, n), oo.state(0, n)
+        for key in ("m_codes", "m_scales", "v_codes", "v_scales"):
+            assert _same_bits(sg[key], so[key]), (huge, key)
+
+
 def test_adam_reference_behaviour(ctx):
     # tests/optim.rs:62-131 through the GPU path
     g = np.array([((i * 7) % 43) / 43 - 0.5 for i in range(256)], np.float32)

@@ -15,12 +15,16 @@
 //    [4l, 4l + 4) of every 256-element chunk of its block: one float4 load
 //    of p and of g and one u32 load of the m and of the v codes per chunk.
 //    The new m and v stay in registers; the block absmax is a wave
-//    reduction (max is exact, so its order does not matter); the codes are
-//    stored as u32.  No LDS and no workgroup barrier.  Divisions by 127, by
-//    b1t and b2t and by the block absmax are double products with the
-//    divisor's reciprocal rounded once to float (`div_by`: the IEEE float
-//    quotient bit for bit); the one division by a per-element value stays a
-//    float division.
+//    reduction (max is exact, so its order does not matter: DPP within
+//    rows of 16 lanes, then the four row maxima as scalars); the codes are
+//    stored as u32.  Divisions by b1t and b2t and by the block absmax are
+//    double products with the divisor's reciprocal rounded once to float
+//    (`div_by`: the IEEE float quotient bit for bit); code / 127 comes from
+//    a 256-entry LDS table of IEEE quotients; the square roots are the
+//    hardware root plus an exact rounding test (`sqrt_cr`), taken when no
+//    variance of the block is below 2^-96 (else the block runs the
+//    IEEE-library path, same bits); the one division by a per-element value
+//    stays a float division.  The only barrier is the table's, at entry.
 //  * k_adam (any other block size or alignment): one workgroup per block,
 //    one element per thread, m and v staged in LDS.
 #include "qh_internal.h"
@@ -88,6 +92,62 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Max over the 64 lanes of a full wave: DPP within each row of 16 lanes
+// (swap 1, swap 2, rotate 4, rotate 8), then the four row maxima read into
+// scalars.  Every lane must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF,
+                                                              0xF, false)));
+}
+__device__ __forceinline__ float wave_max_full(float v) {
+  v = dpp_max<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_max<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_max<0x124>(v);  // row_ror 4
+  v = dpp_max<0x128>(v);  // row_ror 8
+  const int b = __float_as_int(v);
+  return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)),
+                     __int_as_float(__builtin_amdgcn_readlane(b, 16))),
+               fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)),
+                     __int_as_float(__builtin_amdgcn_readlane(b, 48))));
+}
+
+// sqrt(x) correctly rounded, for x >= 2^-96, +inf or NaN.  The hardware
+// root s is within 1 ulp, so the result is s_dn = s - ulp, s or s_up = s + ulp.
+// sqrt(x) lies below the midpoint (s_dn + s) / 2 iff x < s_dn * s + ulp^2 / 4,
+// and x - s_dn * s is a multiple of a grid far coarser than ulp^2 / 4 (x is a
+// float near s^2), so the test is x - s_dn * s <= 0, whose sign one fma gives
+// exactly; likewise above (s + s_up) / 2 iff x - s_up * s > 0.  (At x = inf
+// both residuals are NaN and s = inf stands.)
+__device__ __forceinline__ float sqrt_cr(float x) {
+  const float s = __builtin_amdgcn_sqrtf(x);
+  const float dn = __int_as_float(__float_as_int(s) - 1);
+  const float up = __int_as_float(__float_as_int(s) + 1);
+  float r = s;
+  if (__builtin_fmaf(-dn, s, x) <= 0.0f) r = dn;
+  if (__builtin_fmaf(-up, s, x) > 0.0f) r = up;
+  return r;
+}
+
+// round-half-away-from-zero of |t| <= 127 as an int8 code byte (NaN -> 0):
+// t + copysign(0.5, t) is exact in double and the conversion truncates.
+__device__ __forceinline__ uint32_t q8_round(float t) {
+  const double td = (double)t;
+  const int c = (int)(td + __builtin_copysign(0.5, td));
+  return t == t ? (uint32_t)(c & 0xFF) : 0u;
+}
+
+// 1 / (double)a for a > 0, a finite float, within 2^-51 relative (what
+// `div_by` needs): the hardware reciprocal (within 2^-23) and two Newton
+// steps, each of which squares the relative error.
+__device__ __forceinline__ double inv_f64(float a) {
+  const double d = (double)a;
+  double y = __builtin_amdgcn_rcp(d);
+  y = __builtin_fma(__builtin_fma(-d, y, 1.0), y, y);
+  y = __builtin_fma(__builtin_fma(-d, y, 1.0), y, y);
+  return y;
+}
+
 // The tensor of global block gb (wave-uniform: gb is).
 __device__ __forceinline__ int tensor_of(const AdamBatch &B, int64_t gb) {
   int ti = 0;
@@ -130,8 +190,10 @@ __device__ __forceinline__ void load_block(BlockRegs<NC> &R, const AdamBatch &B,
   }
 }
 
+// The update of one block with the math library's square root and the
+// shuffle reduction: any block length, any values.
 template <int NC>
-__device__ __forceinline__ void update_block(const BlockRegs<NC> &R, const Upd &u0, int lane) {
+__device__ __forceinline__ void update_block_lib(const BlockRegs<NC> &R, const Upd &u0, int lane) {
   const AdamTensor &T = R.T;
   Upd u = u0;
   u.b1t = T.b1t;
@@ -202,6 +264,78 @@ __device__ __forceinline__ void update_block(const BlockRegs<NC> &R, const Upd &
   }
 }
 
+// The update of one full block (len = 256 NC) through the cheaper exact
+// operations; a block with a variance below 2^-96 (where the hardware root
+// loses its 1-ulp bound) goes to update_block_lib instead: same bits.
+// `tab[c]` = (int8)c / 127 as IEEE float quotients.
+template <int NC>
+__device__ __forceinline__ void update_block(const BlockRegs<NC> &R, const Upd &u0, int lane,
+                                             const float *tab) {
+  if (R.len != 256 * NC) {
+    update_block_lib<NC>(R, u0, lane);
+    return;
+  }
+  const AdamTensor &T = R.T;
+  float m[NC][4], var[NC][4], vh[NC][4];
+  bool tiny = false;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float gg[4] = {R.g4[c].x, R.g4[c].y, R.g4[c].z, R.g4[c].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float mo = tab[(R.mc[c] >> (8 * e)) & 0xFF] * R.ms;
+      const float vo = tab[(R.vc[c] >> (8 * e)) & 0xFF] * R.vs;
+      // optim.rs:229-232, in the reference's operation order
+      m[c][e] = u0.beta1 * mo + u0.one_m_b1 * gg[e];
+      var[c][e] = u0.beta2 * vo * vo + u0.one_m_b2 * gg[e] * gg[e];
+      vh[c][e] = div_by(var[c][e], T.inv_b2t);
+      // below 2^-96 (zero included), not NaN
+      tiny |= (!(var[c][e] >= 0x1p-96f) && var[c][e] == var[c][e]) ||
+              (!(vh[c][e] >= 0x1p-96f) && vh[c][e] == vh[c][e]);
+    }
+  }
+  if (__builtin_amdgcn_ballot_w64(tiny) != 0) {
+    update_block_lib<NC>(R, u0, lane);
+    return;
+  }
+  float v[NC][4];
+  float am = 0.0f, av = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    float pp[4] = {R.p4[c].x, R.p4[c].y, R.p4[c].z, R.p4[c].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[c][e] = sqrt_cr(var[c][e]);
+      const float mh = div_by(m[c][e], T.inv_b1t);
+      pp[e] = pp[e] - u0.lr * mh / (sqrt_cr(vh[c][e]) + u0.eps);
+      am = fmaxf(am, fabsf(m[c][e]));
+      av = fmaxf(av, fabsf(v[c][e]));
+    }
+    *(float4 *)(T.p + R.s + 256 * c + 4 * lane) = make_float4(pp[0], pp[1], pp[2], pp[3]);
+  }
+  am = wave_max_full(am);
+  av = wave_max_full(av);
+  // a zero absmax quantizes to 0 (optim.rs:86-88); x / inf is 0 (or NaN for inf)
+  const double iam = am == 0.0f ? 1.0 : (__builtin_isinf(am) ? 0.0 : inv_f64(am));
+  const double iav = av == 0.0f ? 1.0 : (__builtin_isinf(av) ? 0.0 : inv_f64(av));
+  const uint32_t mz = am != 0.0f ? 0xFFFFFFFFu : 0u, vz = av != 0.0f ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    uint32_t mc = 0, vc = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      mc |= q8_round(div_by(m[c][e], iam) * 127.0f) << (8 * e);
+      vc |= q8_round(div_by(v[c][e], iav) * 127.0f) << (8 * e);
+    }
+    *(uint32_t *)(T.m_codes + R.s + 256 * c + 4 * lane) = mc & mz;
+    *(uint32_t *)(T.v_codes + R.s + 256 * c + 4 * lane) = vc & vz;
+  }
+  if (lane == 0) {
+    T.m_scales[R.b] = am;
+    T.v_scales[R.b] = av;
+  }
+}
+
 // NC 256-element chunks per block, one block per wave (measured against
 // two and four blocks per wave with every load issued up front: one is
 // fastest, as more waves hide the latency better than more loads per wave).
@@ -214,11 +348,15 @@ __global__ __launch_bounds__(256) void k_adam_wave(AdamBatch B, int64_t first_bl
   // the tensors' pointers live in scalar registers
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t gb = first_block + (int64_t)blockIdx.x * 4 + wave;
-  if (gb >= total_blocks) return;
+  __shared__ float tab[256];
+  tab[threadIdx.x] = (float)(int8_t)(uint8_t)threadIdx.x / 127.0f;
+  const bool live = gb < total_blocks;
   const Upd u{lr, beta1, beta2, eps, 1.0f - beta1, 1.0f - beta2, 1.0f, 1.0f};
   BlockRegs<NC> R;
-  load_block<NC>(R, B, gb, lane);
-  update_block<NC>(R, u, lane);
+  if (live) load_block<NC>(R, B, gb, lane);
+  __syncthreads();  // the table; every wave arrives, live or not
+  if (!live) return;
+  update_block<NC>(R, u, lane, tab);
 }
 
 __device__ float block_max(float v, float *red) {
