@@ -4,9 +4,13 @@ double reciprocal, rounded once to float.  That is the IEEE float quotient
 bit for bit: an exact quotient of two floats is never a float midpoint and
 lies at least 2^-49 (relative) away from every midpoint, while
 RN_d(x * RN_d(1/y)) is within 2^-52 of x/y, so rounding it to float lands on
-RN_f(x/y).  These tests check the claim (numpy's float32 division is IEEE);
-they plant a mistake in the claim's own terms (a float reciprocal instead of
-a double one) to show that they can fail."""
+RN_f(x/y) -- for quotients in the normal float range.  A subnormal quotient
+has fewer bits and can be a float midpoint, where the product may round the
+other way: the kernel sends those to a float division (m / b1t) or uses the
+quotient only where it rounds to code 0 (x / absmax * 127).  These tests
+check the claim (numpy's float32 division is IEEE), pin its boundary with a
+subnormal counterexample, and plant a mistake in the claim's own terms (a
+float reciprocal instead of a double one) to show that they can fail."""
 import numpy as np
 
 
@@ -73,3 +77,17 @@ def test_a_float_reciprocal_would_not_be_exact():
     y = np.abs(_random_floats(rng, 100_000, -10, 10))
     wrong = (x * (np.float32(1.0) / y)).astype(np.float32)
     assert not np.array_equal(wrong.view(np.uint32), _ieee(x, y).view(np.uint32))
+
+
+def test_subnormal_quotient_can_be_a_midpoint():
+    # 147 * 2^-149 / 98 = 1.5 * 2^-149, a midpoint: IEEE rounds to even (2),
+    # the double product falls just below it (1).  The claim stops at the
+    # normal range, and a subnormal quotient of m / b1t takes the kernel's
+    # float division.
+    x = np.array([147 * 2.0 ** -149], np.float32)
+    y = np.array([98.0], np.float32)
+    assert _ieee(x, y).view(np.uint32)[0] == 2
+    assert _via_double(x, y).view(np.uint32)[0] == 1
+    # and quantization: any subnormal quotient times 127 rounds to code 0
+    q = np.float32(np.nextafter(np.float32(2.0 ** -126), np.float32(0)))
+    assert abs(float(np.float32(q * np.float32(127.0)))) < 0.5

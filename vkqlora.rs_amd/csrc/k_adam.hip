@@ -21,10 +21,11 @@
 //    double products with the divisor's reciprocal rounded once to float
 //    (`div_by`: the IEEE float quotient bit for bit); code / 127 comes from
 //    a 256-entry LDS table of IEEE quotients; the square roots are the
-//    hardware root plus an exact rounding test (`sqrt_cr`), taken when no
-//    variance of the block is below 2^-96 (else the block runs the
-//    IEEE-library path, same bits); the one division by a per-element value
-//    stays a float division.  The only barrier is the table's, at entry.
+//    hardware root plus an exact rounding test (`sqrt_cr`).  A block with a
+//    variance below 2^-96 or a subnormal m / b1t runs the library path
+//    instead (IEEE float divisions and roots, same bits); the one division
+//    by a per-element value stays a float division.  The only barrier is
+//    the table's, at entry.
 //  * k_adam (any other block size or alignment): one workgroup per block,
 //    one element per thread, m and v staged in LDS.
 #include "qh_internal.h"
@@ -43,11 +44,14 @@ __device__ __forceinline__ float deq_i8(uint8_t c, float absmax) {
   return (float)(int8_t)c / 127.0f * absmax;
 }
 
-// Float quotients without a float division, bit for bit the IEEE ones: an
-// exact quotient of two floats is never a float midpoint and lies at least
-// 2^-49 (relative) from every midpoint, while RN_d(x * RN_d(1/y)) is within
-// 2^-52 of x/y, so its rounding to float is RN_f(x/y).  `inv` is the
-// divisor's double reciprocal (1 / (double)y, correctly rounded).
+// Float quotients without a float division, bit for bit the IEEE ones
+// whenever the quotient is in the normal range: there an exact quotient of
+// two floats is never a float midpoint and lies at least 2^-49 (relative)
+// from every midpoint, while RN_d(x * inv) is within 2^-51 of x/y, so its
+// rounding to float is RN_f(x/y).  `inv` is the divisor's double reciprocal
+// within 2^-51 (relative).  A subnormal quotient can be a midpoint (21
+// 2^-149 / 6), so div_by serves only where such a quotient cannot change
+// the result (a code that rounds to 0) or is sent to a float division.
 __device__ __forceinline__ float div_by(float x, double inv) {
   return (float)((double)x * inv);
 }
@@ -64,16 +68,6 @@ struct Upd {
     v = sqrtf(var);
     const float mh = m / b1t;
     const float vh = var / b2t;
-    return p - lr * mh / (sqrtf(vh) + eps);
-  }
-  // The same with m / b1t and var / b2t through div_by (same bits).
-  __device__ __forceinline__ float step_fast(float &m, float &v, float p, float g, double ib1,
-                                             double ib2) const {
-    m = beta1 * m + one_m_b1 * g;
-    const float var = beta2 * v * v + one_m_b2 * g * g;
-    v = sqrtf(var);
-    const float mh = div_by(m, ib1);
-    const float vh = div_by(var, ib2);
     return p - lr * mh / (sqrtf(vh) + eps);
   }
 };
@@ -210,7 +204,7 @@ __device__ __forceinline__ void update_block_lib(const BlockRegs<NC> &R, const U
       for (int e = 0; e < 4; ++e) {
         m[c][e] = deq_i8_fast((uint8_t)(R.mc[c] >> (8 * e)), R.ms);
         v[c][e] = deq_i8_fast((uint8_t)(R.vc[c] >> (8 * e)), R.vs);
-        pp[e] = u.step_fast(m[c][e], v[c][e], pp[e], gg[e], T.inv_b1t, T.inv_b2t);
+        pp[e] = u.step(m[c][e], v[c][e], pp[e], gg[e]);
         am = fmaxf(am, fabsf(m[c][e]));
         av = fmaxf(av, fabsf(v[c][e]));
       }
@@ -223,7 +217,7 @@ __device__ __forceinline__ void update_block_lib(const BlockRegs<NC> &R, const U
           const int64_t i = R.s + j0 + e;
           m[c][e] = deq_i8_fast(T.m_codes[i], R.ms);
           v[c][e] = deq_i8_fast(T.v_codes[i], R.vs);
-          T.p[i] = u.step_fast(m[c][e], v[c][e], T.p[i], T.g[i], T.inv_b1t, T.inv_b2t);
+          T.p[i] = u.step(m[c][e], v[c][e], T.p[i], T.g[i]);
           am = fmaxf(am, fabsf(m[c][e]));
           av = fmaxf(av, fabsf(v[c][e]));
         }
@@ -276,7 +270,7 @@ __device__ __forceinline__ void update_block(const BlockRegs<NC> &R, const Upd &
     return;
   }
   const AdamTensor &T = R.T;
-  float m[NC][4], var[NC][4], vh[NC][4];
+  float m[NC][4], var[NC][4], vh[NC][4], mh[NC][4];
   bool tiny = false;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -289,9 +283,12 @@ __device__ __forceinline__ void update_block(const BlockRegs<NC> &R, const Upd &
       m[c][e] = u0.beta1 * mo + u0.one_m_b1 * gg[e];
       var[c][e] = u0.beta2 * vo * vo + u0.one_m_b2 * gg[e] * gg[e];
       vh[c][e] = div_by(var[c][e], T.inv_b2t);
-      // below 2^-96 (zero included), not NaN
+      mh[c][e] = div_by(m[c][e], T.inv_b1t);
+      // a variance below 2^-96 (zero included, NaN not), or a subnormal
+      // m / b1t (where a quotient can be a float midpoint)
       tiny |= (!(var[c][e] >= 0x1p-96f) && var[c][e] == var[c][e]) ||
-              (!(vh[c][e] >= 0x1p-96f) && vh[c][e] == vh[c][e]);
+              (!(vh[c][e] >= 0x1p-96f) && vh[c][e] == vh[c][e]) ||
+              (fabsf(mh[c][e]) < 0x1p-126f && m[c][e] != 0.0f);
     }
   }
   if (__builtin_amdgcn_ballot_w64(tiny) != 0) {
@@ -306,8 +303,7 @@ __device__ __forceinline__ void update_block(const BlockRegs<NC> &R, const Upd &
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       v[c][e] = sqrt_cr(var[c][e]);
-      const float mh = div_by(m[c][e], T.inv_b1t);
-      pp[e] = pp[e] - u0.lr * mh / (sqrt_cr(vh[c][e]) + u0.eps);
+      pp[e] = pp[e] - u0.lr * mh[c][e] / (sqrt_cr(vh[c][e]) + u0.eps);
       am = fmaxf(am, fabsf(m[c][e]));
       av = fmaxf(av, fabsf(v[c][e]));
     }
