@@ -48,46 +48,85 @@ __device__ void dq_superblock(const float *sblk, int nhere, int64_t sb,
   if (tid == 0) absmax[sb] = amax;
 }
 
+__constant__ QhNf4Buckets c_buckets = qh_nf4_make_buckets();
+
+
+// 1 / (double)a for a finite a > 0 within 2^-51 (relative): the hardware
+// reciprocal (within 2^-23) and two Newton steps, each squaring the error.
+__device__ __forceinline__ double inv_f64(float a) {
+  const double d = (double)a;
+  double y = __builtin_amdgcn_rcp(d);
+  y = __builtin_fma(__builtin_fma(-d, y, 1.0), y, y);
+  y = __builtin_fma(__builtin_fma(-d, y, 1.0), y, y);
+  return y;
+}
+
 // block_size == 64.  One workgroup per super-block of 256 blocks (16384
 // elements); 8 lanes per block, 8 contiguous elements per lane, 32 blocks
-// per pass, 8 passes.
+// per pass, 8 passes, every pass's loads issued before the first is used
+// (measured: 213 us at 28672 x 8192 against 262 us for persistent
+// workgroups that reload each pass's registers with the next super-block).
+// The target t = fl(w / absmax) is the double product of w with the block's
+// reciprocal rounded to float: the IEEE quotient bit for bit when t is a
+// normal float (an exact quotient of two floats lies at least 2^-49
+// relative from every float midpoint; the product is within 2^-51), and
+// any subnormal t is nearest to level 0 (code 7) whatever its last bits.
+// |t| <= 1 (the absmax bounds |w|), so the bucketed search applies: one LDS
+// byte (the bucket's c0) and one 16-byte LDS read (L[c0 .. c0 + 2]).
 __global__ __launch_bounds__(256) void k_quantize64(
     const float *__restrict__ w, int64_t n, int dq, uint8_t *__restrict__ codes,
     int64_t codes_len, float *__restrict__ scales,
     uint8_t *__restrict__ scale_codes, float *__restrict__ absmax, int64_t nb) {
-  __shared__ float lut[17];
+  __shared__ __align__(16) uint8_t bkt[QH_NF4_BUCKETS];
+  __shared__ __align__(16) float lq[16][4];  // L[c], L[c+1], L[c+2], unused
   __shared__ float sblk[256];
   __shared__ float red[4];
   const int tid = threadIdx.x;
-  if (tid < 17) lut[tid] = c_lut17[tid];
-  __syncthreads();
   const int64_t sb = blockIdx.x;
   const int l8 = tid & 7, grp = tid >> 3;
-#pragma unroll 1
+  // every pass's data first: 16 float4 per lane in flight
+  float4 va[8], vb[8];
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass) {
+    const int64_t e0 = (sb * 256 + pass * 32 + grp) * 64 + l8 * 8;
+    if (e0 + 8 <= n) {
+      const float4 *p = reinterpret_cast<const float4 *>(w + e0);
+      va[pass] = p[0];
+      vb[pass] = p[1];
+    } else {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (e0 + i < n) ? w[e0 + i] : 0.0f;
+      va[pass] = make_float4(v[0], v[1], v[2], v[3]);
+      vb[pass] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  }
+  reinterpret_cast<uint4 *>(bkt)[tid] = reinterpret_cast<const uint4 *>(c_buckets.c0)[tid];
+  if (tid < 16)
+    *reinterpret_cast<float4 *>(lq[tid]) =
+        make_float4(qh_nf4_levels[tid], qh_nf4_levels[tid + 1], qh_nf4_levels[tid + 2], 0.0f);
+  __syncthreads();
+#pragma unroll
   for (int pass = 0; pass < 8; ++pass) {
     const int64_t blk = sb * 256 + pass * 32 + grp;
     const int64_t e0 = blk * 64 + l8 * 8;
-    float v[8];
-    if (e0 + 8 <= n) {
-      const float4 *p = reinterpret_cast<const float4 *>(w + e0);
-      float4 a = p[0];
-      float4 b = p[1];
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (e0 + i < n) ? w[e0 + i] : 0.0f;
-    }
+    const float v[8] = {va[pass].x, va[pass].y, va[pass].z, va[pass].w,
+                        vb[pass].x, vb[pass].y, vb[pass].z, vb[pass].w};
     // Padding with 0 leaves the fold max(0, |w|...) unchanged.
     float am = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
     am = wave_max8(am);
+    // w / inf is 0 (NaN for inf / inf): a zero reciprocal gives both
+    const double inv = __builtin_isinf(am) ? 0.0 : inv_f64(am != 0.0f ? am : 1.0f);
     uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      uint32_t code = QH_NF4_ZERO_CODE;
-      if (am != 0.0f) code = qh_nf4_code_of_target(v[i] / am, lut);
+      const float t = (float)((double)v[i] * inv);
+      const uint32_t c0 = bkt[qh_nf4_bucket(t)];
+      const float4 L = *reinterpret_cast<const float4 *>(lq[c0]);
+      uint32_t code = qh_nf4_code_bucketed(t, c0, L.x, L.y, L.z);
+      if (am == 0.0f) code = QH_NF4_ZERO_CODE;
       if (e0 + i >= n) code = 0;
       word |= code << (4 * i);
     }

@@ -61,6 +61,59 @@ QH_HD inline uint32_t qh_nf4_code_of_target(float t, const float *L) {
   return (d1 < d0) ? c + 1u : c;
 }
 
+// ---- bucketed search: one table read and one comparison per target ------
+// A target's bucket is its float bits >> 20: sign, exponent and the top
+// three mantissa bits (4096 buckets).  Inside [-1, 1] a bucket spans at most
+// an eighth of an octave (<= 1/16 wide), less than the gap between any two
+// adjacent levels (>= 0.0795), so c(t) = max{j : L_j <= t} takes at most two
+// values on it: c0 = c(the bucket's lowest target) and c0 + 1.  Buckets of
+// exponent 255 (inf, NaN) get c0 = 0.  The host test checks the bucketed
+// search against the scan for every float in [-1, 1].
+#define QH_NF4_BUCKETS 4096
+
+constexpr float qh_nf4_levels[18] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
+    0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+    0.7229568362236023f, 1.0f, __builtin_inff(), __builtin_inff()};
+
+constexpr uint32_t qh_nf4_floor_code(float t) {
+  uint32_t c = 0;
+  for (uint32_t j = 1; j < 16; ++j)
+    if (qh_nf4_levels[j] <= t) c = j;
+  return c;
+}
+
+struct QhNf4Buckets {
+  uint8_t c0[QH_NF4_BUCKETS];
+};
+
+constexpr QhNf4Buckets qh_nf4_make_buckets() {
+  QhNf4Buckets b{};
+  for (uint32_t i = 0; i < QH_NF4_BUCKETS; ++i) {
+    // the lowest target: the bucket's smallest magnitude when positive, its
+    // largest when negative
+    const uint32_t bits = (i >> 11) ? ((i << 20) | 0xFFFFFu) : (i << 20);
+    const bool special = ((i >> 3) & 0xFFu) == 0xFFu;
+    b.c0[i] = special ? 0 : (uint8_t)qh_nf4_floor_code(__builtin_bit_cast(float, bits));
+  }
+  return b;
+}
+
+QH_HD inline uint32_t qh_nf4_bucket(float t) { return __builtin_bit_cast(uint32_t, t) >> 20; }
+
+// The nearest code of a target |t| <= 1 (or NaN) from its bucket's c0 and the
+// levels L[c0], L[c0 + 1], L[c0 + 2] (+inf past L[15]): c = c0 + (t >= L[c0+1]),
+// then c or c + 1 by the rule of qh_nf4_code_of_target (ties keep c).  NaN
+// fails every comparison: c0 = 0 and code 0.
+QH_HD inline uint32_t qh_nf4_code_bucketed(float t, uint32_t c0, float l0, float l1, float l2) {
+  const bool up = t >= l1;
+  const float lo = up ? l1 : l0, hi = up ? l2 : l1;
+  const float d0 = __builtin_fabsf(lo - t), d1 = __builtin_fabsf(hi - t);
+  return c0 + (up ? 1u : 0u) + (d1 < d0 ? 1u : 0u);
+}
+
 // Rust `(x).round() as i32` followed by `.clamp(-127, 127)`: round half
 // away from zero, saturating cast with NaN -> 0 (quant.rs:293,
 // optim.rs:91).
