@@ -85,7 +85,8 @@ constexpr uint32_t qh_nf4_floor_code(float t) {
   return c;
 }
 
-struct QhNf4Buckets {
+// 16-byte aligned: the kernels copy it to LDS with 16-byte loads
+struct alignas(16) QhNf4Buckets {
   uint8_t c0[QH_NF4_BUCKETS];
 };
 
