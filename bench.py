@@ -505,6 +505,39 @@ def _timed_ms(torch, fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
+def _graph_ms(torch, fn, outs, reps):
+    """fn() captured once as a HIP graph and replayed: mean time per replay
+    between GPU events (the kernels' own time, host launch cost excluded).
+    The replays must reproduce the eager result of fn() bit for bit (every
+    tensor of outs()), checked before timing."""
+    fn()
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in outs()]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        fn()
+    for _ in range(3):
+        gr.replay()
+        torch.cuda.synchronize()
+        for t, r in zip(outs(), ref):
+            assert torch.equal(t, r), "graph replay differs from the eager run"
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del gr
+    return e0.elapsed_time(e1) / reps
+
+
 def _layer(torch, dev, QD, ctx, g, N, K, M, r, alpha, act=None):
     act = act or torch.float32
     w = torch.randn(N, K, device=dev, generator=g) * 0.02
@@ -597,9 +630,14 @@ def extra_bench(args, ctx, torch, dev, QD):
     L = _layer(torch, dev, QD, ctx, g, 576, 576, 64, 8, 16.0)
     ms = _timed_ms(torch, lambda: _fwd_bwd(QD, ctx, L), 20)
     f = _fwd_bwd_flops(L)
+    gms = _graph_ms(torch, lambda: _fwd_bwd(QD, ctx, L),
+                    lambda: [L["y"], L["gx"], L["ga"], L["gb"]], 50)
     out["C1"] = dict(workload="fwd+bwd 576x576 NF4, 64 tokens, r=8", ms=ms, flops=f,
                      tflops=f / (ms * 1e9), frac_fp32_peak=f / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS,
-                     bound="launch")
+                     bound="launch", graph_ms=gms, graph_tflops=f / (gms * 1e9),
+                     timing=("ms: eager calls between GPU events (host launch cost "
+                             "included); graph_ms: the same calls replayed as one HIP "
+                             "graph, checked bit-equal to the eager result"))
     if not args.no_cpu_baseline:
         out["C1"]["cpu_baseline"] = cpu_baseline_c1()
     del L
@@ -641,6 +679,8 @@ def extra_bench(args, ctx, torch, dev, QD):
     ms = _timed_ms(torch, c4_fb, 5)
     ms_pl = _timed_ms(torch, c4_per_layer, 5)
     f = sum(_fwd_bwd_flops(L) for L in Ls)
+    gms = _graph_ms(torch, c4_fb, lambda: [t for L in Ls for t in (L["y"], L["gx"], L["ga"],
+                                                                    L["gb"])], 20)
     tens = []
     for L in Ls:
         tens += [(L["a"].clone(), L["ga"]), (L["b"].clone(), L["gb"])]
@@ -651,7 +691,12 @@ def extra_bench(args, ctx, torch, dev, QD):
                                "adapter tensors"),
                      fwd_bwd_ms=ms, per_layer_ms=ms_pl, flops=f, tflops=f / (ms * 1e9),
                      frac_fp32_peak=f / (ms * 1e9) / FP32_MFMA_PEAK_TFLOPS, adam=ad,
-                     step_ms=ms + ad["ms"])
+                     step_ms=ms + ad["ms"], graph_fwd_bwd_ms=gms,
+                     graph_tflops=f / (gms * 1e9),
+                     graph_frac_fp32_peak=f / (gms * 1e9) / FP32_MFMA_PEAK_TFLOPS,
+                     timing=("fwd_bwd_ms: eager calls between GPU events (host launch "
+                             "cost included); graph_fwd_bwd_ms: the same calls replayed "
+                             "as one HIP graph, checked bit-equal to the eager result"))
     del Ls, tens
     torch.cuda.empty_cache()
     # C5: 70B-class layers: quantize throughput (bit-exact path), fwd+bwd
