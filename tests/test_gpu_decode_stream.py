@@ -77,12 +77,9 @@ def test_stream_parity(ctx, QD, N, K):
             y, t1, rep = _forward(QD, ctx, W, lora, torch.from_numpy(xa).to(dev).to(act), M, N, r)
             # batch 2 computes T1 in the launch where its slices fit a
             # producer lane's registers, else in a launch just before (at
-            # 14336 rows that needs 4 tiles per workgroup of the 4-row
-            # template, not compiled: the two-kernel path runs)
-            if M == 1 or N != 14336:
-                assert "decode_stream" in rep, rep
-            else:
-                assert "decode_small" in rep, rep
+            # 14336 rows the 4-row template's 4 tiles per workgroup are not
+            # compiled: it streams in two rounds of 2-tile workgroups)
+            assert "decode_stream" in rep, rep
             tol = TOL_F32 if act == torch.float32 else TOL_BF16
             yo = O.qlora_forward(wd, N, K, a, b, r, alpha, xa, M)
             e = nerr(y.cpu().numpy().ravel(), yo, K, xa, wd)
@@ -443,3 +440,32 @@ def test_group_batches_share_one_t1_launch(ctx, QD, batch, act):
             assert torch.equal(y, yr), (with_t1, L["N"], L["K"])
             if with_t1 and L["r"]:
                 assert torch.equal(t1, t1r)
+
+
+@pytest.mark.parametrize("M", [4, 11])
+def test_stream_multi_round_70b_layer(ctx, QD, M):
+    """A 70B-class layer (28672 x 8192: 1792 row tiles, more lines than one
+    round of one workgroup per CU can hold) at batches of 3-16 streams in
+    several rounds of one-tile workgroups (T1 from its own launch first): y
+    and T1 against the oracle."""
+    N, K, r, alpha = 28672, 8192, 16, 32.0
+    _say(f"stream multi-round N={N} K={K} M={M}")
+    gen = torch.Generator(device="cuda").manual_seed(70 + M)
+    dev = torch.device("cuda:0")
+    w = torch.randn(N, K, device=dev, generator=gen) * 0.02
+    a = (torch.rand(r, K, device=dev, generator=gen) * 2 - 1) / np.sqrt(K)
+    b = torch.randn(N, r, device=dev, generator=gen) * 0.01
+    x = torch.randn(M, K, device=dev, generator=gen)
+    W = QD.DeviceWeight.quantize(w, ctx=ctx)
+    wd = W.dequantize(ctx=ctx).cpu().numpy()
+    del w
+    lora = QD.lora_struct(a, b, r, alpha)
+    y, t1, rep = _forward(QD, ctx, W, lora, x, M, N, r)
+    assert "decode_stream" in rep, rep
+    an, bn, xn = a.cpu().numpy().ravel(), b.cpu().numpy().ravel(), x.cpu().numpy().ravel()
+    yo = O.qlora_forward(wd.ravel(), N, K, an, bn, r, alpha, xn, M)
+    t1o = O.matmul_trans_b(xn, an, M, K, r)
+    e = nerr(y.cpu().numpy().ravel(), yo, K, xn, wd)
+    et = nerr(t1.cpu().numpy().ravel(), t1o, K, xn, an)
+    _say(f"  y {e:.2e} t1 {et:.2e}")
+    assert e < TOL_F32 and et < TOL_F32, (e, et)

@@ -996,22 +996,36 @@ StreamPlan stream_plan(const DevQW &w, int Mt, int mact, int64_t r, int LW = kLW
     return p;
   const int64_t T = (w.rows + 15) / 16, KL = w.cols / kLine;
   if (KL < kLW) return p;
-  const int64_t R = (T + cus - 1) / cus;
   const int64_t KLW = (KL + kLW - 1) / kLW;
-  if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW, Mt)) return p;
-  if (LW != kLW && (LW != kLW / 2 || Mt > 2 || R * KLW * (kLW / LW) > kMaxLinesHalf)) return p;
-  const int64_t G = (T + R - 1) / R;
   const int64_t M = Mt;
   int64_t MRp = 1;
   while (MRp < M * r) MRp *= 2;
-  const int64_t P = t1in ? t1_slices((int)G, (int)MRp) : 0;
-  if (t1in && r > 0) {
-    // T1 slices: every producer lane covers at most kT1Units float4 units.
+  // T1 slices: every producer lane covers at most t1_units(R) float4 units
+  auto t1_fits = [&](int64_t R, int64_t G) {
+    if (!t1in || r == 0) return true;
+    const int64_t P = t1_slices((int)G, (int)MRp);
     const int64_t lpj = (int64_t)1 << (63 - __builtin_clzll(64 / r));
     const int64_t units = (w.cols / 4 + P - 1) / P;
-    if (w.cols / 4 < P || (units + lpj - 1) / lpj > t1_units((int)R)) return p;
-    if (MRp > 64 || P * MRp > (int64_t)kT1Loads * kThreads) return p;
+    return w.cols / 4 >= P && (units + lpj - 1) / lpj <= t1_units((int)R) && MRp <= 64 &&
+           P * MRp <= (int64_t)kT1Loads * kThreads;
+  };
+  // One round of one workgroup per CU (R tiles each) when its lines fit;
+  // a layer too large for that (70B-class rows) runs in several rounds of
+  // workgroups with fewer tiles, the most that fit: 8-wave launches whose
+  // T1 comes from an earlier launch only (the in-launch T1's launch epochs
+  // need every workgroup of a launch resident at once, G <= 16 x 16).
+  int64_t R = (T + cus - 1) / cus;
+  if (R * KLW > kMaxLines || !shape_compiled((int)R, (int)KLW, Mt) ||
+      !t1_fits(R, (T + R - 1) / R)) {
+    if (LW != kLW || t1in) return p;
+    R = std::min<int64_t>(R, kMaxLines / KLW);
+    while (R >= 1 && (!shape_compiled((int)R, (int)KLW, Mt) || !t1_fits(R, (T + R - 1) / R)))
+      --R;
+    if (R < 1) return p;
   }
+  if (LW != kLW && (LW != kLW / 2 || Mt > 2 || R * KLW * (kLW / LW) > kMaxLinesHalf)) return p;
+  const int64_t G = (T + R - 1) / R;
+  const int64_t P = t1in ? t1_slices((int)G, (int)MRp) : 0;
   // per-wave T1 partials (kLW MRp floats); the recomputed slices (P MRp
   // floats) reuse the X fragments' space
   const size_t frag_line = (size_t)16 * 2 * M * 4 * (M == 1 ? 16 : 8);
