@@ -103,13 +103,13 @@ def test_stream_f32_scales_no_adapter(ctx, QD):
     assert nerr(y.cpu().numpy().ravel(), yo, K, x, wd) < TOL_F32
 
 
-@pytest.mark.parametrize("M,r,stream", [(1, 64, False), (2, 32, True), (2, 64, True),
+@pytest.mark.parametrize("M,r,stream", [(1, 64, True), (2, 32, True), (2, 64, True),
                                         (1, 1, True), (1, 5, True), (1, 16, True), (2, 8, True)])
 def test_stream_ranks(ctx, QD, M, r, stream):
     # small adapters run in one launch; where the T1 slices would not fit
     # the producer's registers (batch * r of 64 and more at this shape)
-    # batch 2 takes T1 from a launch before its weight stream and batch 1
-    # the two-kernel path, with the same result
+    # batches 1 and 2 take T1 from a launch before their weight stream (the
+    # 4-row template), with the same result
     N, K, alpha = 4096, 4096, 16.0
     g = O.Rng(SEED ^ (100 + 7 * r + M))
     w = g.normal(N * K, 0.02)

@@ -1212,10 +1212,9 @@ bool decode_stream_t1_in(const DevQW &w, int64_t M, int64_t r) {
 bool decode_stream_ok(const DevQW &w, int64_t M, int64_t r) {
   if (M < 1 || M > kStreamMaxRows) return false;
   if (decode_stream_t1_in(w, M, r)) return true;
-  // batch 1 only with T1 in the launch; batch 2 and wider batches take T1
-  // from launch_decode_stream_t1, and every chunk of 8 rows (the last one
-  // possibly narrower) must fit
-  if (M == 1) return false;
+  // otherwise T1 comes from launch_decode_stream_t1 and every chunk of 8
+  // rows (the last one possibly narrower; batch 1 on the 4-row template,
+  // e.g. a 70B-class layer that needs several rounds) must fit
   for (int64_t m0 = 0; m0 < M; m0 += 8) {
     const int mact = (int)std::min<int64_t>(8, M - m0);
     if (!stream_plan(w, stream_rows(mact), mact, r).ok) return false;
