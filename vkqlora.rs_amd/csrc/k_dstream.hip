@@ -963,7 +963,7 @@ int cu_count() {
 #define QH_STREAM_SHAPES(F) \
   F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(1, 8) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2) F(4, 1) F(4, 2)
 #define QH_STREAM_SHAPES_WIDE(F) \
-  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(2, 1) F(2, 2) F(3, 1) F(3, 2)
+  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2)
 
 bool shape_compiled(int R, int KLW, int Mt) {
 #define QH_SHAPE_EQ(rr, kk) if (R == rr && KLW == kk) return true;
