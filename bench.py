@@ -723,7 +723,55 @@ def extra_bench(args, ctx, torch, dev, QD):
         torch.cuda.empty_cache()
     c5.update(quantize=qs, fwd_bwd=fbs, adam=_adam_step_ms(torch, ctx, tens))
     out["C5"] = c5
+    del tens
+    torch.cuda.empty_cache()
+    out["decode_70b"] = decode_large_bench(torch, dev, QD, ctx, g)
     return out
+
+
+def decode_large_bench(torch, dev, QD, ctx, g):
+    """Decode (forward only) of C5's 28672x8192 layer, r=16, at batches 1, 4
+    and 16: not a BASELINE configuration, the 70B-class case of the decode
+    GEMV (several rounds of workgroups; T1 from its own launch).  Three
+    weight copies (363 MB) rotate past the MALL; the time per call is the
+    sum of the call's kernels' GPU-stamped durations (host gaps excluded)."""
+    N, K, r = 28672, 8192, 16
+    copies = []
+    for _ in range(3):
+        w = torch.randn(N, K, device=dev, generator=g) * 0.02
+        W = QD.DeviceWeight.quantize(w, 64, True, ctx=ctx)
+        del w
+        a = (torch.rand(r, K, device=dev, generator=g) * 2 - 1) / math.sqrt(K)
+        b = torch.randn(N, r, device=dev, generator=g) * 0.01
+        copies.append((W, QD.lora_struct(a, b, r, 2.0 * r), a, b))
+    torch.cuda.empty_cache()
+    wbytes = N * K // 2 + N * K // 64 + N * K // 16384 * 4
+    res = {}
+    for M in (1, 4, 16):
+        x = torch.randn(M, K, device=dev, generator=g)
+        y = torch.empty(M, N, device=dev)
+        for W, lora, _, _ in copies:
+            QD.forward(W, lora, x, M, y, ctx=ctx)
+        torch.cuda.synchronize()
+        reps = 12
+        ctx.set_timing(True)
+        ctx.timing_report(reset=True)
+        for i in range(reps):
+            W, lora, _, _ = copies[i % len(copies)]
+            QD.forward(W, lora, x, M, y, ctx=ctx)
+        torch.cuda.synchronize()
+        rep = ctx.timing_report(reset=True)
+        ctx.set_timing(False)
+        ms = sum(t for _, t in rep.values()) / reps
+        algo = wbytes + (r * K + N * r + M * K + M * N) * 4
+        res[str(M)] = dict(ms=ms, weight_gbs=wbytes / (ms * 1e6), total_gbs=algo / (ms * 1e6),
+                           frac_hbm=algo / (ms * 1e6) / HBM_PEAK_GBS,
+                           kernels={k: dict(launches=n, avg_ms=t / n) for k, (n, t) in rep.items()})
+    print("# decode 70b-class 28672x8192: " + ", ".join(
+        f"batch {m} {v['ms'] * 1e3:.1f} us ({v['total_gbs']:.0f} GB/s)" for m, v in res.items()),
+        file=sys.stderr, flush=True)
+    return dict(workload=("decode forward of the 28672x8192 NF4 layer (block 64, double quant), "
+                          "r=16, fp32 X, batches 1/4/16; 3 weight copies rotated"), batches=res)
 
 
 def glue_bench(args, ctx, torch, dev, QD):
