@@ -442,13 +442,14 @@ def test_group_batches_share_one_t1_launch(ctx, QD, batch, act):
                 assert torch.equal(t1, t1r)
 
 
-@pytest.mark.parametrize("M", [4, 11])
-def test_stream_multi_round_70b_layer(ctx, QD, M):
-    """A 70B-class layer (28672 x 8192: 1792 row tiles, more lines than one
-    round of one workgroup per CU can hold) at batches of 3-16 streams in
-    several rounds of one-tile workgroups (T1 from its own launch first): y
-    and T1 against the oracle."""
-    N, K, r, alpha = 28672, 8192, 16, 32.0
+@pytest.mark.parametrize("N,K,M", [(28672, 8192, 1), (28672, 8192, 4), (28672, 8192, 11),
+                                   (8192, 28672, 1), (8192, 28672, 16)])
+def test_stream_multi_round_70b_layer(ctx, QD, N, K, M):
+    """70B-class layers: 28672 x 8192 (1792 row tiles, more than one round
+    of one workgroup per CU can hold) streams in several rounds of 2-tile
+    workgroups, 8192 x 28672 (14 K-lines per wave) in two rounds of one-tile
+    ones, T1 from its own launch first: y and T1 against the oracle."""
+    r, alpha = 16, 32.0
     _say(f"stream multi-round N={N} K={K} M={M}")
     gen = torch.Generator(device="cuda").manual_seed(70 + M)
     dev = torch.device("cuda:0")

@@ -57,7 +57,7 @@ constexpr int kLW = 8;                    // line waves per workgroup
 constexpr int kThreads = kLW * 64;
 constexpr int kCopies = 32;               // codebook table copies
 constexpr uint32_t kTabBytes = 256u * kCopies * 8u;  // 64 KiB at LDS offset 0
-constexpr int kMaxLines = 8;   // code lines a wave holds in registers
+constexpr int kMaxLines = 14;  // code lines of a wave's K slice (in registers DL at a time)
 constexpr int kMaxLinesHalf = 12;  // the same for the 4-wave workgroups of a layer pair
 constexpr int kT1Loads = 4;   // tagged T1 partials read per thread (P * M * r <= 2048)
 constexpr int kLinesAhead = 3; // K-lines of loads a wave keeps in flight
@@ -961,9 +961,10 @@ int cu_count() {
 
 // (R, KLW) pairs that are compiled, for batches of 1-2 and of 4-8 rows.
 #define QH_STREAM_SHAPES(F) \
-  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(1, 8) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2) F(4, 1) F(4, 2)
+  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(1, 8) F(1, 14) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2) \
+  F(4, 1) F(4, 2)
 #define QH_STREAM_SHAPES_WIDE(F) \
-  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2)
+  F(1, 1) F(1, 2) F(1, 3) F(1, 4) F(1, 6) F(1, 14) F(2, 1) F(2, 2) F(2, 4) F(3, 1) F(3, 2)
 
 bool shape_compiled(int R, int KLW, int Mt) {
 #define QH_SHAPE_EQ(rr, kk) if (R == rr && KLW == kk) return true;
