@@ -730,12 +730,21 @@ def extra_bench(args, ctx, torch, dev, QD):
 
 
 def decode_large_bench(torch, dev, QD, ctx, g):
-    """Decode (forward only) of C5's 28672x8192 layer, r=16, at batches 1, 4
-    and 16: not a BASELINE configuration, the 70B-class case of the decode
-    GEMV (several rounds of workgroups; T1 from its own launch).  Three
-    weight copies (363 MB) rotate past the MALL; the time per call is the
-    sum of the call's kernels' GPU-stamped durations (host gaps excluded)."""
-    N, K, r = 28672, 8192, 16
+    """Decode (forward only) of C5's layers (28672x8192 and 8192x28672),
+    r=16, at batches 1, 4 and 16: not a BASELINE configuration, the
+    70B-class case of the decode GEMV (several rounds of workgroups; T1 from
+    its own launch).  Three weight copies (363 MB) rotate past the MALL; the
+    time per call is the sum of the call's kernels' GPU-stamped durations
+    (host gaps excluded)."""
+    out = {}
+    for N, K in ((28672, 8192), (8192, 28672)):
+        out[f"{N}x{K}"] = _decode_large(torch, dev, QD, ctx, g, N, K)
+    return dict(workload=("decode forward of C5's NF4 layers (block 64, double quant), r=16, "
+                          "fp32 X, batches 1/4/16; 3 weight copies rotated"), layers=out)
+
+
+def _decode_large(torch, dev, QD, ctx, g, N, K):
+    r = 16
     copies = []
     for _ in range(3):
         w = torch.randn(N, K, device=dev, generator=g) * 0.02
@@ -767,11 +776,12 @@ def decode_large_bench(torch, dev, QD, ctx, g):
         res[str(M)] = dict(ms=ms, weight_gbs=wbytes / (ms * 1e6), total_gbs=algo / (ms * 1e6),
                            frac_hbm=algo / (ms * 1e6) / HBM_PEAK_GBS,
                            kernels={k: dict(launches=n, avg_ms=t / n) for k, (n, t) in rep.items()})
-    print("# decode 70b-class 28672x8192: " + ", ".join(
+    print(f"# decode 70b-class {N}x{K}: " + ", ".join(
         f"batch {m} {v['ms'] * 1e3:.1f} us ({v['total_gbs']:.0f} GB/s)" for m, v in res.items()),
         file=sys.stderr, flush=True)
-    return dict(workload=("decode forward of the 28672x8192 NF4 layer (block 64, double quant), "
-                          "r=16, fp32 X, batches 1/4/16; 3 weight copies rotated"), batches=res)
+    del copies
+    torch.cuda.empty_cache()
+    return res
 
 
 def glue_bench(args, ctx, torch, dev, QD):
