@@ -5,8 +5,10 @@
 //   y[m][n] = sum_b s_{n,b} sum_{k in b} x[m][k] L[c_{n,k}]
 //           + (alpha/r) sum_j T1[m][j] B[n][j],      T1 = X A^T.
 //
-// Grid: at most one workgroup per CU (each needs more than half of a CU's
-// LDS), 8 waves per workgroup.  Two independent layers go in one launch as
+// Grid: at most one workgroup per CU at a time (each needs more than half
+// of a CU's LDS), 8 waves per workgroup; one round when the layer's tiles
+// fit, several rounds of fewer-tile workgroups for 70B-class layers whose
+// T1 comes from an earlier launch.  Two independent layers go in one launch as
 // 4-wave workgroups of at most half a CU's LDS, one of each layer per CU
 // (k_dstream2, below).
 //  * Workgroup c owns R consecutive 16-row tiles and the whole of K.  Line
